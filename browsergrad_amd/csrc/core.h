@@ -1,0 +1,145 @@
+// Internal declarations shared by the libbghip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/bghip.h"
+
+namespace bg {
+
+// Thrown inside the library, converted to a status + message at the C ABI.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] void fail(int code, const std::string& msg);
+void hip_check(hipError_t e, const char* what);
+
+int64_t dtype_size(int dtype);
+const char* dtype_name(int dtype);
+
+// A device allocation.  Several handles may share one (reshape views).
+struct Alloc {
+  void* ptr = nullptr;
+  size_t bytes = 0;   // requested bytes
+  size_t cap = 0;     // bytes of the pooled block
+  int refs = 0;
+};
+
+struct Record {
+  Alloc* alloc = nullptr;
+  int64_t offset = 0;  // byte offset of this view inside alloc
+  int64_t nbytes = 0;
+  std::vector<int64_t> shape;
+  int dtype = BG_F32;
+  char* ptr() const { return static_cast<char*>(alloc->ptr) + offset; }
+  int64_t numel() const {
+    int64_t n = 1;
+    for (int64_t d : shape) n *= d;
+    return n;
+  }
+};
+
+struct PendingProfile {
+  hipEvent_t start;
+  hipEvent_t stop;
+  bg_pass_profile info;
+};
+
+}  // namespace bg
+
+struct bg_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool profiling = false;
+  std::string err;
+  uint64_t next_id = 1;
+  std::unordered_map<uint64_t, bg::Record> handles;
+
+  // Accounting, per allocation (realizer.ts:908-943 counts per buffer).
+  int64_t current_owned = 0;
+  int64_t peak_owned = 0;
+  int64_t total_allocated = 0;
+  int64_t total_released = 0;
+
+  // Block cache: pooled-size -> free device blocks.
+  std::multimap<size_t, void*> free_blocks;
+  int64_t cached_bytes = 0;
+  int64_t pool_hits = 0;
+  int64_t pool_misses = 0;
+
+  // Profiling.
+  std::vector<bg::PendingProfile> pending;
+  std::vector<bg_pass_profile> done;
+  std::vector<hipEvent_t> event_pool;
+
+  // Scratch buffers reused across launches (workspace for pre-passes).
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+};
+
+namespace bg {
+
+// Handle table / allocation helpers (core.cpp).
+Record& get(bg_ctx* ctx, bg_handle h, const char* op);
+bg_handle mint(bg_ctx* ctx, size_t nbytes, const std::vector<int64_t>& shape,
+               int dtype);
+bg_handle mint_view(bg_ctx* ctx, const Record& src, int64_t offset,
+                    int64_t nbytes, const std::vector<int64_t>& shape,
+                    int dtype);
+void* scratch(bg_ctx* ctx, size_t bytes);
+std::vector<int64_t> to_shape(const int64_t* shape, int rank);
+int64_t numel(const std::vector<int64_t>& shape);
+
+// RAII profiling scope around one dispatch (hipEvent pair on ctx->stream).
+struct Profile {
+  bg_ctx* ctx;
+  bool on;
+  PendingProfile p;
+  Profile(bg_ctx* c, const char* label, int64_t bytes, int64_t flops);
+  ~Profile();
+};
+
+// Kernel launchers (one per translation unit).
+void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out);
+void launch_cast(bg_ctx* ctx, const void* src, int src_dtype, void* dst,
+                 int dst_dtype, int64_t n);
+void launch_cast_transpose(bg_ctx* ctx, const void* src, int src_dtype,
+                           void* dst, int dst_dtype, int64_t rows,
+                           int64_t cols, int64_t batch);
+void launch_copy_strided(bg_ctx* ctx, const void* src, int64_t elem_size,
+                         void* dst, const std::vector<int64_t>& shape,
+                         const std::vector<int64_t>& strides);
+void launch_layer_norm(bg_ctx* ctx, const void* x, int x_dtype,
+                       const float* w, const float* b, void* y, int y_dtype,
+                       int64_t rows, int64_t cols, float eps);
+void launch_reduce_last(bg_ctx* ctx, const void* x, int dtype, void* y,
+                        int64_t rows, int64_t cols, int op);
+void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a,
+                   const Record& b, const Record* bias, Record& out);
+void launch_attention(bg_ctx* ctx, const bg_attention_desc& d,
+                      const Record& q, const Record& k, const Record& v,
+                      Record& out);
+void launch_attention_generic(bg_ctx* ctx, const bg_attention_desc& d, const void* q,
+                              const void* k, const void* v, const float* mask, int64_t mask_sb,
+                              int64_t mask_sh, void* o, bool two_pass);
+void launch_attention_masked_f32(bg_ctx* ctx, const float* q, const float* k,
+                                 const float* v, const float* mask,
+                                 int64_t mask_b, int64_t mask_h, float* o,
+                                 int64_t b, int64_t h, int64_t sq, int64_t sk,
+                                 int64_t d, float scale);
+
+// Plan executor (plan.cpp).
+bg_handle run_plan(bg_ctx* ctx, const char* json, const int64_t* ids,
+                   const bg_handle* handles, int n, int dtype);
+
+}  // namespace bg

@@ -1,0 +1,459 @@
+// Data-movement and normalisation kernels for gfx950:
+//   * cast between f32 / f16 / bf16 with round-to-nearest-even narrowing
+//     (the reference bridge only copies f32->f32, realizer.ts:1087-1120; the
+//     oracle is NumPy astype, _realize.py:210-212);
+//   * cast + batched 2-D transpose through LDS (GEMM operand re-layout);
+//   * strided gather copy (PERMUTE / SLICE / BROADCAST materialisation,
+//     tensor_plan.ts:824-997);
+//   * LayerNorm, one wavefront per row with the row held in registers
+//     (tensor_plan.ts:2170-2208; oracle _realize.py:1008-1034);
+//   * a generic attention kernel (one wavefront per query row) used for f32,
+//     for additive masks (flash_attention.ts:45-131) and for head sizes the
+//     MFMA kernel does not cover.
+#include <algorithm>
+#include <cmath>
+
+#include "common.cuh"
+#include "core.h"
+
+namespace {
+
+using namespace bgk;
+
+// ---- cast -------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256) cast_kernel(const void* __restrict__ src, int sd,
+                                                   void* __restrict__ dst, int dd, int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  for (; i + 3 < n; i += stride * 4) {
+    float v[4];
+    if (sd == 0) {
+      float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + i);
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+      uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) + i);
+      uint16_t h[4] = {uint16_t(t.x), uint16_t(t.x >> 16), uint16_t(t.y), uint16_t(t.y >> 16)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = sd == 1 ? f16_bits_to_f32(h[j]) : bf16_bits_to_f32(h[j]);
+    }
+    if (dd == 0) {
+      *reinterpret_cast<float4*>(static_cast<float*>(dst) + i) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint16_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = dd == 1 ? f32_to_f16_bits(v[j]) : f32_to_bf16_bits(v[j]);
+      uint2 t;
+      t.x = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
+      t.y = uint32_t(h[2]) | (uint32_t(h[3]) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(dst) + i) = t;
+    }
+  }
+  // Tail (at most 3 elements, handled by the thread that reached it).
+  if (i < n) {
+    for (; i < n; ++i) store_from_f32(dst, dd, i, load_as_f32(src, sd, i));
+  }
+}
+
+__global__ void __launch_bounds__(256) cast_scalar_kernel(const void* __restrict__ src, int sd,
+                                                          void* __restrict__ dst, int dd, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x)
+    store_from_f32(dst, dd, i, load_as_f32(src, sd, i));
+}
+
+// dst[b][c][r] = src[b][r][c] converted; 64x64 tiles through LDS.
+__global__ void __launch_bounds__(256) cast_transpose_kernel(const void* __restrict__ src, int sd,
+                                                             void* __restrict__ dst, int dd,
+                                                             int64_t rows, int64_t cols) {
+  __shared__ float tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+  const int64_t base = b * rows * cols;
+  for (int y = ty; y < 64; y += 4) {
+    const int64_t r = r0 + y, c = c0 + tx;
+    tile[y][tx] = (r < rows && c < cols) ? load_as_f32(src, sd, base + r * cols + c) : 0.f;
+  }
+  __syncthreads();
+  for (int y = ty; y < 64; y += 4) {
+    const int64_t c = c0 + y, r = r0 + tx;
+    if (r < rows && c < cols) store_from_f32(dst, dd, base + c * rows + r, tile[tx][y]);
+  }
+}
+
+// ---- strided copy -------------------------------------------------------------
+
+struct CopyArgs {
+  int64_t shape[BG_MAX_RANK];
+  int64_t stride[BG_MAX_RANK];
+  int rank;
+  int64_t n;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) copy_strided_kernel(const T* __restrict__ src,
+                                                           T* __restrict__ dst, CopyArgs A) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < A.n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    int64_t rem = i, off = 0;
+    for (int d = A.rank - 1; d >= 0; --d) {
+      const int64_t idx = rem % A.shape[d];
+      rem /= A.shape[d];
+      off += idx * A.stride[d];
+    }
+    dst[i] = src[off];
+  }
+}
+
+// ---- LayerNorm -----------------------------------------------------------------
+// Same arithmetic as the oracle: mean = sum/cols; centered = x - mean;
+// var = sum(centered^2)/cols; inv = 1/sqrt(var + eps); y = centered*inv*w + b,
+// every step rounded to f32 (no contraction in this file).
+
+template <int PER>
+__global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict__ x, int xd,
+                                                         const float* __restrict__ w,
+                                                         const float* __restrict__ bias,
+                                                         void* __restrict__ y, int yd,
+                                                         int64_t rows, int64_t cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // no block-level barriers below
+  const int64_t base = row * cols;
+  float v[PER];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t c = int64_t(j) * 64 + lane;
+    v[j] = c < cols ? load_as_f32(x, xd, base + c) : 0.f;
+    s += v[j];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float mean = s / float(cols);
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t c = int64_t(j) * 64 + lane;
+    const float cv = v[j] - mean;
+    v[j] = cv;
+    if (c < cols) q += cv * cv;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+  const float var = q / float(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t c = int64_t(j) * 64 + lane;
+    if (c < cols) {
+      const float xh = v[j] * inv;
+      const float t = xh * w[c];
+      store_from_f32(y, yd, base + c, t + bias[c]);
+    }
+  }
+}
+
+// Fallback for very wide rows: three passes over global memory.
+__global__ void __launch_bounds__(256) layer_norm_wide_kernel(const void* __restrict__ x, int xd,
+                                                              const float* __restrict__ w,
+                                                              const float* __restrict__ bias,
+                                                              void* __restrict__ y, int yd,
+                                                              int64_t rows, int64_t cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) s += load_as_f32(x, xd, base + c);
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float mean = s / float(cols);
+  float q = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float cv = load_as_f32(x, xd, base + c) - mean;
+    q += cv * cv;
+  }
+  for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+  const float inv = 1.0f / sqrtf(q / float(cols) + eps);
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float xh = (load_as_f32(x, xd, base + c) - mean) * inv;
+    const float t = xh * w[c];
+    store_from_f32(y, yd, base + c, t + bias[c]);
+  }
+}
+
+// ---- generic attention ----------------------------------------------------------
+// One wavefront per query row.  Lanes own keys in chunks of 64 for the score
+// pass and own output dims (d = lane + 64*t) for the P@V pass.  Supports:
+//   * one-pass online softmax (f32, the legacy kernel's m0 = -1e20 sentinel
+//     and 1/l guard, flash_attention.ts:99-129);
+//   * exact two-pass softmax with P rounded to the 16-bit input dtype before
+//     P@V and scores rounded before scaling (the AMP SDPA graph,
+//     _functional.py:1505-1533 realized by _realize.py handlers);
+//   * additive f32 mask [1|B,1|H,Sq,Sk] and a causal flag (j > i masked,
+//     np.triu(..., k=1) in the reference SDPA).
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* mask;
+  void* o;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int64_t mask_sb, mask_sh;
+  int64_t B, H, Sq, Sk, D;
+  float scale;
+  int causal;
+  int in_dtype;
+  int out_dtype;
+  int round_scores;
+  int two_pass;
+};
+
+constexpr int kGenMaxD = 256;
+
+__global__ void __launch_bounds__(256) attention_generic_kernel(AttnArgs A) {
+  __shared__ float qs[4][kGenMaxD];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t row = int64_t(blockIdx.x) * 4 + w;
+  const int64_t total = A.B * A.H * A.Sq;
+  const bool active = row < total;
+  const int64_t rr = active ? row : 0;
+  const int64_t i = rr % A.Sq;
+  const int64_t bh = rr / A.Sq;
+  const int64_t h = bh % A.H, b = bh / A.H;
+  const char* qp = static_cast<const char*>(A.q);
+  const int es = A.in_dtype == 0 ? 4 : 2;
+  const int64_t qbase = b * A.q_sb + h * A.q_sh + i * A.q_ss;
+  for (int64_t d = lane; d < A.D; d += 64) qs[w][d] = load_as_f32(qp, A.in_dtype, qbase + d);
+  __syncthreads();
+  (void)es;
+  const int64_t kbase = b * A.k_sb + h * A.k_sh;
+  const int64_t vbase = b * A.v_sb + h * A.v_sh;
+  const float* mrow = A.mask ? A.mask + b * A.mask_sb + h * A.mask_sh + i * A.Sk : nullptr;
+  const int64_t kend = A.causal ? std::min<int64_t>(A.Sk, i + 1) : A.Sk;
+
+  auto score = [&](int64_t j) -> float {
+    if (j >= kend) return -INFINITY;
+    float s = 0.f;
+    const int64_t kb = kbase + j * A.k_ss;
+    for (int64_t d = 0; d < A.D; ++d) s += qs[w][d] * load_as_f32(A.k, A.in_dtype, kb + d);
+    if (A.round_scores) s = round_through(s, A.in_dtype);
+    s = s * A.scale;
+    if (mrow) s = s + mrow[j];
+    return s;
+  };
+
+  constexpr int kT = kGenMaxD / 64;
+  float acc[kT];
+#pragma unroll
+  for (int t = 0; t < kT; ++t) acc[t] = 0.f;
+  float m = -1.0e20f, l = 0.f;
+
+  if (!A.two_pass) {
+    for (int64_t j0 = 0; j0 < A.Sk; j0 += 64) {
+      const int64_t j = j0 + lane;
+      const float s = (active && j < A.Sk) ? score(j) : -INFINITY;
+      float cmax = s;
+      for (int o = 32; o >= 1; o >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, o, 64));
+      const float mn = fmaxf(m, cmax);
+      const float alpha = expf(m - mn);
+      const float p = expf(s - mn);
+      float ps = p;
+      for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o, 64);
+      l = alpha * l + ps;
+      m = mn;
+#pragma unroll
+      for (int t = 0; t < kT; ++t) acc[t] *= alpha;
+      const int64_t jn = std::min<int64_t>(64, A.Sk - j0);
+      for (int jj = 0; jj < jn; ++jj) {
+        const float pj = __shfl(p, jj, 64);
+        const int64_t vb = vbase + (j0 + jj) * A.v_ss;
+#pragma unroll
+        for (int t = 0; t < kT; ++t) {
+          const int64_t d = int64_t(t) * 64 + lane;
+          if (d < A.D) acc[t] += pj * load_as_f32(A.v, A.in_dtype, vb + d);
+        }
+      }
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) acc[t] *= inv;
+  } else {
+    // Pass 1: row max and sum of exp(s - max) (softmax in f32).
+    float mx = -INFINITY;
+    for (int64_t j0 = 0; j0 < A.Sk; j0 += 64) {
+      const int64_t j = j0 + lane;
+      const float s = (active && j < A.Sk) ? score(j) : -INFINITY;
+      mx = fmaxf(mx, s);
+    }
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float sum = 0.f;
+    for (int64_t j0 = 0; j0 < A.Sk; j0 += 64) {
+      const int64_t j = j0 + lane;
+      const float s = (active && j < A.Sk) ? score(j) : -INFINITY;
+      sum += (j < A.Sk) ? expf(s - mx) : 0.f;
+    }
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    // Pass 2: P = exp(s - max) / sum rounded to the input dtype, then P@V.
+    for (int64_t j0 = 0; j0 < A.Sk; j0 += 64) {
+      const int64_t j = j0 + lane;
+      const float s = (active && j < A.Sk) ? score(j) : -INFINITY;
+      float p = (j < A.Sk) ? expf(s - mx) / sum : 0.f;
+      p = round_through(p, A.in_dtype);
+      const int64_t jn = std::min<int64_t>(64, A.Sk - j0);
+      for (int jj = 0; jj < jn; ++jj) {
+        const float pj = __shfl(p, jj, 64);
+        const int64_t vb = vbase + (j0 + jj) * A.v_ss;
+#pragma unroll
+        for (int t = 0; t < kT; ++t) {
+          const int64_t d = int64_t(t) * 64 + lane;
+          if (d < A.D) acc[t] += pj * load_as_f32(A.v, A.in_dtype, vb + d);
+        }
+      }
+    }
+  }
+  if (!active) return;
+  const int64_t obase = b * A.o_sb + h * A.o_sh + i * A.o_ss;
+#pragma unroll
+  for (int t = 0; t < kT; ++t) {
+    const int64_t d = int64_t(t) * 64 + lane;
+    if (d < A.D) store_from_f32(A.o, A.out_dtype, obase + d, acc[t]);
+  }
+}
+
+int grid1(int64_t n, int per) {
+  return int(std::max<int64_t>(1, std::min<int64_t>((n + per - 1) / per, 256 * 64)));
+}
+
+}  // namespace
+
+namespace bg {
+
+void launch_cast(bg_ctx* ctx, const void* src, int sd, void* dst, int dd, int64_t n) {
+  if (n <= 0) return;
+  const bool aligned = reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+  if (aligned) {
+    hipLaunchKernelGGL(cast_kernel, dim3(grid1(n / 4 + 1, 256)), dim3(256), 0, ctx->stream,
+                       src, sd, dst, dd, n);
+  } else {
+    hipLaunchKernelGGL(cast_scalar_kernel, dim3(grid1(n, 256)), dim3(256), 0, ctx->stream, src,
+                       sd, dst, dd, n);
+  }
+  hip_check(hipGetLastError(), "cast launch");
+}
+
+void launch_cast_transpose(bg_ctx* ctx, const void* src, int sd, void* dst, int dd,
+                           int64_t rows, int64_t cols, int64_t batch) {
+  if (rows <= 0 || cols <= 0 || batch <= 0) return;
+  if (batch > 65535) fail(BG_E_UNSUPPORTED, "cast_transpose: batch > 65535");
+  dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64), unsigned(batch));
+  hipLaunchKernelGGL(cast_transpose_kernel, grid, dim3(256), 0, ctx->stream, src, sd, dst, dd,
+                     rows, cols);
+  hip_check(hipGetLastError(), "cast_transpose launch");
+}
+
+void launch_copy_strided(bg_ctx* ctx, const void* src, int64_t es, void* dst,
+                         const std::vector<int64_t>& shape, const std::vector<int64_t>& strides) {
+  CopyArgs A{};
+  A.rank = int(shape.size());
+  A.n = 1;
+  for (int i = 0; i < A.rank; ++i) {
+    A.shape[i] = shape[i];
+    A.stride[i] = strides[i];
+    A.n *= shape[i];
+  }
+  if (A.n == 0) return;
+  if (A.rank == 0) {
+    A.rank = 1;
+    A.shape[0] = 1;
+    A.stride[0] = 0;
+  }
+  const int g = grid1(A.n, 256);
+  switch (es) {
+    case 1: hipLaunchKernelGGL(copy_strided_kernel<uint8_t>, dim3(g), dim3(256), 0, ctx->stream,
+                               static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), A); break;
+    case 2: hipLaunchKernelGGL(copy_strided_kernel<uint16_t>, dim3(g), dim3(256), 0, ctx->stream,
+                               static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), A); break;
+    case 4: hipLaunchKernelGGL(copy_strided_kernel<uint32_t>, dim3(g), dim3(256), 0, ctx->stream,
+                               static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), A); break;
+    case 8: hipLaunchKernelGGL(copy_strided_kernel<uint64_t>, dim3(g), dim3(256), 0, ctx->stream,
+                               static_cast<const uint64_t*>(src), static_cast<uint64_t*>(dst), A); break;
+    default: fail(BG_E_DTYPE, "copy_strided: unsupported element size");
+  }
+  hip_check(hipGetLastError(), "copy_strided launch");
+}
+
+void launch_layer_norm(bg_ctx* ctx, const void* x, int xd, const float* w, const float* b,
+                       void* y, int yd, int64_t rows, int64_t cols, float eps) {
+  if (rows == 0) return;
+  const dim3 grid(unsigned((rows + 3) / 4));
+  if (cols <= 256) {
+    hipLaunchKernelGGL(layer_norm_kernel<4>, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y, yd,
+                       rows, cols, eps);
+  } else if (cols <= 1024) {
+    hipLaunchKernelGGL(layer_norm_kernel<16>, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y, yd,
+                       rows, cols, eps);
+  } else if (cols <= 2048) {
+    hipLaunchKernelGGL(layer_norm_kernel<32>, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y, yd,
+                       rows, cols, eps);
+  } else {
+    hipLaunchKernelGGL(layer_norm_wide_kernel, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y,
+                       yd, rows, cols, eps);
+  }
+  hip_check(hipGetLastError(), "layer_norm launch");
+}
+
+void launch_attention_generic(bg_ctx* ctx, const bg_attention_desc& d, const void* q,
+                              const void* k, const void* v, const float* mask, int64_t mask_sb,
+                              int64_t mask_sh, void* o, bool two_pass) {
+  if (d.d > kGenMaxD) fail(BG_E_UNSUPPORTED, "flash_attention: head dim > 256");
+  AttnArgs A{};
+  A.q = q; A.k = k; A.v = v; A.mask = mask; A.o = o;
+  A.q_sb = d.q_sb; A.q_sh = d.q_sh; A.q_ss = d.q_ss;
+  A.k_sb = d.k_sb; A.k_sh = d.k_sh; A.k_ss = d.k_ss;
+  A.v_sb = d.v_sb; A.v_sh = d.v_sh; A.v_ss = d.v_ss;
+  A.o_sb = d.o_sb; A.o_sh = d.o_sh; A.o_ss = d.o_ss;
+  A.mask_sb = mask_sb; A.mask_sh = mask_sh;
+  A.B = d.batch; A.H = d.heads; A.Sq = d.sq; A.Sk = d.sk; A.D = d.d;
+  A.scale = d.scale;
+  A.causal = d.causal;
+  A.in_dtype = d.in_dtype;
+  A.out_dtype = d.out_dtype;
+  A.round_scores = d.round_scores;
+  A.two_pass = two_pass ? 1 : 0;
+  const int64_t rows = d.batch * d.heads * d.sq;
+  hipLaunchKernelGGL(attention_generic_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0,
+                     ctx->stream, A);
+  hip_check(hipGetLastError(), "attention launch");
+}
+
+void launch_attention_masked_f32(bg_ctx* ctx, const float* q, const float* k, const float* v,
+                                 const float* mask, int64_t mask_b, int64_t mask_h, float* o,
+                                 int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t dd,
+                                 float scale) {
+  bg_attention_desc d{};
+  d.batch = b; d.heads = h; d.sq = sq; d.sk = sk; d.d = dd;
+  d.q_ss = dd; d.q_sh = sq * dd; d.q_sb = h * sq * dd;
+  d.k_ss = dd; d.k_sh = sk * dd; d.k_sb = h * sk * dd;
+  d.v_ss = dd; d.v_sh = sk * dd; d.v_sb = h * sk * dd;
+  d.o_ss = dd; d.o_sh = sq * dd; d.o_sb = h * sq * dd;
+  d.scale = scale;
+  d.in_dtype = BG_F32;
+  d.out_dtype = BG_F32;
+  launch_attention_generic(ctx, d, q, k, v, mask, mask_b, mask_h, o, false);
+}
+
+void launch_reduce_last(bg_ctx* ctx, const void* x, int dtype, void* y, int64_t rows,
+                        int64_t cols, int op) {
+  (void)ctx; (void)x; (void)dtype; (void)y; (void)rows; (void)cols; (void)op;
+  fail(BG_E_UNSUPPORTED, "reduce_last: routed through fused_ex");
+}
+
+}  // namespace bg

@@ -1,0 +1,221 @@
+"""Kernel-level parity of the HIP path against the NumPy oracle (GPU).
+
+Every test calls libbghip through the bridge (C ABI) on seeded inputs and
+compares with oracle/ops.py at sizes the oracle finishes in seconds:
+bit-exact for casts / masks / copies, abs-or-rel 1e-4 for f32 and 2e-2 for
+f16/bf16 MFMA paths (the tolerances BASELINE.json's north star states).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+TOL32 = 1e-4
+TOL16 = 2e-2
+
+
+def up(br, a, dtype=None):
+    a = np.ascontiguousarray(a)
+    return br.upload(a, a.shape, dtype or a.dtype.name)
+
+
+def test_upload_materialize_roundtrip(bridge, rng):
+    for dt in (np.float32, np.float16, np.uint8):
+        a = (rng.standard_normal((7, 33)) * 10).astype(dt)
+        h = up(bridge, a)
+        back = bridge.to_numpy(h)
+        assert back.dtype == a.dtype and np.array_equal(back.view(np.uint8), a.view(np.uint8))
+        bridge.release(h)
+        bridge.release(h)  # idempotent (realizer.ts:1036-1041)
+
+
+def test_bridge_matmul_known_answer(bridge):
+    # webgpu_real.test.ts:1558-1589
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([[5, 6], [7, 8]], np.float32)
+    ha, hb = up(bridge, a), up(bridge, b)
+    hc = bridge.matmul(ha, hb, 2, 2, 2, "float32")
+    assert bridge.to_numpy(hc).ravel().tolist() == [19, 22, 43, 50]
+    # reference.test.ts:42-50
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    hd = bridge.matmul(up(bridge, a), up(bridge, b), 2, 3, 2, "float32")
+    assert bridge.to_numpy(hd).ravel().tolist() == [58, 64, 139, 154]
+
+
+@pytest.mark.parametrize("m,k,n", [(17, 23, 19), (64, 784, 128), (64, 128, 10), (129, 65, 257), (256, 512, 384)])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_gemm_f32(bridge, rng, m, k, n, trans_b):
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, k) if trans_b else (k, n)).astype(np.float32)
+    h = bridge.matmul_ex(up(bridge, a), up(bridge, b), m=m, n=n, k=k, trans_b=trans_b, in_dtype="float32")
+    y = bridge.to_numpy(h)
+    ref = a @ (b.T if trans_b else b)
+    truth = a.astype(np.float64) @ (b.T if trans_b else b).astype(np.float64)
+    err_gpu = np.abs(y - truth)
+    err_ref = np.abs(ref - truth)
+    ok = O.within(y, ref, TOL32) | (err_gpu <= np.maximum(err_ref, TOL32))
+    assert ok.all(), O.report(y, ref, TOL32)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("m,k,n,trans_b", [(17, 24, 19, False), (128, 64, 128, True), (256, 256, 256, False),
+                                           (300, 136, 200, True), (512, 1024, 768, True)])
+def test_gemm_16bit_round_bias(bridge, rng, dtype, m, k, n, trans_b):
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, k) if trans_b else (k, n)).astype(np.float32)
+    bias = rng.uniform(-0.1, 0.1, (n,)).astype(np.float32)
+    if dtype == "float16":
+        a16, b16 = a.astype(np.float16), b.astype(np.float16)
+        ha, hb = up(bridge, a16), up(bridge, b16)
+        bm = b16.T if trans_b else b16
+        ref = O.matmul(a16, np.ascontiguousarray(bm)).astype(np.float32) + bias
+    else:
+        a16, b16 = O.f32_to_bf16_bits(a), O.f32_to_bf16_bits(b)
+        ha, hb = up(bridge, a16, "bfloat16"), up(bridge, b16, "bfloat16")
+        bm = b16.T if trans_b else b16
+        ref = O.bf16_bits_to_f32(O.matmul_bf16(a16, np.ascontiguousarray(bm))) + bias
+    hbias = up(bridge, bias)
+    h = bridge.matmul_ex(ha, hb, m=m, n=n, k=k, trans_b=trans_b, in_dtype=dtype, out_dtype="float32",
+                         bias=hbias, round_out=True)
+    y = bridge.to_numpy(h)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
+def test_gemm_batched_f16(bridge, rng):
+    B, m, k, n = 6, 96, 64, 80
+    a = rng.standard_normal((B, m, k)).astype(np.float16)
+    b = rng.standard_normal((B, n, k)).astype(np.float16)
+    h = bridge.matmul_ex(up(bridge, a), up(bridge, b), batch=B, m=m, n=n, k=k, trans_b=True,
+                         in_dtype="float16", out_dtype="float16", round_out=True)
+    y = bridge.to_numpy(h).astype(np.float32)
+    ref = np.stack([O.matmul(a[i], np.ascontiguousarray(b[i].T)) for i in range(B)]).astype(np.float32)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
+@pytest.mark.parametrize("shape", [(4, 4096), (33, 100), (128, 4096), (3, 5, 64)])
+def test_fused_c2_rowsum(bridge, rng, shape):
+    a, b, c = (rng.standard_normal(shape).astype(np.float32) for _ in range(3))
+    ops = [("MUL", -1, -2, 0), ("ADD", 0, -3, 0), ("IMM", 0, 0, 0), ("CMP_GT", 1, 2, 0),
+           ("WHERE", 3, 1, 2), ("NEG", -1, 0, 0), ("MUL", 5, -1, 0), ("EXP", 6, 0, 0), ("MUL", 4, 7, 0)]
+    hs = [up(bridge, t) for t in (a, b, c)]
+    h = bridge.fused_ex(hs, ops, shape, "float32", imms=[0.0], reduce=1)
+    y = bridge.to_numpy(h)
+    ref = O.c2_chain(a.reshape(-1, shape[-1]), b.reshape(-1, shape[-1]), c.reshape(-1, shape[-1]))
+    ref = ref.reshape(shape[:-1])
+    assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)
+    # Elementwise part alone (no reduction): within 1e-4 (exp is not bit-exact).
+    h2 = bridge.fused_ex(hs, ops, shape, "float32", imms=[0.0])
+    y2 = bridge.to_numpy(h2)
+    ref2 = O.fused_program([a, b, c], ops, [0.0])
+    assert O.within(y2, ref2, TOL32).all(), O.report(y2, ref2, TOL32)
+
+
+def test_fused_reference_opcodes_bit_exact(bridge, rng):
+    # ADD/MUL/DIV/NEG are IEEE single ops: bit-exact against NumPy.
+    a = rng.standard_normal((257, 31)).astype(np.float32)
+    b = rng.standard_normal((257, 31)).astype(np.float32) + 3
+    ops = [("ADD", -1, -2), ("MUL", 0, -1), ("DIV", 1, -2), ("NEG", 2, 0)]
+    h = bridge.fused_elementwise([up(bridge, a), up(bridge, b)], ops, a.shape, "float32")
+    y = bridge.to_numpy(h)
+    ref = O.fused_program([a, b], ops)
+    assert np.array_equal(y, ref)
+    # closed form exp(a+b)/a (webgpu_real.test.ts:1431-1472), tolerance 1e-3 there.
+    ops2 = [("ADD", -1, -2), ("EXP", 0, 0), ("DIV", 1, -1)]
+    h2 = bridge.fused_elementwise([up(bridge, a), up(bridge, b)], ops2, a.shape, "float32")
+    y2 = bridge.to_numpy(h2)
+    assert O.within(y2, np.exp(a + b) / a, TOL32).all()
+
+
+def test_fused_broadcast_where_cmp_bool(bridge, rng):
+    x = rng.standard_normal((6, 40)).astype(np.float32)
+    bias = rng.standard_normal((40,)).astype(np.float32)
+    col = rng.standard_normal((6, 1)).astype(np.float32)
+    hx, hb, hc = up(bridge, x), up(bridge, bias), up(bridge, col)
+    ops = [("ADD", -1, -2, 0), ("CMP_LT", 0, -3, 0)]
+    strides = [[40, 1], [0, 1], [1, 0]]
+    h = bridge.fused_ex([hx, hb, hc], ops, (6, 40), "bool", in_strides=strides)
+    y = bridge.to_numpy(h)
+    assert y.dtype == np.bool_ and np.array_equal(y, (x + bias) < col)
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 1000, 4099])
+def test_cast_bit_exact(bridge, rng, n):
+    x = (rng.standard_normal(n) * 300).astype(np.float32)
+    x[: min(n, 3)] = [np.inf, -0.0, 65520.0][: min(n, 3)]
+    h = up(bridge, x)
+    h16 = bridge.cast(h, "float32", "float16", (n,))
+    assert np.array_equal(bridge.to_numpy(h16).view(np.uint16), x.astype(np.float16).view(np.uint16))
+    hb = bridge.cast(h, "float32", "bfloat16", (n,))
+    assert np.array_equal(bridge.to_numpy(hb), O.f32_to_bf16_bits(x))
+    hback = bridge.cast(h16, "float16", "float32", (n,))
+    assert np.array_equal(bridge.to_numpy(hback), x.astype(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 768), (5, 100), (3, 3000), (64, 2048)])
+def test_layer_norm(bridge, rng, rows, cols):
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 3 + 1
+    w = rng.standard_normal(cols).astype(np.float32)
+    b = rng.standard_normal(cols).astype(np.float32)
+    h = bridge.layer_norm(up(bridge, x), up(bridge, w), up(bridge, b), rows, cols, 1e-5)
+    y = bridge.to_numpy(h)
+    ref = O.layer_norm(x, w, b, 1e-5)
+    assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)
+
+
+def test_copy_strided_permute(bridge, rng):
+    x = rng.standard_normal((2, 5, 3, 4)).astype(np.float32)
+    h = up(bridge, x)
+    perm = (0, 2, 1, 3)
+    shape = tuple(x.shape[p] for p in perm)
+    st = np.array(x.strides) // 4
+    strides = tuple(int(st[p]) for p in perm)
+    y = bridge.to_numpy(bridge.copy_strided(h, 0, shape, strides))
+    assert np.array_equal(y, np.transpose(x, perm))
+
+
+@pytest.mark.parametrize("b,h,s,causal", [(1, 2, 4, False), (2, 3, 128, True), (1, 2, 200, True),
+                                          (2, 2, 256, False), (1, 1, 1000, True)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_attention_mfma(bridge, rng, b, h, s, causal, dtype):
+    d = 64
+    q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
+    scale = 1.0 / np.sqrt(d)
+    if dtype == "float16":
+        q16, k16, v16 = (t.astype(np.float16) for t in (q, k, v))
+        hq, hk, hv = up(bridge, q16), up(bridge, k16), up(bridge, v16)
+        ref = O.sdpa_amp(q16, k16, v16, scale, causal).astype(np.float32)
+    else:
+        q16, k16, v16 = (O.f32_to_bf16_bits(t) for t in (q, k, v))
+        hq, hk, hv = (up(bridge, t, "bfloat16") for t in (q16, k16, v16))
+        ref = O.bf16_bits_to_f32(O.sdpa_bf16(q16, k16, v16, scale, causal))
+    ho = bridge.attention_ex(hq, hk, hv, batch=b, heads=h, sq=s, sk=s, d=d, scale=scale, causal=causal,
+                             in_dtype=dtype, round_scores=True)
+    y = bridge.to_numpy(ho)
+    y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
+def test_attention_generic_f32_legacy(bridge, rng):
+    b, h, s, d = 1, 2, 33, 16
+    q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
+    mask = np.where(rng.random((s, s)) < 0.2, -1e9, 0).astype(np.float32)
+    ho = bridge.flash_attention(up(bridge, q), up(bridge, k), up(bridge, v), up(bridge, mask),
+                                b, h, s, s, d, 0.25, "float32")
+    y = bridge.to_numpy(ho)
+    ref = O.attention_online_f32(q, k, v, 0.25, mask)
+    assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)
+
+
+def test_alive_handles_and_snapshot(bridge, rng):
+    before = bridge.aliveHandleCount()
+    h = up(bridge, rng.standard_normal(10).astype(np.float32))
+    assert bridge.aliveHandleCount() == before + 1
+    snap = bridge.resourceSnapshot()
+    assert snap["currentOwnedGpuBytes"] >= 40
+    bridge.release(h)
+    assert bridge.aliveHandleCount() == before

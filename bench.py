@@ -1,0 +1,319 @@
+#!/usr/bin/env python3
+"""Benchmark of the HIP realizer on 1 MI355X (the BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,...]
+
+Prints ONE JSON line.  ``value`` is configs[1] of BASELINE.json -- the fused
+elementwise + row-reduction chain ``relu(a*b+c)*exp(-a*a) -> sum(axis=1)`` on
+[4096, 4096] f32 -- in GB/s of algorithmic traffic (3 x 64 MiB read + 16 KiB
+written per step).  One step is one realization of that chain (one fused
+kernel launch) over inputs already resident in HBM.  Three input sets are
+rotated so the 256 MB Infinity Cache cannot hold the working set.
+
+``extra`` carries the other configs of the metric (GEMM and attention
+TFLOP/s with their fraction of the MFMA peak, the MLP latency), each with
+the per-launch kernel time measured by HIP events on the library's stream.
+
+``roofline`` is for the dominant kernel of ``value`` (the fused kernel),
+``cpu_baseline`` is the NumPy restatement of the reference CPU realizer
+(oracle/, test infrastructure, used here only as the timed comparator and
+the parity check) on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2516.6  # dense fp16/bf16
+FP32_PEAK_TFLOPS = 157.3       # dense fp32 (MFMA)
+
+C2_SHAPE = (4096, 4096)
+C2_BYTES = 3 * 4096 * 4096 * 4 + 4096 * 4  # 201,342,976 B per step
+C2_OPS = [("MUL", -1, -2, 0), ("ADD", 0, -3, 0), ("IMM", 0, 0, 0), ("CMP_GT", 1, 2, 0),
+          ("WHERE", 3, 1, 2), ("NEG", -1, 0, 0), ("MUL", 5, -1, 0), ("EXP", 6, 0, 0),
+          ("MUL", 4, 7, 0)]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed(br, step, steps: int, warmup: int, label: str):
+    """Run `warmup` untimed steps, then `steps` timed ones bracketed by a
+    stream synchronize on both sides.  Returns (wall ms/step, mean per-launch
+    ms of kernels whose profile label is `label`, launches counted)."""
+    for _ in range(warmup):
+        step()
+    br.synchronize()
+    n0 = len(br.flushProfiles()["passProfiles"])
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    br.synchronize()
+    t1 = time.perf_counter()
+    profs = br.flushProfiles()["passProfiles"][n0:]
+    ks = [p["gpuMs"] for p in profs if p["label"] == label]
+    kmean = float(np.mean(ks)) if ks else float("nan")
+    return (t1 - t0) * 1e3 / steps, kmean, len(ks)
+
+
+# --------------------------------------------------------------------------- C2
+
+def bench_c2(br, steps, warmup, check=True):
+    rng = np.random.default_rng(2)
+    sets = []
+    host0 = None
+    for s in range(3):
+        r = np.random.default_rng(1000 + s) if s else rng
+        a, b, c = (r.standard_normal(C2_SHAPE, dtype=np.float32) for _ in range(3))
+        if s == 0:
+            host0 = (a, b, c)
+        sets.append([br.upload(t, t.shape, "float32") for t in (a, b, c)])
+    i = [0]
+
+    def step():
+        hs = sets[i[0] % 3]
+        i[0] += 1
+        h = br.fused_ex(hs, C2_OPS, C2_SHAPE, "float32", imms=[0.0], reduce=1)
+        br.release(h)
+
+    wall_ms, k_ms, nk = timed(br, step, steps, warmup, "fused_reduce")
+    parity = None
+    if check:
+        from oracle import ops as O  # checker only
+        h = br.fused_ex(sets[0], C2_OPS, C2_SHAPE, "float32", imms=[0.0], reduce=1)
+        y = br.to_numpy(h)
+        br.release(h)
+        ref = O.c2_chain(*host0)
+        parity = O.report(y, ref, 1e-4)
+    for hs in sets:
+        for h in hs:
+            br.release(h)
+    return {
+        "wall_ms": wall_ms, "kernel_ms": k_ms, "launches": nk,
+        "gbs_wall": C2_BYTES / (wall_ms * 1e-3) / 1e9,
+        "gbs_kernel": C2_BYTES / (k_ms * 1e-3) / 1e9,
+        "parity": parity,
+    }, host0
+
+
+def cpu_c2(host, budget_s=12.0, max_reps=40):
+    """Time the NumPy oracle of C2 on the full [4096,4096] input (one thread:
+    NumPy's ufuncs and float32 sum run single-threaded)."""
+    from oracle import ops as O  # timed comparator only
+    a, b, c = host
+    O.c2_chain(a, b, c)
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < max_reps and time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        O.c2_chain(a, b, c)
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": C2_BYTES / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle.ops.c2_chain on the full [4096,4096] f32 input, {len(ts)} reps, "
+                      f"median {med * 1e3:.1f} ms"}
+
+
+# --------------------------------------------------------------------------- C3
+
+def bench_c3(br, steps, warmup, dtype):
+    M = N = K = 4096
+    rng = np.random.default_rng(3)
+    x = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    w = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, (N,)).astype(np.float32)
+    hb = br.upload(b, b.shape, "float32")
+    if dtype == "float16":
+        # AMP operands resident in HBM: x16 [M][K], w16 stored as W^T [N][K]
+        # (the layout the fused cast-transpose of the walker produces).
+        hx = br.upload(x.astype(np.float16), (M, K), "float16")
+        hw = br.upload(np.ascontiguousarray(w.astype(np.float16).T), (N, K), "float16")
+        kw = dict(trans_b=True, in_dtype="float16", out_dtype="float32", round_out=True)
+        label = "gemm_f16"
+        peak = MFMA_F16_PEAK_TFLOPS
+    else:
+        hx = br.upload(x, x.shape, "float32")
+        hw = br.upload(w, w.shape, "float32")
+        kw = dict(trans_b=False, in_dtype="float32", out_dtype="float32")
+        label = "gemm_f32"
+        peak = FP32_PEAK_TFLOPS
+
+    def step():
+        h = br.matmul_ex(hx, hw, m=M, n=N, k=K, bias=hb, **kw)
+        br.release(h)
+
+    wall_ms, k_ms, _ = timed(br, step, steps, warmup, label)
+    flops = 2.0 * M * N * K
+    out = {"wall_ms": wall_ms, "kernel_ms": k_ms,
+           "tflops_kernel": flops / (k_ms * 1e-3) / 1e12,
+           "tflops_wall": flops / (wall_ms * 1e-3) / 1e12}
+    out["frac_of_peak"] = out["tflops_kernel"] / peak
+    # Parity on a 256-row slice against the oracle (rel 1e-4 f32 / 2e-2 f16).
+    from oracle import ops as O  # checker only
+    h = br.matmul_ex(hx, hw, m=M, n=N, k=K, bias=hb, **kw)
+    y = br.to_numpy(h)[:256]
+    br.release(h)
+    if dtype == "float16":
+        ref = O.linear_amp(x[:256], w, b)
+        out["parity"] = O.report(y, ref, 2e-2)
+    else:
+        ref = x[:256] @ w + b
+        out["parity"] = O.report(y, ref, 1e-3)
+    for h in (hx, hw, hb):
+        br.release(h)
+    return out
+
+
+# --------------------------------------------------------------------------- C4
+
+def bench_c4(br, steps, warmup):
+    B, H, S, D = 8, 16, 2048, 64
+    rng = np.random.default_rng(4)
+    q, k, v = (rng.standard_normal((B, H, S, D), dtype=np.float32).astype(np.float16) for _ in range(3))
+    hq, hk, hv = (br.upload(t, t.shape, "float16") for t in (q, k, v))
+    scale = 1.0 / np.sqrt(D)
+
+    def run():
+        return br.attention_ex(hq, hk, hv, batch=B, heads=H, sq=S, sk=S, d=D, scale=scale, causal=True,
+                               in_dtype="float16", out_dtype="float16", round_scores=True)
+
+    def step():
+        br.release(run())
+
+    wall_ms, k_ms, _ = timed(br, step, steps, warmup, "attention_f16")
+    flops = 4.0 * B * H * D * S * (S + 1) / 2
+    out = {"wall_ms": wall_ms, "kernel_ms": k_ms,
+           "tflops_kernel": flops / (k_ms * 1e-3) / 1e12,
+           "tflops_wall": flops / (wall_ms * 1e-3) / 1e12}
+    out["frac_of_peak"] = out["tflops_kernel"] / MFMA_F16_PEAK_TFLOPS
+    from oracle import ops as O  # checker only: two (b, h) slices
+    h = run()
+    y = br.to_numpy(h).astype(np.float32)
+    br.release(h)
+    sl = (slice(0, 1), slice(0, 2))
+    ref = O.sdpa_amp(q[sl], k[sl], v[sl], scale, True).astype(np.float32)
+    out["parity"] = O.report(y[sl], ref, 2e-2)
+    for hh in (hq, hk, hv):
+        br.release(hh)
+    return out
+
+
+# --------------------------------------------------------------------------- C1
+
+def bench_c1(br, steps, warmup):
+    """MLP 784 -> 128 -> ReLU -> 10, batch 64, f32: two GEMM launches with the
+    PERMUTE folded into the NT layout and bias / relu fused in the epilogue."""
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((64, 784)).astype(np.float32)
+    lim1, lim2 = 1 / np.sqrt(784), 1 / np.sqrt(128)
+    w1 = rng.uniform(-lim1, lim1, (128, 784)).astype(np.float32)
+    b1 = rng.uniform(-lim1, lim1, (128,)).astype(np.float32)
+    w2 = rng.uniform(-lim2, lim2, (10, 128)).astype(np.float32)
+    b2 = rng.uniform(-lim2, lim2, (10,)).astype(np.float32)
+    hx, hw1, hb1, hw2, hb2 = (br.upload(t, t.shape, "float32") for t in (x, w1, b1, w2, b2))
+
+    def run():
+        h1 = br.matmul_ex(hx, hw1, m=64, n=128, k=784, trans_b=True, bias=hb1, act=1)
+        h2 = br.matmul_ex(h1, hw2, m=64, n=10, k=128, trans_b=True, bias=hb2)
+        br.release(h1)
+        return h2
+
+    def step():
+        br.release(run())
+
+    wall_ms, k_ms, _ = timed(br, step, steps, warmup, "gemm_f32")
+    h = run()
+    y = br.to_numpy(h)
+    br.release(h)
+    ref = np.maximum(x @ w1.T + b1, 0) @ w2.T + b2
+    from oracle import ops as O  # checker only
+    for hh in (hx, hw1, hb1, hw2, hb2):
+        br.release(hh)
+    return {"wall_us": wall_ms * 1e3, "kernel_us_per_gemm": k_ms * 1e3,
+            "parity": O.report(y, ref, 1e-4)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="c1,c2,c3,c4")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
+              f"the multi-GPU path is design-only", file=sys.stderr)
+        return 2
+    only = set(a.only.split(","))
+
+    from browsergrad_amd.bridge import HipRealizerBridge
+    br = HipRealizerBridge(device=0, profiling=True)
+
+    log("c2 fused elementwise + row sum [4096,4096] f32")
+    c2, host0 = bench_c2(br, a.steps, a.warmup)
+    log(f"c2 kernel {c2['kernel_ms'] * 1e3:.2f} us  {c2['gbs_kernel']:.0f} GB/s  parity {c2['parity']}")
+    extra = {}
+    if "c3" in only:
+        log("c3 gemm 4096^3 fp16 autocast")
+        extra["c3_gemm_fp16"] = bench_c3(br, max(10, a.steps // 2), a.warmup, "float16")
+        log(f"  {extra['c3_gemm_fp16']}")
+        log("c3 gemm 4096^3 fp32")
+        extra["c3_gemm_fp32"] = bench_c3(br, max(5, a.steps // 10), 2, "float32")
+        log(f"  {extra['c3_gemm_fp32']}")
+    if "c4" in only:
+        log("c4 causal attention B8 H16 S2048 D64 fp16")
+        extra["c4_attention_fp16"] = bench_c4(br, max(10, a.steps // 2), a.warmup)
+        log(f"  {extra['c4_attention_fp16']}")
+    if "c1" in only:
+        log("c1 mlp 784-128-10 batch 64 f32")
+        extra["c1_mlp_fp32"] = bench_c1(br, a.steps, a.warmup)
+        log(f"  {extra['c1_mlp_fp32']}")
+
+    cpu = None
+    if not a.no_cpu:
+        log("cpu baseline (NumPy oracle of C2, 1 thread)")
+        cpu = cpu_c2(host0)
+    br.close()
+
+    kernel_gbs = c2["gbs_kernel"]
+    line = {
+        "metric": "GEMM & attention TFLOP/s, fused-elementwise GB/s, % roofline on 1 MI355X",
+        "value": round(c2["gbs_wall"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(c2["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy PCG64 N(0,1)); 3 rotating input sets",
+        "config": {"workload": "C2: relu(a*b+c)*exp(-a*a) -> row sum, a,b,c [4096,4096] f32, "
+                               "one fused HIP kernel per step"},
+        "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_us": round(c2["kernel_ms"] * 1e3, 3),
+                     "algorithmic_bytes_per_launch": C2_BYTES},
+        "cpu_baseline": cpu,
+        "parity": c2["parity"],
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -354,6 +354,9 @@ std::string generate(const Plan& p) {
 struct KernelCache {
   std::mutex mu;
   std::unordered_map<uint64_t, hipFunction_t> fns;  // keyed by hash(device, source)
+  // Front cache keyed by the compact plan signature, so a repeated launch
+  // skips source generation, hashing and the device-property query.
+  std::unordered_map<std::string, hipFunction_t> by_plan;
 };
 
 KernelCache& cache() {
@@ -618,8 +621,31 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
   for (int i = 0; i < n_in; ++i)
     if (plan.kind[i] != IN_SCALAR) in_bytes += dtype_size(plan.dtype[i]);
 
-  const std::string src = generate(plan);
-  hipFunction_t fn = get_kernel(ctx->device, src);
+  // Compact binary signature of everything generate() depends on.
+  std::string sig;
+  {
+    int32_t head[8] = {ctx->device, plan.n_in, plan.nlead, plan.vec,
+                       plan.reduce, plan.tpr, plan.out_dtype, int32_t(plan.ops.size())};
+    sig.append(reinterpret_cast<const char*>(head), sizeof(head));
+    for (int i = 0; i < plan.n_in; ++i) {
+      int32_t io[2] = {plan.kind[i], plan.dtype[i]};
+      sig.append(reinterpret_cast<const char*>(io), sizeof(io));
+    }
+    sig.append(reinterpret_cast<const char*>(plan.ops.data()), plan.ops.size() * sizeof(bg_fused_op));
+  }
+  hipFunction_t fn = nullptr;
+  {
+    KernelCache& c = cache();
+    std::lock_guard<std::mutex> g(c.mu);
+    auto it = c.by_plan.find(sig);
+    if (it != c.by_plan.end()) fn = it->second;
+  }
+  if (!fn) {
+    fn = get_kernel(ctx->device, generate(plan));
+    KernelCache& c = cache();
+    std::lock_guard<std::mutex> g(c.mu);
+    c.by_plan[sig] = fn;
+  }
   size_t argsz = sizeof(A);
   void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &A, HIP_LAUNCH_PARAM_BUFFER_SIZE, &argsz,
                  HIP_LAUNCH_PARAM_END};

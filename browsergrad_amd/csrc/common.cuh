@@ -12,21 +12,19 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t v) {
   return __uint_as_float(uint32_t(v) << 16);
 }
 
-// Round-to-nearest-even f32 -> bf16 bits; NaN is kept quiet.
+// Round-to-nearest-even f32 -> bf16 bits (gfx950 v_cvt_pk_bf16_f32; NaN
+// stays a quiet NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
+// Round-to-nearest-even f32 -> f16 bits (v_cvt_f16_f32).
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
-  __half h = __float2half_rn(f);
-  return *reinterpret_cast<uint16_t*>(&h);
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t v) {
-  return __half2float(*reinterpret_cast<__half*>(&v));
+  return static_cast<float>(__builtin_bit_cast(_Float16, v));
 }
 
 // dtype codes follow include/bghip.h (0 f32, 1 f16, 2 bf16).
@@ -46,8 +44,8 @@ __device__ __forceinline__ void store_from_f32(void* p, int dtype, int64_t i, fl
 
 // Round an f32 value through the 16-bit dtype (1 f16, 2 bf16) and back.
 __device__ __forceinline__ float round_through(float x, int dtype) {
-  if (dtype == 1) return __half2float(__float2half_rn(x));
-  if (dtype == 2) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+  if (dtype == 1) return static_cast<float>(static_cast<_Float16>(x));
+  if (dtype == 2) return static_cast<float>(static_cast<__bf16>(x));
   return x;
 }
 

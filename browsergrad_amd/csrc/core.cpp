@@ -177,17 +177,18 @@ static void drop(bg_ctx* ctx, Record& r) {
   r.alloc = nullptr;
 }
 
-void* scratch(bg_ctx* ctx, size_t bytes) {
-  if (bytes <= ctx->scratch_bytes) return ctx->scratch;
-  if (ctx->scratch) {
+void* scratch(bg_ctx* ctx, size_t bytes, int slot) {
+  if (bytes <= ctx->scratch_bytes[slot]) return ctx->scratch[slot];
+  if (ctx->scratch[slot]) {
     hip_check(hipStreamSynchronize(ctx->stream), "synchronize before scratch grow");
-    hip_check(hipFree(ctx->scratch), "hipFree(scratch)");
-    ctx->scratch = nullptr;
+    hip_check(hipFree(ctx->scratch[slot]), "hipFree(scratch)");
+    ctx->scratch[slot] = nullptr;
+    ctx->scratch_bytes[slot] = 0;
   }
   size_t cap = pooled_size(bytes);
-  hip_check(hipMalloc(&ctx->scratch, cap), "hipMalloc(scratch)");
-  ctx->scratch_bytes = cap;
-  return ctx->scratch;
+  hip_check(hipMalloc(&ctx->scratch[slot], cap), "hipMalloc(scratch)");
+  ctx->scratch_bytes[slot] = cap;
+  return ctx->scratch[slot];
 }
 
 static hipEvent_t take_event(bg_ctx* ctx) {
@@ -210,12 +211,32 @@ Profile::Profile(bg_ctx* c, const char* label, int64_t bytes, int64_t flops)
   p.info.flops = flops;
   p.start = take_event(ctx);
   p.stop = take_event(ctx);
-  hip_check(hipEventRecord(p.start, ctx->stream), "hipEventRecord");
+  prev = ctx->active_profile;
+  ctx->active_profile = this;
 }
 
 Profile::~Profile() {
   if (!on) return;
-  if (hipEventRecord(p.stop, ctx->stream) == hipSuccess) ctx->pending.push_back(p);
+  ctx->active_profile = prev;
+  if (launches == 0) {
+    // Nothing was dispatched (e.g. an empty tensor): no timing to report.
+    ctx->event_pool.push_back(p.start);
+    ctx->event_pool.push_back(p.stop);
+    return;
+  }
+  if (launches > 1 && hipEventRecord(p.stop, ctx->stream) != hipSuccess) return;
+  ctx->pending.push_back(p);
+}
+
+void next_dispatch_events(bg_ctx* ctx, hipEvent_t* start, hipEvent_t* stop) {
+  *start = nullptr;
+  *stop = nullptr;
+  Profile* pr = ctx->active_profile;
+  if (!pr || !pr->on) return;
+  if (pr->launches++ == 0) {
+    *start = pr->p.start;
+    *stop = pr->p.stop;
+  }
 }
 
 static void resolve_profiles(bg_ctx* ctx) {
@@ -307,7 +328,8 @@ int bg_ctx_destroy(bg_ctx* ctx) {
     (void)hipEventDestroy(p.stop);
   }
   for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
-  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  for (void* sp : ctx->scratch)
+    if (sp) (void)hipFree(sp);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return BG_OK;

@@ -1,6 +1,7 @@
 // Internal declarations shared by the libbghip translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -8,6 +9,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 #include <unordered_map>
 #include <vector>
 
@@ -49,6 +51,8 @@ struct Record {
   }
 };
 
+struct Profile;
+
 struct PendingProfile {
   hipEvent_t start;
   hipEvent_t stop;
@@ -81,10 +85,13 @@ struct bg_ctx {
   std::vector<bg::PendingProfile> pending;
   std::vector<bg_pass_profile> done;
   std::vector<hipEvent_t> event_pool;
+  bg::Profile* active_profile = nullptr;
 
-  // Scratch buffers reused across launches (workspace for pre-passes).
-  void* scratch = nullptr;
-  size_t scratch_bytes = 0;
+  // Scratch buffers reused across launches (workspace for pre-passes):
+  // slot 0 = re-laid-out GEMM operand, slot 1 = f32 GEMM result awaiting an
+  // elementwise epilogue pass.
+  void* scratch[2] = {nullptr, nullptr};
+  size_t scratch_bytes[2] = {0, 0};
 };
 
 namespace bg {
@@ -96,21 +103,52 @@ bg_handle mint(bg_ctx* ctx, size_t nbytes, const std::vector<int64_t>& shape,
 bg_handle mint_view(bg_ctx* ctx, const Record& src, int64_t offset,
                     int64_t nbytes, const std::vector<int64_t>& shape,
                     int dtype);
-void* scratch(bg_ctx* ctx, size_t bytes);
+void* scratch(bg_ctx* ctx, size_t bytes, int slot = 0);
 std::vector<int64_t> to_shape(const int64_t* shape, int rank);
 int64_t numel(const std::vector<int64_t>& shape);
 
-// RAII profiling scope around one dispatch (hipEvent pair on ctx->stream).
+// RAII profiling scope around the dispatches of one bridge operation.  The
+// first kernel dispatched inside the scope carries the scope's start/stop
+// events in its own dispatch packet (hipExtLaunchKernel), so the measured
+// time is the kernel's execution time; when a scope dispatches more than one
+// kernel, the stop event is re-recorded on the stream when the scope closes.
 struct Profile {
   bg_ctx* ctx;
   bool on;
+  int launches = 0;
+  Profile* prev = nullptr;
   PendingProfile p;
   Profile(bg_ctx* c, const char* label, int64_t bytes, int64_t flops);
   ~Profile();
 };
 
+// Events the next dispatch on ctx->stream should carry (both NULL when no
+// profiling scope is open or the scope already dispatched a kernel).
+void next_dispatch_events(bg_ctx* ctx, hipEvent_t* start, hipEvent_t* stop);
+
+// Launch `kernel` on the context stream with the profiling scope's events.
+template <typename... KArgs, typename... Args>
+void dispatch(bg_ctx* ctx, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
+              Args... args) {
+  static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+  std::tuple<KArgs...> vals(static_cast<KArgs>(args)...);
+  void* ptrs[sizeof...(KArgs)];
+  std::apply([&ptrs](auto&... v) {
+    size_t i = 0;
+    ((ptrs[i++] = static_cast<void*>(&v)), ...);
+  }, vals);
+  hipEvent_t start = nullptr, stop = nullptr;
+  next_dispatch_events(ctx, &start, &stop);
+  hip_check(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, shmem,
+                               ctx->stream, start, stop, 0),
+            "kernel launch");
+}
+
 // Kernel launchers (one per translation unit).
 void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out);
+void launch_gelu_rows(bg_ctx* ctx, const float* src, int64_t ld_src, int64_t stride_src, void* dst,
+                      int64_t ld_dst, int64_t stride_dst, int dst_dtype, int64_t batch, int64_t rows,
+                      int64_t cols);
 void launch_cast(bg_ctx* ctx, const void* src, int src_dtype, void* dst,
                  int dst_dtype, int64_t n);
 void launch_cast_transpose(bg_ctx* ctx, const void* src, int src_dtype,

@@ -289,7 +289,7 @@ __global__ void __launch_bounds__(256) fa_fwd_d64_kernel(FaArgs P) {
 template <bool BF16, bool CAUSAL, bool ROUND_S>
 void launch_fa(bg_ctx* ctx, const FaArgs& A, int bh, int nqb) {
   dim3 grid(unsigned(bh), unsigned(nqb), 1);
-  hipLaunchKernelGGL((fa_fwd_d64_kernel<BF16, CAUSAL, ROUND_S>), grid, dim3(256), 0, ctx->stream, A);
+  bg::dispatch(ctx, fa_fwd_d64_kernel<BF16, CAUSAL, ROUND_S>, grid, dim3(256), 0, A);
 }
 
 bool al(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }

@@ -22,6 +22,7 @@
 // Numerics: every op runs in f32 and is rounded per op (-ffp-contract=off,
 // so a*b+c never becomes an FMA), matching NumPy's per-ufunc rounding; f16 /
 // bf16 rounding ops are explicit round-to-nearest-even conversions.
+#include <hip/hip_ext.h>
 #include <hip/hiprtc.h>
 
 #include <algorithm>
@@ -72,14 +73,9 @@ struct u2_ { u32 x, y; };
 __device__ __forceinline__ float bg_h2f(u16 v) { return (float)__builtin_bit_cast(_Float16, v); }
 __device__ __forceinline__ u16 bg_f2h(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
 __device__ __forceinline__ float bg_b2f(u16 v) { return __builtin_bit_cast(float, ((u32)v) << 16); }
-__device__ __forceinline__ u16 bg_f2b(float f) {
-  u32 u = __builtin_bit_cast(u32, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (u16)(u >> 16);
-}
+__device__ __forceinline__ u16 bg_f2b(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
 __device__ __forceinline__ float bg_rh(float x) { return (float)(_Float16)x; }
-__device__ __forceinline__ float bg_rb(float x) { return bg_b2f(bg_f2b(x)); }
+__device__ __forceinline__ float bg_rb(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float bg_max(float a, float b) { return (a != a || b != b) ? a + b : fmaxf(a, b); }
 __device__ __forceinline__ float bg_min(float a, float b) { return (a != a || b != b) ? a + b : fminf(a, b); }
 )";
@@ -662,7 +658,11 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
   }
   Profile prof(ctx, d.reduce_op == BG_RED_NONE ? "fused_elementwise" : "fused_reduce",
                total * in_bytes + obytes, total * int64_t(plan.ops.size()));
-  hip_check(hipModuleLaunchKernel(fn, grid, 1, 1, 256, 1, 1, 0, ctx->stream, nullptr, cfg),
+  hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+  next_dispatch_events(ctx, &ev_start, &ev_stop);
+  // Global size in work-items (grid blocks x 256 lanes).
+  hip_check(hipExtModuleLaunchKernel(fn, grid * 256u, 1, 1, 256, 1, 1, 0, ctx->stream, nullptr, cfg,
+                                     ev_start, ev_stop, 0),
             "fused_elementwise launch");
 }
 

@@ -2,27 +2,33 @@
 //
 // Replaces the reference's 16x16 scalar tiled WGSL GEMM
 // (packages/browsergrad-kernels/src/kernels/matmul_tiled.ts:51-139) behind
-// bridge.matmul (realizer.ts:1043-1060) and the autocast MATMUL semantics of
+// bridge.matmul (realizer.ts:1043-1060) and realizes the autocast MATMUL of
 // the CPU oracle (_realize.py:395-412: f16 inputs, f32 accumulate, result
-// rounded to f16).
+// rounded to f16) together with the bias ADD that follows it.
 //
-// 16-bit path (f16 / bf16 inputs):
+// 16-bit path (f16 / bf16 inputs), gemm16_kernel:
 //   * NT layout: A [M][K] and B^T [N][K], both K-contiguous, so every MFMA
-//     operand is one 16-byte LDS read.  x @ W.T (nn.Linear) is NT natively;
-//     x @ w (B = [K][N]) is re-laid out once by a cast/transpose pre-pass.
-//   * v_mfma_f32_32x32x16_{f16,bf16}; block tile BM x BN x 64, four
+//     operand fragment is one 16-byte LDS read.  x @ W.T (nn.Linear) is NT
+//     natively; x @ w (B = [K][N]) is re-laid out once by a transpose pass.
+//   * v_mfma_f32_32x32x16_{f16,bf16}; block tile BM x BN x 64; four
 //     wavefronts in a 2x2 grid, each owning (BM/2) x (BN/2) of C in
-//     accumulator registers.
-//   * Global -> registers -> LDS, double buffered, one barrier per K step;
-//     LDS rows are 128 B (64 halfs) with the 16-byte chunk index XOR-swizzled
-//     by (row >> 1) & 7 so fragment reads and tile writes are conflict-free.
-//   * Tile order is XCD-aware: hardware dispatches workgroup i to XCD i % 8,
-//     so consecutive tiles of one XCD are remapped to a compact GROUP_M x N
-//     patch that shares A and B panels in that XCD's L2.
-//   * Epilogue fused: [round acc to f16/bf16] -> [+ bias[n]] -> [relu /
-//     tanh-GELU] -> store f32/f16/bf16 (the reference AMP graph
-//     CAST -> MATMUL(f16 out) -> ADD(bias, f32) realized in one pass).
-// f32 path: v_mfma_f32_32x32x2_f32 with k-major LDS tiles; NN and NT.
+//     accumulator registers (256 x 256 tile: 4 x 4 MFMA tiles per wave).
+//   * Global -> registers -> LDS, double buffered, one barrier per K step.
+//     LDS rows are 128 B (64 halves); the 16-byte chunk index is XOR-swizzled
+//     by the row so fragment reads and tile writes spread over all banks.
+//   * Loads are branch-free: FULL tiles load unconditionally; edge tiles
+//     clamp the address into the matrix and select zero outside it.
+//   * Tile order is XCD-aware: workgroup i runs on XCD i % 8, so the tiles
+//     one XCD receives are remapped to a compact patch of C that shares A
+//     and B panels in that XCD's L2.
+//   * Epilogue: the accumulators are staged through LDS (the operand buffers
+//     are free by then) and written back as row vectors, applying
+//     [round acc to f16/bf16] -> [+ bias[n] in f32] -> [relu / tanh-GELU]
+//     -> store f32/f16/bf16 (the reference AMP graph CAST -> MATMUL(f16 out)
+//     -> ADD(bias, f32) in one pass).  Staging keeps every accumulator index
+//     static, so the accumulators never leave registers.
+// f32 path, gemm32_kernel: v_mfma_f32_32x32x2_f32 with k-major LDS tiles
+// (NN and NT), the same staged epilogue.
 #include <algorithm>
 
 #include "common.cuh"
@@ -35,6 +41,9 @@ using namespace bgk;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf168 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+// Native 16-byte vector (HIP's uint4 is a union-based struct, which keeps
+// arrays of it from being promoted to registers).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
   const void* A;
@@ -46,11 +55,14 @@ struct GemmArgs {
   int64_t sa, sb, sc;  // batch strides (elements)
   int tiles_m, tiles_n;
   int round_dtype;  // 0 none, 1 f16, 2 bf16
-  int act;
-  int out_dtype;
+  int act;          // BG_ACT_*
+  int out_dtype;    // BG_F32 / BG_F16 / BG_BF16
+  int vec_store;    // C rows can take 4-element vector stores (ldc % 4, alignment)
 };
 
-// XCD-aware tile index -> (tile_m, tile_n).
+// XCD-aware tile index -> (tile_m, tile_n).  Workgroups are dispatched
+// round-robin over the 8 XCDs; the tiles of one XCD are made consecutive and
+// then walked in groups of G tile-rows so neighbours share A and B panels.
 __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   if (total % 8 == 0) {
@@ -66,60 +78,153 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
   tn = in_group / gsz;
 }
 
-__device__ __forceinline__ void epilogue_store(const GemmArgs& P, void* C, int64_t row,
-                                               int64_t col, float v) {
-  if (row >= P.M || col >= P.N) return;
+__device__ __forceinline__ float epilogue_value(const GemmArgs& P, float v, float bias) {
   if (P.round_dtype) v = round_through(v, P.round_dtype);
-  if (P.bias) v = v + P.bias[col];
-  if (P.act == 1) v = v > 0.f ? v : 0.f;
-  else if (P.act == 2) v = gelu_tanh_ref(v);
-  store_from_f32(C, P.out_dtype, row * P.ldc + col, v);
+  if (P.bias) v = v + bias;
+  if (P.act == BG_ACT_RELU) v = v > 0.f ? v : 0.f;
+  else if (P.act == BG_ACT_GELU_TANH) v = gelu_tanh_ref(v);
+  return v;
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_elem(char* p, float v) {
+  if constexpr (OUT == BG_F32) *reinterpret_cast<float*>(p) = v;
+  else if constexpr (OUT == BG_F16) *reinterpret_cast<uint16_t*>(p) = f32_to_f16_bits(v);
+  else *reinterpret_cast<uint16_t*>(p) = f32_to_bf16_bits(v);
+}
+
+// Epilogue in registers, stored straight to C, one 32x32 accumulator tile
+// (16 values per lane) at a time: [round to the 16-bit type] -> [+ bias[n]]
+// -> [relu] -> store, each stage behind one uniform branch per tile.
+// Scheduling fences between tiles keep the live set to one tile, so the
+// accumulators never spill.  tanh-GELU is applied by a separate elementwise
+// pass over C (launch_matmul): its exponentials and divide would swamp the
+// store stream.
+// 32x32 MFMA accumulator layout: lane l, register e holds row
+// 8*(e/4) + 4*(l/32) + e%4, column l%32, so each store instruction writes 32
+// consecutive columns of two rows.  Addresses are a uniform per-row base plus
+// one 32-bit per-lane offset; nothing in the loop waits on memory.
+template <int TM, int TN, bool FULL, int OUT>
+__device__ __forceinline__ void epilogue_tiles(const GemmArgs& P, char* C, float16v (&acc)[TM][TN],
+                                               int64_t row0, int64_t col0, const float (&bz)[TN]) {
+  constexpr int ES = OUT == BG_F32 ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int64_t cl = col0 + (lane & 31);
+  char* corner = C + (row0 * P.ldc + col0) * ES;
+  const uint32_t lane_off = uint32_t((4 * half * P.ldc + (lane & 31)) * ES);
+  const int64_t row_bytes = P.ldc * ES;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e];
+      if (P.round_dtype == 1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = round_through(v[e], 1);
+      } else if (P.round_dtype == 2) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = round_through(v[e], 2);
+      }
+      if (P.bias) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = v[e] + bz[j];
+      }
+      if (P.act == BG_ACT_RELU) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = v[e] > 0.f ? v[e] : 0.f;
+      }
+      const bool col_ok = FULL || cl + j * 32 < P.N;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rr = i * 32 + 8 * (e >> 2) + (e & 3);
+        if (FULL || (col_ok && row0 + rr + 4 * half < P.M))
+          store_elem<OUT>(corner + rr * row_bytes + lane_off + j * 32 * ES, v[e]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int TM, int TN, bool FULL>
+__device__ __forceinline__ void direct_epilogue(const GemmArgs& P, char* C, float16v (&acc)[TM][TN],
+                                                int64_t row0, int64_t col0) {
+  const int lane = threadIdx.x & 63;
+  const int64_t cl = col0 + (lane & 31);
+  float bz[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+    bz[j] = (P.bias && (FULL || cl + j * 32 < P.N)) ? P.bias[cl + j * 32] : 0.f;
+  if (P.out_dtype == BG_F32) epilogue_tiles<TM, TN, FULL, BG_F32>(P, C, acc, row0, col0, bz);
+  else if (P.out_dtype == BG_F16) epilogue_tiles<TM, TN, FULL, BG_F16>(P, C, acc, row0, col0, bz);
+  else epilogue_tiles<TM, TN, FULL, BG_BF16>(P, C, acc, row0, col0, bz);
 }
 
 // ---- 16-bit MFMA kernel ---------------------------------------------------------
 
 constexpr int BK16 = 64;
 
-template <int R, bool ALIGNED>
-__device__ __forceinline__ void load_tile16(const uint16_t* __restrict__ base, int64_t ld,
-                                            int64_t row0, int64_t rows, int64_t k0, int64_t K,
-                                            uint4 (&regs)[R / 32]) {
+// Physical 16-byte chunk of logical chunk c in LDS row r.
+template <int SWZ>
+__device__ __forceinline__ int swz(int r, int c) {
+  if constexpr (SWZ == 0) return c ^ (r & 7);
+  else return c ^ ((r >> 1) & 7);
+}
+
+// One thread's share of a R x 64 tile (R/32 chunks of 8 halves).  Rows are
+// r = i*32 + tid/8, chunk tid%8.  VEC: 16-byte loads (K % 8 == 0 and aligned
+// rows); otherwise element loads.  Out-of-matrix rows / columns read a
+// clamped in-bounds address and are replaced by zero.
+template <int R, bool FULL, bool VEC>
+__device__ __forceinline__ void load_tile16(const uint16_t* __restrict__ base, int64_t ld, int64_t row0,
+                                            int64_t rows, int64_t k0, int64_t K, u32x4 (&regs)[R / 32]) {
   const int tid = threadIdx.x;
+  const int c = tid & 7;
 #pragma unroll
   for (int i = 0; i < R / 32; ++i) {
-    const int v = i * 256 + tid;
-    const int r = v >> 3, c = v & 7;
-    const int64_t gr = row0 + r, gk = k0 + c * 8;
-    if constexpr (ALIGNED) {
-      if (gr < rows && gk < K) regs[i] = *reinterpret_cast<const uint4*>(base + gr * ld + gk);
-      else regs[i] = make_uint4(0, 0, 0, 0);
+    const int64_t gr = row0 + i * 32 + (tid >> 3);
+    const int64_t gk = k0 + c * 8;
+    if constexpr (FULL) {
+      regs[i] = *reinterpret_cast<const u32x4*>(base + gr * ld + gk);
+    } else if constexpr (VEC) {
+      const bool ok = gr < rows && gk < K;
+      const int64_t r = gr < rows ? gr : rows - 1;
+      const int64_t k = gk < K ? gk : K - 8;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(base + r * ld + k);
+      regs[i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
     } else {
+      const int64_t r = gr < rows ? gr : rows - 1;
       uint16_t e[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) e[j] = (gr < rows && gk + j < K) ? base[gr * ld + gk + j] : 0;
-      regs[i] = make_uint4(uint32_t(e[0]) | (uint32_t(e[1]) << 16), uint32_t(e[2]) | (uint32_t(e[3]) << 16),
-                           uint32_t(e[4]) | (uint32_t(e[5]) << 16), uint32_t(e[6]) | (uint32_t(e[7]) << 16));
+      for (int j = 0; j < 8; ++j) {
+        const int64_t k = gk + j < K ? gk + j : K - 1;
+        const uint16_t x = base[r * ld + k];
+        e[j] = (gr < rows && gk + j < K) ? x : uint16_t(0);
+      }
+      regs[i] = u32x4{uint32_t(e[0]) | (uint32_t(e[1]) << 16), uint32_t(e[2]) | (uint32_t(e[3]) << 16),
+                           uint32_t(e[4]) | (uint32_t(e[5]) << 16), uint32_t(e[6]) | (uint32_t(e[7]) << 16)};
     }
   }
 }
 
-template <int R>
-__device__ __forceinline__ void store_tile16(uint4* __restrict__ lds, const uint4 (&regs)[R / 32]) {
+template <int R, int SWZ>
+__device__ __forceinline__ void store_tile16(u32x4* __restrict__ lds, const u32x4 (&regs)[R / 32]) {
   const int tid = threadIdx.x;
+  const int c = tid & 7;
 #pragma unroll
   for (int i = 0; i < R / 32; ++i) {
-    const int v = i * 256 + tid;
-    const int r = v >> 3, c = v & 7;
-    lds[r * 8 + (c ^ ((r >> 1) & 7))] = regs[i];
+    const int r = i * 32 + (tid >> 3);
+    lds[r * 8 + swz<SWZ>(r, c)] = regs[i];
   }
 }
 
-template <int BM, int BN, bool BF16, bool ALIGNED>
-__global__ void __launch_bounds__(256, 1) gemm16_nt_kernel(GemmArgs P) {
+template <int BM, int BN, bool BF16, bool FULL, bool VEC, int SWZ>
+__global__ void __launch_bounds__(256) gemm16_kernel(GemmArgs P) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  __shared__ uint4 As[2][BM * 8];
-  __shared__ uint4 Bs[2][BN * 8];
+  constexpr int STAGE_BUF = (BM + BN) * 8;  // u32x4 per pipeline stage
+  __shared__ u32x4 smem[2 * STAGE_BUF];
 
   int tm_, tn_;
   tile_coords(blockIdx.x, P.tiles_m, P.tiles_n, tm_, tn_);
@@ -127,7 +232,7 @@ __global__ void __launch_bounds__(256, 1) gemm16_nt_kernel(GemmArgs P) {
   const int64_t batch = blockIdx.z;
   const uint16_t* A = static_cast<const uint16_t*>(P.A) + batch * P.sa;
   const uint16_t* B = static_cast<const uint16_t*>(P.B) + batch * P.sb;
-  char* C = static_cast<char*>(P.C) + batch * P.sc * (P.out_dtype == 0 ? 4 : 2);
+  char* C = static_cast<char*>(P.C) + batch * P.sc * (P.out_dtype == BG_F32 ? 4 : 2);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -141,35 +246,34 @@ __global__ void __launch_bounds__(256, 1) gemm16_nt_kernel(GemmArgs P) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  uint4 ra[BM / 32], rb[BN / 32];
+  u32x4 ra[BM / 32], rb[BN / 32];
   const int nk = int((P.K + BK16 - 1) / BK16);
-  load_tile16<BM, ALIGNED>(A, P.lda, m0, P.M, 0, P.K, ra);
-  load_tile16<BN, ALIGNED>(B, P.ldb, n0, P.N, 0, P.K, rb);
-  store_tile16<BM>(As[0], ra);
-  store_tile16<BN>(Bs[0], rb);
+  load_tile16<BM, FULL, VEC>(A, P.lda, m0, P.M, 0, P.K, ra);
+  load_tile16<BN, FULL, VEC>(B, P.ldb, n0, P.N, 0, P.K, rb);
+  store_tile16<BM, SWZ>(smem, ra);
+  store_tile16<BN, SWZ>(smem + BM * 8, rb);
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
+    const u32x4* as = smem + (kt & 1) * STAGE_BUF;
+    const u32x4* bs = as + BM * 8;
     if (kt + 1 < nk) {
-      load_tile16<BM, ALIGNED>(A, P.lda, m0, P.M, int64_t(kt + 1) * BK16, P.K, ra);
-      load_tile16<BN, ALIGNED>(B, P.ldb, n0, P.N, int64_t(kt + 1) * BK16, P.K, rb);
+      load_tile16<BM, FULL, VEC>(A, P.lda, m0, P.M, int64_t(kt + 1) * BK16, P.K, ra);
+      load_tile16<BN, FULL, VEC>(B, P.ldb, n0, P.N, int64_t(kt + 1) * BK16, P.K, rb);
     }
-    const uint4* as = As[cur];
-    const uint4* bs = Bs[cur];
 #pragma unroll
     for (int kk = 0; kk < BK16 / 16; ++kk) {
       const int c = kk * 2 + (lane >> 5);
-      uint4 af[TM], bf[TN];
+      u32x4 af[TM], bf[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = wm * WTM + i * 32 + (lane & 31);
-        af[i] = as[r * 8 + (c ^ ((r >> 1) & 7))];
+        af[i] = as[r * 8 + swz<SWZ>(r, c)];
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int r = wn * WTN + j * 32 + (lane & 31);
-        bf[j] = bs[r * 8 + (c ^ ((r >> 1) & 7))];
+        bf[j] = bs[r * 8 + swz<SWZ>(r, c)];
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -185,24 +289,242 @@ __global__ void __launch_bounds__(256, 1) gemm16_nt_kernel(GemmArgs P) {
         }
     }
     if (kt + 1 < nk) {
-      store_tile16<BM>(As[cur ^ 1], ra);
-      store_tile16<BN>(Bs[cur ^ 1], rb);
+      u32x4* nxt = smem + ((kt + 1) & 1) * STAGE_BUF;
+      store_tile16<BM, SWZ>(nxt, ra);
+      store_tile16<BN, SWZ>(nxt + BM * 8, rb);
     }
     __syncthreads();
   }
 
-  // C layout of a 32x32 MFMA tile: lane l, register e holds
-  // row 8*(e/4) + 4*(l/32) + e%4, column l%32.
+  direct_epilogue<TM, TN, FULL>(P, C, acc, m0 + wm * WTM, n0 + wn * WTN);
+}
+
+// ---- 16-bit MFMA kernel, direct-to-LDS multi-stage pipeline -------------------------
+//
+// Same 2x2-wavefront tiling as gemm16_kernel, built for latency hiding:
+//   * Operand tiles stream from HBM straight into LDS with
+//     buffer_load_dwordx4 ... lds (no VGPR round trip, no ds_write).  Each
+//     wavefront instruction fills 1 KB of LDS, lane L writing 16-byte unit
+//     L, so the lane fetches whichever (row, k-chunk) the swizzled layout
+//     puts in that unit.
+//   * Lanes outside the matrix (rows >= M/N or k >= K) get an offset past
+//     the buffer's num_records and the hardware returns zeros: edge tiles and
+//     the pipeline's run-out stages need no branches.
+//   * S stages of BK-deep tiles form a ring in LDS; loads run S-1 stages
+//     ahead of the MFMAs.  Each step waits only for the loads of the next
+//     stage (partial vmcnt), so S-2 stages stay in flight across the barrier.
+//   * The loop is rotated: the last 16-wide k sub-step's MFMAs are issued
+//     after the barrier, behind the next stage's first fragment reads and
+//     loads, so neither LDS latency nor the barrier idles the matrix cores.
+//     Operand fragments are double buffered in registers across sub-steps.
+//   * LDS layout: the tile is viewed as 128-byte lines (RPL = 128 / (2*BK)
+//     rows per line); a line's eight 16-byte units are XOR-permuted by the
+//     line index so that ds_read_b128 -- which serves the even lanes of a
+//     16-lane group in one cycle and the odd lanes in the next -- reads eight
+//     distinct units per cycle (measured: zero SQ_LDS_BANK_CONFLICT).
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr uint32_t kOob = 0x80000000u;  // >= num_records: load returns 0
+
+template <int BK>
+struct LdsLayout {
+  static constexpr int CPR = BK / 8;    // 16-byte chunks per row
+  static constexpr int RPL = 8 / CPR;   // rows per 128-byte line
+  __device__ static __forceinline__ int perm(int line) {
+    return RPL == 1 ? ((line >> 1) & 7) : (line & 7);
+  }
+  // 16-byte unit holding (row r, chunk c).
+  __device__ static __forceinline__ int unit(int r, int c) {
+    const int line = r / RPL;
+    return line * 8 + ((((r % RPL) * CPR) + c) ^ perm(line));
+  }
+};
+
+// s_waitcnt that waits for vmcnt <= n only (expcnt / lgkmcnt left open).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Same, and also lgkmcnt == 0 (this wavefront's LDS reads have completed).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// Per-lane operand offsets of one R x BK tile, fixed for the whole K loop:
+// instruction i of wavefront w fills 1 KB block blk = i*4 + w; lane L writes
+// unit blk*64 + L and fetches the (row, chunk) the layout keeps there.  Rows
+// outside the matrix get kOob (the load returns zeros).  The k offset of a
+// stage is added through the scalar soffset, so issuing a stage costs one
+// instruction per 1 KB block.
+template <int R, int BK>
+struct TileLoads {
+  static constexpr int INSTR = R * BK * 2 / 1024;  // wavefront instructions per tile
+  static_assert(INSTR % 4 == 0, "tile must split over four wavefronts");
+  uint32_t voff[INSTR / 4];
+  uint32_t chunk_k[INSTR / 4];  // k offset of the lane's chunk (elements), for K tails
+
+  __device__ __forceinline__ void init(int w, int64_t ld, int64_t row0, int64_t rows) {
+    using L = LdsLayout<BK>;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < INSTR / 4; ++i) {
+      const int u = (i * 4 + w) * 64 + lane;
+      const int line = u >> 3;
+      const int sl = (u & 7) ^ L::perm(line);
+      const int r = line * L::RPL + sl / L::CPR;
+      const int c = sl % L::CPR;
+      const int64_t gr = row0 + r;
+      chunk_k[i] = uint32_t(c * 8);
+      voff[i] = gr < rows ? uint32_t((gr * ld + c * 8) * 2) : kOob;
+    }
+  }
+
+  // KTAIL: lanes whose chunk lies at or past K load zeros.
+  template <bool KTAIL>
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, char* lds_tile, int w, int64_t k0,
+                                        int64_t K) const {
+#pragma unroll
+    for (int i = 0; i < INSTR / 4; ++i) {
+      uint32_t off = voff[i];
+      if constexpr (KTAIL) off = (k0 + chunk_k[i] < K) ? off : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(lds_tile + (i * 4 + w) * 1024), 16, off,
+                                               uint32_t(k0 * 2), 0, 0);
+    }
+  }
+};
+
+// Scheduling pattern for one sub-step region: MFMA q is followed by one
+// fragment read (q < NDS) and LPM operand loads (while loads remain).
+template <int Q, int NMF, int NDS, int NVM, int LPM>
+__device__ __forceinline__ void sched_pattern() {
+  if constexpr (Q < NMF) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (Q < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if constexpr (Q * LPM < NVM)
+      __builtin_amdgcn_sched_group_barrier(0x020, (NVM - Q * LPM) < LPM ? (NVM - Q * LPM) : LPM, 0);
+    sched_pattern<Q + 1, NMF, NDS, NVM, LPM>();
+  }
+}
+
+template <int BM, int BN, int BK, int S, bool BF16, bool FULL, bool KTAIL>
+__global__ void __launch_bounds__(256) gemm16_lds_kernel(GemmArgs P, uint32_t a_bytes, uint32_t b_bytes) {
+  using L = LdsLayout<BK>;
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int KK = BK / 16;                         // 16-wide sub-steps per stage
+  constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
+  constexpr int NLD = (BM + BN) * BK * 2 / 1024 / 4;  // loads per wavefront per stage
+  static_assert(KK % 2 == 0, "fragment double buffering needs an even sub-step count");
+  static_assert(NLD * (S - 1) < 64, "vmcnt range");
+  __shared__ u32x4 smem[S * STAGE_BYTES / 16];
+
+  int tm_, tn_;
+  tile_coords(blockIdx.x, P.tiles_m, P.tiles_n, tm_, tn_);
+  const int64_t m0 = int64_t(tm_) * BM, n0 = int64_t(tn_) * BN;
+  const int64_t batch = blockIdx.z;
+  const uint16_t* A = static_cast<const uint16_t*>(P.A) + batch * P.sa;
+  const uint16_t* B = static_cast<const uint16_t*>(P.B) + batch * P.sb;
+  char* C = static_cast<char*>(P.C) + batch * P.sc * (P.out_dtype == BG_F32 ? 4 : 2);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, int(a_bytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, int(b_bytes), 0x00020000);
+  // Zero-length descriptors: every load of a run-out stage returns zeros.
+  const __amdgpu_buffer_rsrc_t ra0 = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb0 = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, 0, 0x00020000);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  TileLoads<BM, BK> la;
+  TileLoads<BN, BK> lb;
+  la.init(wave, P.lda, m0, P.M);
+  lb.init(wave, P.ldb, n0, P.N);
+
+  float16v acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int64_t col = n0 + wn * WTN + j * 32 + (lane & 31);
-        epilogue_store(P, C, row, col, acc[i][j][e]);
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  char* sbytes = reinterpret_cast<char*>(smem);
+  const int nk = int((P.K + BK - 1) / BK);
+  auto issue_stage = [&](int t) {
+    char* st = sbytes + (t % S) * STAGE_BYTES;
+    const bool real = t < nk;
+    const int64_t k0 = real ? int64_t(t) * BK : 0;
+    la.template issue<KTAIL>(real ? ra : ra0, st, wave, k0, P.K);
+    lb.template issue<KTAIL>(real ? rb : rb0, st + BM * BK * 2, wave, k0, P.K);
+  };
+  // Fragment reads of sub-step kk of stage t: A rows / B^T rows, 8 halves.
+  auto read_frags = [&](int t, int kk, u32x4 (&fa)[TM], u32x4 (&fb)[TN]) {
+    const u32x4* as = smem + (t % S) * (STAGE_BYTES / 16);
+    const u32x4* bs = as + BM * BK * 2 / 16;
+    const int c = kk * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[i] = as[L::unit(wm * WTM + i * 32 + (lane & 31), c)];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[j] = bs[L::unit(wn * WTN + j * 32 + (lane & 31), c)];
+  };
+  auto mfmas = [&](const u32x4 (&fa)[TM], const u32x4 (&fb)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (BF16)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, fa[i]),
+                                                              __builtin_bit_cast(bf168, fb[j]), acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, fa[i]),
+                                                             __builtin_bit_cast(half8, fb[j]), acc[i][j], 0, 0, 0);
       }
+  };
+  // One fragment read after each of the first TM+TN MFMAs of a sub-step.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int q = 0; q < TM + TN; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+  };
+
+#pragma unroll
+  for (int t = 0; t < S; ++t) issue_stage(t);
+  wait_vmcnt<NLD * (S - 1)>();
+  __syncthreads();
+
+  u32x4 fa[2][TM], fb[2][TN];
+  read_frags(0, 0, fa[0], fb[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int t = 0; t < nk; ++t) {
+#pragma unroll
+    for (int kk = 0; kk < KK - 1; ++kk) {
+      read_frags(t, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      mfmas(fa[kk & 1], fb[kk & 1]);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // End of stage t: its last fragments are in registers.  Wait for stage
+    // t+1's loads, let every wavefront finish reading slot t % S, refill it
+    // with stage t+S, then run the last sub-step behind the next reads.
+    wait_vmcnt_lgkm0<NLD * (S - 2)>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_stage(t + S);
+    read_frags(t + 1, 0, fa[0], fb[0]);
+    mfmas(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+    // MFMA, fragment read and stage load interleaved.
+    sched_pattern<0, TM * TN, TM + TN, NLD, (NLD + TM * TN - 1) / (TM * TN)>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  direct_epilogue<TM, TN, FULL>(P, C, acc, m0 + wm * WTM, n0 + wn * WTN);
 }
 
 // ---- f32 MFMA kernel ----------------------------------------------------------------
@@ -210,12 +532,13 @@ __global__ void __launch_bounds__(256, 1) gemm16_nt_kernel(GemmArgs P) {
 constexpr int BK32 = 16;
 
 template <int BM, int BN, bool TRANS_B, bool ALIGNED>
-__global__ void __launch_bounds__(256, 1) gemm32_kernel(GemmArgs P) {
+__global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int LA = BM + 32, LB = BN + 32;  // k-major rows, padded (row % 64 == 32 banks)
-  __shared__ float As[2][BK32][LA];
-  __shared__ float Bs[2][BK32][LB];
+  constexpr int LA = BM + 32, LB = BN + 32;  // k-major rows, padded
+  constexpr int A_FLOATS = BK32 * LA, B_FLOATS = BK32 * LB;
+  constexpr int STAGE_FLOATS = A_FLOATS + B_FLOATS;
+  __shared__ float smem[2 * STAGE_FLOATS];
 
   int tm_, tn_;
   tile_coords(blockIdx.x, P.tiles_m, P.tiles_n, tm_, tn_);
@@ -223,7 +546,7 @@ __global__ void __launch_bounds__(256, 1) gemm32_kernel(GemmArgs P) {
   const int64_t batch = blockIdx.z;
   const float* A = static_cast<const float*>(P.A) + batch * P.sa;
   const float* B = static_cast<const float*>(P.B) + batch * P.sb;
-  char* C = static_cast<char*>(P.C) + batch * P.sc * (P.out_dtype == 0 ? 4 : 2);
+  char* C = static_cast<char*>(P.C) + batch * P.sc * (P.out_dtype == BG_F32 ? 4 : 2);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -243,32 +566,48 @@ __global__ void __launch_bounds__(256, 1) gemm32_kernel(GemmArgs P) {
   float4 ra[NA], rb[NB];
   auto load_rowk = [&](const float* base, int64_t ld, int64_t row0, int64_t rows, int64_t k0,
                        float4* regs, int n) {
+#pragma unroll
     for (int i = 0; i < n; ++i) {
       const int v = i * 256 + tid;
       const int r = v >> 2, c = (v & 3) * 4;
       const int64_t gr = row0 + r, gk = k0 + c;
+      const int64_t rr = gr < rows ? gr : rows - 1;
       if (ALIGNED) {
-        regs[i] = (gr < rows && gk < P.K) ? *reinterpret_cast<const float4*>(base + gr * ld + gk)
-                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int64_t kc = gk < P.K ? gk : P.K - 4;
+        const float4 x = *reinterpret_cast<const float4*>(base + rr * ld + kc);
+        regs[i] = (gr < rows && gk < P.K) ? x : make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
         float e[4];
-        for (int j = 0; j < 4; ++j) e[j] = (gr < rows && gk + j < P.K) ? base[gr * ld + gk + j] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t kc = gk + j < P.K ? gk + j : P.K - 1;
+          const float x = base[rr * ld + kc];
+          e[j] = (gr < rows && gk + j < P.K) ? x : 0.f;
+        }
         regs[i] = make_float4(e[0], e[1], e[2], e[3]);
       }
     }
   };
   // B in [K][N] layout: BK x BN tile loaded along N.
   auto load_kn = [&](int64_t k0, float4* regs) {
+#pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int v = i * 256 + tid;
       const int kr = v / (BN / 4), c = (v % (BN / 4)) * 4;
       const int64_t gk = k0 + kr, gn = n0 + c;
+      const int64_t kc = gk < P.K ? gk : P.K - 1;
       if (ALIGNED) {
-        regs[i] = (gk < P.K && gn < P.N) ? *reinterpret_cast<const float4*>(B + gk * P.ldb + gn)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int64_t nc = gn < P.N ? gn : P.N - 4;
+        const float4 x = *reinterpret_cast<const float4*>(B + kc * P.ldb + nc);
+        regs[i] = (gk < P.K && gn < P.N) ? x : make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
         float e[4];
-        for (int j = 0; j < 4; ++j) e[j] = (gk < P.K && gn + j < P.N) ? B[gk * P.ldb + gn + j] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t nc = gn + j < P.N ? gn + j : P.N - 1;
+          const float x = B[kc * P.ldb + nc];
+          e[j] = (gk < P.K && gn + j < P.N) ? x : 0.f;
+        }
         regs[i] = make_float4(e[0], e[1], e[2], e[3]);
       }
     }
@@ -279,27 +618,29 @@ __global__ void __launch_bounds__(256, 1) gemm32_kernel(GemmArgs P) {
     else load_kn(k0, rb);
   };
   auto commit = [&](int buf) {
+    float* As = smem + buf * STAGE_FLOATS;
+    float* Bs = As + A_FLOATS;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int v = i * 256 + tid;
       const int r = v >> 2, c = (v & 3) * 4;
-      As[buf][c + 0][r] = ra[i].x;
-      As[buf][c + 1][r] = ra[i].y;
-      As[buf][c + 2][r] = ra[i].z;
-      As[buf][c + 3][r] = ra[i].w;
+      As[(c + 0) * LA + r] = ra[i].x;
+      As[(c + 1) * LA + r] = ra[i].y;
+      As[(c + 2) * LA + r] = ra[i].z;
+      As[(c + 3) * LA + r] = ra[i].w;
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int v = i * 256 + tid;
       if constexpr (TRANS_B) {
         const int r = v >> 2, c = (v & 3) * 4;
-        Bs[buf][c + 0][r] = rb[i].x;
-        Bs[buf][c + 1][r] = rb[i].y;
-        Bs[buf][c + 2][r] = rb[i].z;
-        Bs[buf][c + 3][r] = rb[i].w;
+        Bs[(c + 0) * LB + r] = rb[i].x;
+        Bs[(c + 1) * LB + r] = rb[i].y;
+        Bs[(c + 2) * LB + r] = rb[i].z;
+        Bs[(c + 3) * LB + r] = rb[i].w;
       } else {
         const int kr = v / (BN / 4), c = (v % (BN / 4)) * 4;
-        *reinterpret_cast<float4*>(&Bs[buf][kr][c]) = rb[i];
+        *reinterpret_cast<float4*>(&Bs[kr * LB + c]) = rb[i];
       }
     }
   };
@@ -309,56 +650,63 @@ __global__ void __launch_bounds__(256, 1) gemm32_kernel(GemmArgs P) {
   commit(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
+    const float* As = smem + (kt & 1) * STAGE_FLOATS;
+    const float* Bs = As + A_FLOATS;
     if (kt + 1 < nk) fetch(int64_t(kt + 1) * BK32);
 #pragma unroll
     for (int s = 0; s < BK32 / 2; ++s) {
       const int k = 2 * s + (lane >> 5);
       float af[TM], bf[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = As[cur][k][wm * WTM + i * 32 + (lane & 31)];
+      for (int i = 0; i < TM; ++i) af[i] = As[k * LA + wm * WTM + i * 32 + (lane & 31)];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = Bs[cur][k][wn * WTN + j * 32 + (lane & 31)];
+      for (int j = 0; j < TN; ++j) bf[j] = Bs[k * LB + wn * WTN + j * 32 + (lane & 31)];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) commit(cur ^ 1);
+    if (kt + 1 < nk) commit((kt + 1) & 1);
     __syncthreads();
   }
 
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int64_t col = n0 + wn * WTN + j * 32 + (lane & 31);
-        epilogue_store(P, C, row, col, acc[i][j][e]);
-      }
+  direct_epilogue<TM, TN, false>(P, C, acc, m0 + wm * WTM, n0 + wn * WTN);
 }
 
-template <int BM, int BN, bool BF16>
-void launch16(bg_ctx* ctx, const GemmArgs& P, int64_t batch, bool aligned) {
+template <int BM, int BN, bool BF16, int SWZ>
+void launch16(bg_ctx* ctx, const GemmArgs& P, int64_t batch, bool full, bool vec) {
   dim3 grid(unsigned(P.tiles_m * P.tiles_n), 1, unsigned(batch));
-  if (aligned)
-    hipLaunchKernelGGL((gemm16_nt_kernel<BM, BN, BF16, true>), grid, dim3(256), 0, ctx->stream, P);
+  if (full)
+    bg::dispatch(ctx, gemm16_kernel<BM, BN, BF16, true, true, SWZ>, grid, dim3(256), 0, P);
+  else if (vec)
+    bg::dispatch(ctx, gemm16_kernel<BM, BN, BF16, false, true, SWZ>, grid, dim3(256), 0, P);
   else
-    hipLaunchKernelGGL((gemm16_nt_kernel<BM, BN, BF16, false>), grid, dim3(256), 0, ctx->stream, P);
+    bg::dispatch(ctx, gemm16_kernel<BM, BN, BF16, false, false, SWZ>, grid, dim3(256), 0, P);
+}
+
+template <int BM, int BN, int BK, int S, bool BF16>
+void launch16_lds(bg_ctx* ctx, const GemmArgs& P, int64_t batch, uint32_t a_bytes, uint32_t b_bytes) {
+  dim3 grid(unsigned(P.tiles_m * P.tiles_n), 1, unsigned(batch));
+  const bool full = P.M % BM == 0 && P.N % BN == 0;
+  const bool ktail = P.K % BK != 0;
+  if (full && !ktail)
+    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, true, false>, grid, dim3(256), 0, P, a_bytes, b_bytes);
+  else if (!ktail)
+    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, false, false>, grid, dim3(256), 0, P, a_bytes, b_bytes);
+  else
+    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, false, true>, grid, dim3(256), 0, P, a_bytes, b_bytes);
 }
 
 template <int BM, int BN>
 void launch32(bg_ctx* ctx, const GemmArgs& P, int64_t batch, bool trans_b, bool aligned) {
   dim3 grid(unsigned(P.tiles_m * P.tiles_n), 1, unsigned(batch));
   if (trans_b) {
-    if (aligned) hipLaunchKernelGGL((gemm32_kernel<BM, BN, true, true>), grid, dim3(256), 0, ctx->stream, P);
-    else hipLaunchKernelGGL((gemm32_kernel<BM, BN, true, false>), grid, dim3(256), 0, ctx->stream, P);
+    if (aligned) bg::dispatch(ctx, gemm32_kernel<BM, BN, true, true>, grid, dim3(256), 0, P);
+    else bg::dispatch(ctx, gemm32_kernel<BM, BN, true, false>, grid, dim3(256), 0, P);
   } else {
-    if (aligned) hipLaunchKernelGGL((gemm32_kernel<BM, BN, false, true>), grid, dim3(256), 0, ctx->stream, P);
-    else hipLaunchKernelGGL((gemm32_kernel<BM, BN, false, false>), grid, dim3(256), 0, ctx->stream, P);
+    if (aligned) bg::dispatch(ctx, gemm32_kernel<BM, BN, false, true>, grid, dim3(256), 0, P);
+    else bg::dispatch(ctx, gemm32_kernel<BM, BN, false, false>, grid, dim3(256), 0, P);
   }
 }
 
@@ -368,43 +716,43 @@ bool aligned_to(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p)
 
 namespace bg {
 
-void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
-                   const Record* bias, Record& out) {
-  if (d.batch > 65535) fail(BG_E_UNSUPPORTED, "matmul: batch > 65535");
+// GEMM launch with C described by (c, ldc, stride_c, out_dtype, act).
+static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
+                     const Record* bias, void* c, int64_t ldc, int64_t stride_c, int out_dtype, int act) {
   const int64_t es = dtype_size(d.in_dtype);
   GemmArgs P{};
   P.A = a.ptr() + d.offset_a * es;
   P.B = b.ptr() + d.offset_b * es;
   P.bias = bias ? reinterpret_cast<const float*>(bias->ptr()) : nullptr;
-  P.C = out.ptr();
+  P.C = c;
   P.M = d.m;
   P.N = d.n;
   P.K = d.k;
   P.lda = d.lda;
   P.ldb = d.ldb;
-  P.ldc = d.ldc;
+  P.ldc = ldc;
   P.sa = d.stride_a;
   P.sb = d.stride_b;
-  P.sc = d.stride_c;
+  P.sc = stride_c;
   P.round_dtype = d.round_f16 ? (d.in_dtype == BG_BF16 ? 2 : 1) : 0;
-  P.act = d.act;
-  P.out_dtype = d.out_dtype;
+  P.act = act;
+  P.out_dtype = out_dtype;
+  P.vec_store = (ldc % 4 == 0 && stride_c % 4 == 0 && aligned_to(P.C, 16) &&
+                 (!P.bias || aligned_to(P.bias, 16)))
+                    ? 1
+                    : 0;
   const int64_t flops = 2 * d.batch * d.m * d.n * d.k;
   const int64_t bytes = d.batch * (d.m * d.k + d.n * d.k) * es +
-                        d.batch * d.m * d.n * dtype_size(d.out_dtype);
+                        d.batch * d.m * d.n * dtype_size(out_dtype);
 
   if (d.in_dtype == BG_F32) {
-    const bool big = (d.m >= 2048 && d.n >= 2048);
-    const int BM = 128, BN = 128;
-    (void)big;
-    P.tiles_m = int((d.m + BM - 1) / BM);
-    P.tiles_n = int((d.n + BN - 1) / BN);
+    P.tiles_m = int((d.m + 127) / 128);
+    P.tiles_n = int((d.n + 127) / 128);
     const bool aligned = aligned_to(P.A, 16) && aligned_to(P.B, 16) && d.lda % 4 == 0 &&
                          d.ldb % 4 == 0 && d.k % 4 == 0 && (d.trans_b || d.n % 4 == 0) &&
                          d.stride_a % 4 == 0 && d.stride_b % 4 == 0;
     Profile prof(ctx, "gemm_f32", bytes, flops);
     launch32<128, 128>(ctx, P, d.batch, d.trans_b != 0, aligned);
-    hip_check(hipGetLastError(), "gemm_f32 launch");
     return;
   }
 
@@ -428,24 +776,64 @@ void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const 
     P.ldb = d.k;
     P.sb = d.stride_b == 0 ? 0 : d.n * d.k;
   }
-  const bool aligned = aligned_to(P.A, 16) && aligned_to(P.B, 16) && d.k % 8 == 0 &&
-                       P.lda % 8 == 0 && P.ldb % 8 == 0 && P.sa % 8 == 0 && P.sb % 8 == 0;
+  const bool vec = aligned_to(P.A, 16) && aligned_to(P.B, 16) && d.k % 8 == 0 && P.lda % 8 == 0 &&
+                   P.ldb % 8 == 0 && P.sa % 8 == 0 && P.sb % 8 == 0;
   const bool bf = d.in_dtype == BG_BF16;
   // Large problems: 256x256 tiles (one tile per CU at 4096^2); otherwise 128x128.
   const int64_t t256 = ((d.m + 255) / 256) * ((d.n + 255) / 256) * d.batch;
+  const bool big = t256 >= 192;
+  const int BMN = big ? 256 : 128;
+  P.tiles_m = int((d.m + BMN - 1) / BMN);
+  P.tiles_n = int((d.n + BMN - 1) / BMN);
+  const bool full = vec && d.m % BMN == 0 && d.n % BMN == 0 && d.k % BK16 == 0 && P.vec_store;
   Profile prof(ctx, bf ? "gemm_bf16" : "gemm_f16", bytes, flops);
-  if (t256 >= 192) {
-    P.tiles_m = int((d.m + 255) / 256);
-    P.tiles_n = int((d.n + 255) / 256);
-    if (bf) launch16<256, 256, true>(ctx, P, d.batch, aligned);
-    else launch16<256, 256, false>(ctx, P, d.batch, aligned);
-  } else {
-    P.tiles_m = int((d.m + 127) / 128);
-    P.tiles_n = int((d.n + 127) / 128);
-    if (bf) launch16<128, 128, true>(ctx, P, d.batch, aligned);
-    else launch16<128, 128, false>(ctx, P, d.batch, aligned);
+  // Direct-to-LDS path: operand byte ranges addressable with 32-bit offsets.
+  const int64_t a_span = ((d.m - 1) * P.lda + d.k) * es;
+  const int64_t b_span = ((d.n - 1) * P.ldb + d.k) * es;
+  const bool lds_ok = vec && a_span < (int64_t(1) << 31) && b_span < (int64_t(1) << 31);
+  if (lds_ok) {
+    const uint32_t ab = uint32_t(a_span), bb = uint32_t(b_span);
+    // BK = 64 with two LDS stages measured faster than BK = 32 with four
+    // (4096^3 f16: 132 vs 135 us) and keeps 128-byte LDS rows, whose
+    // swizzle is bank-conflict free.
+    if (big) {
+      if (bf) launch16_lds<256, 256, 64, 2, true>(ctx, P, d.batch, ab, bb);
+      else launch16_lds<256, 256, 64, 2, false>(ctx, P, d.batch, ab, bb);
+    } else {
+      if (bf) launch16_lds<128, 128, 64, 2, true>(ctx, P, d.batch, ab, bb);
+      else launch16_lds<128, 128, 64, 2, false>(ctx, P, d.batch, ab, bb);
+    }
+    return;
   }
-  hip_check(hipGetLastError(), "gemm16 launch");
+  if (big) {
+    if (bf) launch16<256, 256, true, 0>(ctx, P, d.batch, full, vec);
+    else launch16<256, 256, false, 0>(ctx, P, d.batch, full, vec);
+  } else {
+    if (bf) launch16<128, 128, true, 0>(ctx, P, d.batch, full, vec);
+    else launch16<128, 128, false, 0>(ctx, P, d.batch, full, vec);
+  }
+}
+
+void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
+                   const Record* bias, Record& out) {
+  if (d.batch > 65535) fail(BG_E_UNSUPPORTED, "matmul: batch > 65535");
+  if (d.act != BG_ACT_GELU_TANH) {
+    run_gemm(ctx, d, a, b, bias, out.ptr(), d.ldc, d.stride_c, d.out_dtype, d.act);
+    return;
+  }
+  // GELU follows the (rounded, biased) product in f32, as the reference
+  // graph evaluates it: the GEMM leaves f32 in C (or in scratch when C is
+  // 16-bit), then one elementwise pass applies GELU and stores C's dtype.
+  float* f = reinterpret_cast<float*>(out.ptr());
+  int64_t ldf = d.ldc, sf = d.stride_c;
+  if (d.out_dtype != BG_F32) {
+    f = static_cast<float*>(scratch(ctx, size_t(d.batch * d.m * d.n * 4), 1));
+    ldf = d.n;
+    sf = d.m * d.n;
+  }
+  run_gemm(ctx, d, a, b, bias, f, ldf, sf, BG_F32, BG_ACT_NONE);
+  Profile prof(ctx, "gemm_gelu", d.batch * d.m * d.n * (4 + dtype_size(d.out_dtype)), 0);
+  launch_gelu_rows(ctx, f, ldf, sf, out.ptr(), d.ldc, d.stride_c, d.out_dtype, d.batch, d.m, d.n);
 }
 
 }  // namespace bg

@@ -331,6 +331,21 @@ int grid1(int64_t n, int per) {
   return int(std::max<int64_t>(1, std::min<int64_t>((n + per - 1) / per, 256 * 64)));
 }
 
+// tanh-GELU over the rows of an f32 matrix (the GEMM's activation stage):
+// dst[b][r][c] = gelu(src[b][r][c]) stored in dst_dtype.  One block per row
+// chunk; four consecutive columns per lane when the rows allow it.
+__global__ void __launch_bounds__(256) gelu_rows_kernel(const float* __restrict__ src, int64_t ld_src,
+                                                        int64_t stride_src, void* __restrict__ dst,
+                                                        int64_t ld_dst, int64_t stride_dst, int dd,
+                                                        int64_t rows, int64_t cols, int64_t total_rows) {
+  for (int64_t rr = blockIdx.x; rr < total_rows; rr += gridDim.x) {
+    const int64_t b = rr / rows, r = rr - b * rows;
+    const float* s = src + b * stride_src + r * ld_src;
+    const int64_t o = b * stride_dst + r * ld_dst;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) store_from_f32(dst, dd, o + c, gelu_tanh_ref(s[c]));
+  }
+}
+
 }  // namespace
 
 namespace bg {
@@ -340,10 +355,10 @@ void launch_cast(bg_ctx* ctx, const void* src, int sd, void* dst, int dd, int64_
   const bool aligned = reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(dst) % 16 == 0;
   if (aligned) {
-    hipLaunchKernelGGL(cast_kernel, dim3(grid1(n / 4 + 1, 256)), dim3(256), 0, ctx->stream,
+    bg::dispatch(ctx, cast_kernel, dim3(grid1(n / 4 + 1, 256)), dim3(256), 0,
                        src, sd, dst, dd, n);
   } else {
-    hipLaunchKernelGGL(cast_scalar_kernel, dim3(grid1(n, 256)), dim3(256), 0, ctx->stream, src,
+    bg::dispatch(ctx, cast_scalar_kernel, dim3(grid1(n, 256)), dim3(256), 0, src,
                        sd, dst, dd, n);
   }
   hip_check(hipGetLastError(), "cast launch");
@@ -354,7 +369,7 @@ void launch_cast_transpose(bg_ctx* ctx, const void* src, int sd, void* dst, int 
   if (rows <= 0 || cols <= 0 || batch <= 0) return;
   if (batch > 65535) fail(BG_E_UNSUPPORTED, "cast_transpose: batch > 65535");
   dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64), unsigned(batch));
-  hipLaunchKernelGGL(cast_transpose_kernel, grid, dim3(256), 0, ctx->stream, src, sd, dst, dd,
+  bg::dispatch(ctx, cast_transpose_kernel, grid, dim3(256), 0, src, sd, dst, dd,
                      rows, cols);
   hip_check(hipGetLastError(), "cast_transpose launch");
 }
@@ -377,17 +392,27 @@ void launch_copy_strided(bg_ctx* ctx, const void* src, int64_t es, void* dst,
   }
   const int g = grid1(A.n, 256);
   switch (es) {
-    case 1: hipLaunchKernelGGL(copy_strided_kernel<uint8_t>, dim3(g), dim3(256), 0, ctx->stream,
+    case 1: bg::dispatch(ctx, copy_strided_kernel<uint8_t>, dim3(g), dim3(256), 0,
                                static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), A); break;
-    case 2: hipLaunchKernelGGL(copy_strided_kernel<uint16_t>, dim3(g), dim3(256), 0, ctx->stream,
+    case 2: bg::dispatch(ctx, copy_strided_kernel<uint16_t>, dim3(g), dim3(256), 0,
                                static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), A); break;
-    case 4: hipLaunchKernelGGL(copy_strided_kernel<uint32_t>, dim3(g), dim3(256), 0, ctx->stream,
+    case 4: bg::dispatch(ctx, copy_strided_kernel<uint32_t>, dim3(g), dim3(256), 0,
                                static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), A); break;
-    case 8: hipLaunchKernelGGL(copy_strided_kernel<uint64_t>, dim3(g), dim3(256), 0, ctx->stream,
+    case 8: bg::dispatch(ctx, copy_strided_kernel<uint64_t>, dim3(g), dim3(256), 0,
                                static_cast<const uint64_t*>(src), static_cast<uint64_t*>(dst), A); break;
     default: fail(BG_E_DTYPE, "copy_strided: unsupported element size");
   }
   hip_check(hipGetLastError(), "copy_strided launch");
+}
+
+void launch_gelu_rows(bg_ctx* ctx, const float* src, int64_t ld_src, int64_t stride_src, void* dst,
+                      int64_t ld_dst, int64_t stride_dst, int dst_dtype, int64_t batch, int64_t rows,
+                      int64_t cols) {
+  const int64_t total = batch * rows;
+  if (total == 0 || cols == 0) return;
+  const unsigned grid = unsigned(std::min<int64_t>(total, 65536));
+  bg::dispatch(ctx, gelu_rows_kernel, dim3(grid), dim3(256), 0, src, ld_src, stride_src, dst, ld_dst,
+               stride_dst, dst_dtype, rows, cols, total);
 }
 
 void launch_layer_norm(bg_ctx* ctx, const void* x, int xd, const float* w, const float* b,
@@ -395,16 +420,16 @@ void launch_layer_norm(bg_ctx* ctx, const void* x, int xd, const float* w, const
   if (rows == 0) return;
   const dim3 grid(unsigned((rows + 3) / 4));
   if (cols <= 256) {
-    hipLaunchKernelGGL(layer_norm_kernel<4>, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y, yd,
+    bg::dispatch(ctx, layer_norm_kernel<4>, grid, dim3(256), 0, x, xd, w, b, y, yd,
                        rows, cols, eps);
   } else if (cols <= 1024) {
-    hipLaunchKernelGGL(layer_norm_kernel<16>, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y, yd,
+    bg::dispatch(ctx, layer_norm_kernel<16>, grid, dim3(256), 0, x, xd, w, b, y, yd,
                        rows, cols, eps);
   } else if (cols <= 2048) {
-    hipLaunchKernelGGL(layer_norm_kernel<32>, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y, yd,
+    bg::dispatch(ctx, layer_norm_kernel<32>, grid, dim3(256), 0, x, xd, w, b, y, yd,
                        rows, cols, eps);
   } else {
-    hipLaunchKernelGGL(layer_norm_wide_kernel, grid, dim3(256), 0, ctx->stream, x, xd, w, b, y,
+    bg::dispatch(ctx, layer_norm_wide_kernel, grid, dim3(256), 0, x, xd, w, b, y,
                        yd, rows, cols, eps);
   }
   hip_check(hipGetLastError(), "layer_norm launch");
@@ -429,8 +454,7 @@ void launch_attention_generic(bg_ctx* ctx, const bg_attention_desc& d, const voi
   A.round_scores = d.round_scores;
   A.two_pass = two_pass ? 1 : 0;
   const int64_t rows = d.batch * d.heads * d.sq;
-  hipLaunchKernelGGL(attention_generic_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0,
-                     ctx->stream, A);
+  bg::dispatch(ctx, attention_generic_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, A);
   hip_check(hipGetLastError(), "attention launch");
 }
 

@@ -219,3 +219,39 @@ def test_alive_handles_and_snapshot(bridge, rng):
     assert snap["currentOwnedGpuBytes"] >= 40
     bridge.release(h)
     assert bridge.aliveHandleCount() == before
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 136, 200), (256, 256, 256), (129, 72, 77), (70, 100, 33), (1024, 768, 512)])
+@pytest.mark.parametrize("act", ["relu", "gelu"])
+@pytest.mark.parametrize("out_dtype", ["float32", "float16"])
+def test_gemm_amp_epilogue_act(bridge, rng, m, k, n, act, out_dtype):
+    """AMP linear + activation: f16(x) @ f16(W).T -> f16 round -> + b (f32) ->
+    relu / tanh-GELU in f32 -> out dtype.  K = 136 exercises the K-tail loads,
+    K = 100 the element-load fallback, 129 x 77 the edge tiles."""
+    x = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    w = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, (n,)).astype(np.float32)
+    x16, w16 = x.astype(np.float16), w.astype(np.float16)
+    h = bridge.matmul_ex(up(bridge, x16), up(bridge, w16), m=m, n=n, k=k, trans_b=True, in_dtype="float16",
+                         out_dtype=out_dtype, bias=up(bridge, b), round_out=True,
+                         act={"relu": 1, "gelu": 2}[act])
+    y = bridge.to_numpy(h).astype(np.float32)
+    z = O.matmul(x16, np.ascontiguousarray(w16.T)).astype(np.float32) + b
+    ref = np.where(z > 0, z, np.float32(0)) if act == "relu" else O.gelu_tanh_f32(z)
+    if out_dtype == "float16":
+        ref = ref.astype(np.float16).astype(np.float32)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
+@pytest.mark.parametrize("m,k,n", [(64, 784, 128), (64, 128, 10), (33, 17, 65)])
+def test_gemm_f32_bias_relu_gelu(bridge, rng, m, k, n):
+    """f32 linear layer epilogues (C1's Linear + ReLU), rel 1e-4."""
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.uniform(-1 / np.sqrt(k), 1 / np.sqrt(k), (n, k)).astype(np.float32)
+    b = rng.uniform(-1 / np.sqrt(k), 1 / np.sqrt(k), (n,)).astype(np.float32)
+    hx, hw, hb = up(bridge, x), up(bridge, w), up(bridge, b)
+    z = x.astype(np.float64) @ w.T.astype(np.float64) + b
+    for act, f in ((1, lambda t: np.maximum(t, 0)), (2, lambda t: O.gelu_tanh_f32(t.astype(np.float32)))):
+        y = bridge.to_numpy(bridge.matmul_ex(hx, hw, m=m, n=n, k=k, trans_b=True, bias=hb, act=act))
+        ref = f(z)
+        assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)

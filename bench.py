@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the HIP realizer on 1 MI355X (the BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,...]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,c4 | copy]
 
 Prints ONE JSON line.  ``value`` is configs[1] of BASELINE.json -- the fused
 elementwise + row-reduction chain ``relu(a*b+c)*exp(-a*a) -> sum(axis=1)`` on
@@ -42,6 +42,23 @@ C2_BYTES = 3 * 4096 * 4096 * 4 + 4096 * 4  # 201,342,976 B per step
 C2_OPS = [("MUL", -1, -2, 0), ("ADD", 0, -3, 0), ("IMM", 0, 0, 0), ("CMP_GT", 1, 2, 0),
           ("WHERE", 3, 1, 2), ("NEG", -1, 0, 0), ("MUL", 5, -1, 0), ("EXP", 6, 0, 0),
           ("MUL", 4, 7, 0)]
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "fused_c2_rowsum_4096x4096_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the C2 kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (calibrated against a copy kernel of
+    known size); None when that profile is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -244,6 +261,19 @@ def bench_c1(br, steps, warmup):
             "parity": O.report(y, ref, 1e-4)}
 
 
+def copy_probe(br, reps=5):
+    """A plain copy kernel of known size (256 MiB read + 256 MiB written per
+    launch): the calibration point for the FETCH_SIZE / WRITE_SIZE counters."""
+    n = 64 * 1024 * 1024
+    h = br.upload(np.zeros(n, np.float32), (n,), "float32")
+    for _ in range(reps):
+        br.release(br.copy_strided(h, 0, (n,), (1,)))
+    br.synchronize()
+    ms = [p["gpuMs"] for p in br.flushProfiles()["passProfiles"] if p["label"] == "copy_strided"]
+    br.release(h)
+    return {"bytes_read": n * 4, "bytes_written": n * 4, "kernel_ms": float(np.median(ms))}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -261,6 +291,10 @@ def main() -> int:
     from browsergrad_amd.bridge import HipRealizerBridge
     br = HipRealizerBridge(device=0, profiling=True)
 
+    if only == {"copy"}:
+        print(json.dumps({"probe": "copy", **copy_probe(br)}), flush=True)
+        br.close()
+        return 0
     log("c2 fused elementwise + row sum [4096,4096] f32")
     c2, host0 = bench_c2(br, a.steps, a.warmup)
     log(f"c2 kernel {c2['kernel_ms'] * 1e3:.2f} us  {c2['gbs_kernel']:.0f} GB/s  parity {c2['parity']}")
@@ -304,7 +338,7 @@ def main() -> int:
         "config": {"workload": "C2: relu(a*b+c)*exp(-a*a) -> row sum, a,b,c [4096,4096] f32, "
                                "one fused HIP kernel per step"},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel_us": round(c2["kernel_ms"] * 1e3, 3),
                      "algorithmic_bytes_per_launch": C2_BYTES},
         "cpu_baseline": cpu,

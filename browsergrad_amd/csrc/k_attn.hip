@@ -294,6 +294,353 @@ void launch_fa(bg_ctx* ctx, const FaArgs& A, int bh, int nqb) {
 
 bool al(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
+
+// ---- v2: 64 queries per wavefront, DMA K/V ring, transpose reads for V^T --------------
+//
+// One workgroup = 4 wavefronts x 64 queries of one (batch, head).  Keys are
+// processed in 64-key tiles held in a 4-stage LDS ring filled by
+// buffer_load_dwordx4 ... lds (three tiles in flight ahead of the MFMAs).
+//   S^T = K Q^T   v_mfma_f32_32x32x16 with A = K rows (ds_read_b128, rows
+//                 swizzled by (r >> 1) & 7), B = Q^T fragments kept in VGPRs;
+//                 a lane owns one query column, so max / sum are per lane.
+//   softmax       scores rounded to f16 in pairs (v_cvt_pk_f16_f32), max with
+//                 v_pk_max_f16, exponent argument with v_fma_mix_f32 straight
+//                 from the packed f16 scores, v_exp_f32, P packed to f16, row
+//                 sums with v_dot2_f32_f16 on the packed P (so the normaliser
+//                 sums exactly the P the MFMA uses).  O is rescaled only when
+//                 some lane's running max moved (wavefront vote).
+//   O^T += V^T P^T  A = V^T fragments read with ds_read_b64_tr_b16 (each
+//                 16-lane group transposes 4 key rows x 4 d-quads), which
+//                 lets V keep its natural [key][d] layout in LDS; B = P
+//                 straight from registers (the key order inside each 16-wide
+//                 k step is permuted identically on both operands).
+typedef __attribute__((address_space(3))) void* fa_lds_ptr_t;
+typedef short fa_v4s __attribute__((ext_vector_type(4)));
+typedef _Float16 fa_h2 __attribute__((ext_vector_type(2)));
+typedef float fa_f2 __attribute__((ext_vector_type(2)));
+typedef uint32_t fa_u4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFa2QW = 64;              // queries per wavefront
+constexpr int kFa2BQ = 4 * kFa2QW;      // queries per workgroup
+constexpr int kFa2BK = 64;              // keys per tile
+constexpr int kFa2S = 4;                // LDS ring stages
+constexpr int kFa2Tile = kFa2BK * 128;  // bytes of one K or V tile
+constexpr int kFa2NLD = 4;              // DMA instructions per wavefront per tile (2 K + 2 V)
+constexpr uint32_t kFa2Oob = 0x80000000u;
+
+struct Fa2Args {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  void* o;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int H, Sq, Sk, n_qblocks;
+  float sl2;  // scale * log2(e), > 0
+  int out_dtype;
+};
+
+__device__ __forceinline__ int fa2_k_unit(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
+__device__ __forceinline__ int fa2_v_unit(int r, int c) { return r * 8 + (c ^ ((r & 3) << 1)); }
+
+// Value of the lane 32 apart (lanes l and l ^ 32 hold the same query).
+// v_permlane32_swap exchanges the upper half of its first operand with the
+// lower half of its second: lanes 0-31 find the partner in the second
+// result, lanes 32-63 in the first.
+__device__ __forceinline__ float fa2_xor32(float x) {
+  const int v = __builtin_bit_cast(int, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+template <int N>
+__device__ __forceinline__ void fa2_wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+template <bool BF16>
+__device__ __forceinline__ float16v fa2_mfma(fa_u4 a, fa_u4 b, float16v c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, a), __builtin_bit_cast(bf168, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c,
+                                                  0, 0, 0);
+}
+
+// Two floats -> packed 16-bit pair (round to nearest even).
+template <bool BF16>
+__device__ __forceinline__ uint32_t fa2_pack(float a, float b) {
+  if constexpr (BF16) {
+    return uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
+           (uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
+  } else {
+    const fa_h2 h = __builtin_convertvector((fa_f2){a, b}, fa_h2);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float fa2_lo(uint32_t p) {
+  if constexpr (BF16) return __uint_as_float(p << 16);
+  else return static_cast<float>(__builtin_bit_cast(fa_h2, p)[0]);
+}
+template <bool BF16>
+__device__ __forceinline__ float fa2_hi(uint32_t p) {
+  if constexpr (BF16) return __uint_as_float(p & 0xffff0000u);
+  else return static_cast<float>(__builtin_bit_cast(fa_h2, p)[1]);
+}
+
+template <bool BF16, bool CAUSAL, bool ROUND_S>
+__global__ void __launch_bounds__(256) fa2_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
+  __shared__ fa_u4 smem[kFa2S * 2 * kFa2Tile / 16];
+  char* sb = reinterpret_cast<char*>(smem);
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hi = lane >> 5;
+  const int bh = blockIdx.x;
+  const int qblk = P.n_qblocks - 1 - int(blockIdx.y);  // heavy query blocks first
+  const int b = bh / P.H, h = bh % P.H;
+  const int q0 = qblk * kFa2BQ;
+  const int q0w = q0 + w * kFa2QW;
+
+  const uint16_t* Qp = P.q + b * P.q_sb + h * P.q_sh;
+  const uint16_t* Kp = P.k + b * P.k_sb + h * P.k_sh;
+  const uint16_t* Vp = P.v + b * P.v_sb + h * P.v_sh;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kp, (short)0, int(k_bytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vp, (short)0, int(v_bytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t r0 = __builtin_amdgcn_make_buffer_rsrc((void*)Kp, (short)0, 0, 0x00020000);
+
+  const int nt_all = (P.Sk + kFa2BK - 1) / kFa2BK;
+  const int nt = CAUSAL ? min(nt_all, (q0 + kFa2BQ + kFa2BK - 1) / kFa2BK) : nt_all;
+
+  // Per-lane DMA offsets: instruction i of wavefront w fills 1 KB block
+  // blk = i*4 + w (8 rows); lane L writes unit blk*64 + L.
+  uint32_t koff[2], voff[2];
+  int krow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int u = (i * 4 + w) * 64 + lane;
+    const int r = u >> 3, pc = u & 7;
+    krow[i] = r;
+    koff[i] = uint32_t((int64_t(r) * P.k_ss + ((pc ^ ((r >> 1) & 7)) * 8)) * 2);
+    voff[i] = uint32_t((int64_t(r) * P.v_ss + ((pc ^ ((r & 3) << 1)) * 8)) * 2);
+  }
+  auto issue_tile = [&](int t) {
+    char* st = sb + (t % kFa2S) * 2 * kFa2Tile;
+    const bool real = t < nt;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const bool ok = real && t * kFa2BK + krow[i] < P.Sk;
+      const uint32_t kso = real ? uint32_t(int64_t(t) * kFa2BK * P.k_ss * 2) : 0u;
+      const uint32_t vso = real ? uint32_t(int64_t(t) * kFa2BK * P.v_ss * 2) : 0u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? rk : r0, (fa_lds_ptr_t)(st + (i * 4 + w) * 1024), 16,
+                                               ok ? koff[i] : kFa2Oob, kso, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? rv : r0, (fa_lds_ptr_t)(st + kFa2Tile + (i * 4 + w) * 1024),
+                                               16, ok ? voff[i] : kFa2Oob, vso, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int t = 0; t < kFa2S - 1; ++t) issue_tile(t);
+
+  // Q^T fragments (B operand of S^T = K Q^T): query q0w + 32*qb + lane%32,
+  // d = 16*dc + 8*hi .. +8.
+  fa_u4 qf[2][4];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qi = q0w + 32 * qb + (lane & 31);
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc)
+      qf[qb][dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
+                             : fa_u4{0u, 0u, 0u, 0u};
+  }
+
+  float16v acc[2][2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[qb][db][e] = 0.f;
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.f, 0.f};
+  const float sl2 = P.sl2;
+  const fa_h2 ones = {(_Float16)1.f, (_Float16)1.f};
+
+  for (int t = 0; t < nt; ++t) {
+    fa2_wait_vm_lgkm0<kFa2NLD * (kFa2S - 2)>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_tile(t + kFa2S - 1);
+    const int j0 = t * kFa2BK;
+    if (CAUSAL && j0 > q0w + kFa2QW - 1) continue;  // whole tile above this wavefront's diagonal
+    const bool need_mask = (CAUSAL && j0 + kFa2BK - 1 > q0w) || (j0 + kFa2BK > P.Sk);
+    const char* kt = sb + (t % kFa2S) * 2 * kFa2Tile;
+    const char* vt = kt + kFa2Tile;
+
+    // S^T tiles: s[qb][kb] = K[32kb .. +32] Q^T[qb].
+    float16v s[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[qb][kb][e] = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int dc = 0; dc < 4; ++dc) {
+        const int r = kb * 32 + (lane & 31);
+        const fa_u4 kf = *reinterpret_cast<const fa_u4*>(kt + fa2_k_unit(r, dc * 2 + hi) * 16);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) s[qb][kb] = fa2_mfma<BF16>(kf, qf[qb][dc], s[qb][kb]);
+      }
+
+    // Online softmax per query block; P packed into B-operand fragments.
+    fa_u4 pf[2][2][2];  // [qb][kb][mm]
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int qi = q0w + 32 * qb + (lane & 31);
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kj = j0 + kb * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+            if (kj >= P.Sk || (CAUSAL && kj > qi)) s[qb][kb][e] = -INFINITY;
+          }
+      }
+      uint32_t sp[2][8];  // rounded scores, packed pairs (ROUND_S)
+      float mt;
+      if constexpr (ROUND_S) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sp[kb][e] = fa2_pack<BF16>(s[qb][kb][2 * e], s[qb][kb][2 * e + 1]);
+        if constexpr (!BF16) {
+          fa_h2 m2 = __builtin_bit_cast(fa_h2, sp[0][0]);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(fa_h2, sp[kb][e]));
+          mt = fmaxf(static_cast<float>(m2[0]), static_cast<float>(m2[1]));
+        } else {
+          mt = -INFINITY;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mt = fmaxf(mt, fmaxf(fa2_lo<true>(sp[kb][e]), fa2_hi<true>(sp[kb][e])));
+        }
+      } else {
+        mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[qb][kb][e]);
+      }
+      mt = fmaxf(mt, fa2_xor32(mt));
+      const float m_new = fmaxf(m_run[qb], mt * sl2);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+      m_run[qb] = m_new;
+      l_run[qb] *= alpha;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[qb][db][e] *= alpha;
+      }
+      float l_acc = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+          uint32_t pk[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int e = mm * 8 + 2 * j;
+            float x0, x1;
+            if constexpr (ROUND_S) {
+              x0 = __builtin_fmaf(fa2_lo<BF16>(sp[kb][e / 2]), sl2, -m_new);
+              x1 = __builtin_fmaf(fa2_hi<BF16>(sp[kb][e / 2]), sl2, -m_new);
+            } else {
+              x0 = __builtin_fmaf(s[qb][kb][e], sl2, -m_new);
+              x1 = __builtin_fmaf(s[qb][kb][e + 1], sl2, -m_new);
+            }
+            pk[j] = fa2_pack<BF16>(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
+            if constexpr (BF16) l_acc += fa2_lo<true>(pk[j]) + fa2_hi<true>(pk[j]);
+            else l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_h2, pk[j]), ones, l_acc, false);
+          }
+          pf[qb][kb][mm] = fa_u4{pk[0], pk[1], pk[2], pk[3]};
+        }
+      l_run[qb] += l_acc;
+    }
+
+    // O^T += V^T P^T: V^T fragments by transpose reads.  For lane l (group
+    // g = l/16, s = l%16): rows 32kb + 16mm + 8r + 4*(l/32) + s/4,
+    // d = 32db + 16*(g%2) + 4*(s%4).
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+          fa_v4s part[2];
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int row = kb * 32 + mm * 16 + r * 8 + 4 * hi + ((lane & 15) >> 2);
+            const int d = db * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+            const char* addr = vt + fa2_v_unit(row, d >> 3) * 16 + (d & 4) * 2;
+            part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) fa_v4s*)(
+                reinterpret_cast<uintptr_t>(addr)));
+          }
+          // One bit-cast of the concatenated vector. (Rebuilding the halves
+          // element by element through _Float16 casts was miscompiled by
+          // this clang into a single element broadcast.)
+          const fa_u4 vf = __builtin_bit_cast(fa_u4, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) acc[qb][db] = fa2_mfma<BF16>(vf, pf[qb][kb][mm], acc[qb][db]);
+        }
+  }
+
+  // O = acc / l.  O^T layout: lane = query column, register e holds d row
+  // 8*(e/4) + 4*hi + e%4 (+ 32*db): four consecutive d per (e/4) group.
+  char* Ob = static_cast<char*>(P.o);
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qi = q0w + 32 * qb + (lane & 31);
+    const float lt = l_run[qb] + fa2_xor32(l_run[qb]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    if (qi >= P.Sq) continue;
+    const int64_t obase = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * hi;
+        const float x0 = acc[qb][db][4 * g + 0] * inv, x1 = acc[qb][db][4 * g + 1] * inv;
+        const float x2 = acc[qb][db][4 * g + 2] * inv, x3 = acc[qb][db][4 * g + 3] * inv;
+        if (P.out_dtype == 0) {
+          *reinterpret_cast<float4*>(Ob + (obase + d0) * 4) = make_float4(x0, x1, x2, x3);
+        } else if (P.out_dtype == 1) {
+          *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) = make_uint2(fa2_pack<false>(x0, x1), fa2_pack<false>(x2, x3));
+        } else {
+          *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) = make_uint2(fa2_pack<true>(x0, x1), fa2_pack<true>(x2, x3));
+        }
+      }
+  }
+}
+
+template <bool BF16, bool CAUSAL, bool ROUND_S>
+void launch_fa2(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uint32_t vb) {
+  dim3 grid(unsigned(bh), unsigned(nqb), 1);
+  bg::dispatch(ctx, fa2_fwd_kernel<BF16, CAUSAL, ROUND_S>, grid, dim3(256), 0, A, kb, vb);
+}
+
 }  // namespace
 
 namespace bg {
@@ -325,6 +672,48 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     Profile prof(ctx, "attention_generic", bytes, flops);
     launch_attention_generic(ctx, d, qp, kp, vp, nullptr, 0, 0, out.ptr(),
                              d.in_dtype != BG_F32);
+    return;
+  }
+  // v2 kernel: K/V rows 16-byte aligned for the DMA, byte spans within a
+  // 32-bit buffer offset, positive scale (the row max is taken before scaling).
+  const int64_t k_span = ((d.batch - 1) * d.k_sb + (d.heads - 1) * d.k_sh + (sk - 1) * d.k_ss + d.d) * es;
+  const int64_t v_span = ((d.batch - 1) * d.v_sb + (d.heads - 1) * d.v_sh + (sk - 1) * d.v_ss + d.d) * es;
+  const int64_t k_head = ((sk - 1) * d.k_ss + d.d) * es, v_head = ((sk - 1) * d.v_ss + d.d) * es;
+  const bool v2_ok = d.k_ss % 8 == 0 && d.v_ss % 8 == 0 && d.k_sb % 8 == 0 && d.k_sh % 8 == 0 &&
+                     d.v_sb % 8 == 0 && d.v_sh % 8 == 0 && al(vp, 16) && d.scale > 0.f &&
+                     k_span > 0 && v_span > 0 && k_head < (int64_t(1) << 31) &&
+                     v_head < (int64_t(1) << 31) && (sq + kFa2BQ - 1) / kFa2BQ <= 65535;
+  if (v2_ok) {
+    Fa2Args A{};
+    A.q = reinterpret_cast<const uint16_t*>(qp);
+    A.k = reinterpret_cast<const uint16_t*>(kp);
+    A.v = reinterpret_cast<const uint16_t*>(vp);
+    A.o = out.ptr();
+    A.q_sb = d.q_sb; A.q_sh = d.q_sh; A.q_ss = d.q_ss;
+    A.k_sb = d.k_sb; A.k_sh = d.k_sh; A.k_ss = d.k_ss;
+    A.v_sb = d.v_sb; A.v_sh = d.v_sh; A.v_ss = d.v_ss;
+    A.o_sb = d.o_sb; A.o_sh = d.o_sh; A.o_ss = d.o_ss;
+    A.H = int(d.heads);
+    A.Sq = int(sq);
+    A.Sk = int(sk);
+    A.n_qblocks = int((sq + kFa2BQ - 1) / kFa2BQ);
+    A.sl2 = d.scale * 1.4426950408889634f;
+    A.out_dtype = d.out_dtype;
+    const int bh = int(d.batch * d.heads);
+    const bool bf = d.in_dtype == BG_BF16;
+    const bool c = d.causal != 0;
+    const bool r = d.round_scores != 0;
+    const uint32_t kb = uint32_t(k_head), vb = uint32_t(v_head);
+    Profile prof(ctx, bf ? "attention_bf16" : "attention_f16", bytes, flops);
+#define BG_FA2(B_, C_, R_) launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb)
+    if (bf) {
+      if (c) { if (r) BG_FA2(true, true, true); else BG_FA2(true, true, false); }
+      else { if (r) BG_FA2(true, false, true); else BG_FA2(true, false, false); }
+    } else {
+      if (c) { if (r) BG_FA2(false, true, true); else BG_FA2(false, true, false); }
+      else { if (r) BG_FA2(false, false, true); else BG_FA2(false, false, false); }
+    }
+#undef BG_FA2
     return;
   }
   FaArgs A{};

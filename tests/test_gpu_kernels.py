@@ -255,3 +255,55 @@ def test_gemm_f32_bias_relu_gelu(bridge, rng, m, k, n):
         y = bridge.to_numpy(bridge.matmul_ex(hx, hw, m=m, n=n, k=k, trans_b=True, bias=hb, act=act))
         ref = f(z)
         assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_long_sequence(bridge, rng, dtype, causal):
+    """Two full S=2048 heads (the C4 shape per head) and a ragged 1100."""
+    for (b, h, s) in ((1, 2, 2048), (1, 1, 1100)):
+        d = 64
+        q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
+        scale = 0.125
+        if dtype == "float16":
+            q16, k16, v16 = (t.astype(np.float16) for t in (q, k, v))
+            hq, hk, hv = up(bridge, q16), up(bridge, k16), up(bridge, v16)
+            ref = O.sdpa_amp(q16, k16, v16, scale, causal).astype(np.float32)
+        else:
+            q16, k16, v16 = (O.f32_to_bf16_bits(t) for t in (q, k, v))
+            hq, hk, hv = (up(bridge, t, "bfloat16") for t in (q16, k16, v16))
+            ref = O.bf16_bits_to_f32(O.sdpa_bf16(q16, k16, v16, scale, causal))
+        ho = bridge.attention_ex(hq, hk, hv, batch=b, heads=h, sq=s, sk=s, d=d, scale=scale, causal=causal,
+                                 in_dtype=dtype, round_scores=True)
+        y = bridge.to_numpy(ho)
+        y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
+        assert O.within(y, ref, TOL16).all(), (b, h, s, O.report(y, ref, TOL16))
+
+
+def test_attention_rectangular_noncausal(bridge, rng):
+    b, h, sq, sk, d = 2, 3, 100, 300, 64
+    q = rng.standard_normal((b, h, sq, d)).astype(np.float16)
+    k = rng.standard_normal((b, h, sk, d)).astype(np.float16)
+    v = rng.standard_normal((b, h, sk, d)).astype(np.float16)
+    ho = bridge.attention_ex(up(bridge, q), up(bridge, k), up(bridge, v), batch=b, heads=h, sq=sq, sk=sk, d=d,
+                             scale=0.125, causal=False, in_dtype="float16", round_scores=True)
+    y = bridge.to_numpy(ho).astype(np.float32)
+    ref = O.sdpa_amp(q, k, v, 0.125, False).astype(np.float32)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
+def test_attention_strided_fused_qkv_views(bridge, rng):
+    """Q/K/V as views into one fused QKV projection [B, S, 3, H, D] (the GPT-2
+    block layout): head-split without a copy, output [B, S, H, D]."""
+    B, S, H, D = 2, 192, 3, 64
+    qkv = rng.standard_normal((B, S, 3, H, D)).astype(np.float16)
+    h = up(bridge, qkv)
+    sb, ss, sh = S * 3 * H * D, 3 * H * D, D
+    views = [(i * H * D, sb, sh, ss) for i in range(3)]
+    ho = bridge.attention_ex(h, h, h, batch=B, heads=H, sq=S, sk=S, d=D, scale=0.125, causal=True,
+                             in_dtype="float16", round_scores=True, q_view=views[0], k_view=views[1],
+                             v_view=views[2], o_strides=(S * H * D, D, H * D))
+    y = bridge.to_numpy(ho).reshape(B, S, H, D).astype(np.float32)
+    q, k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
+    ref = O.sdpa_amp(q, k, v, 0.125, True).astype(np.float32).transpose(0, 2, 1, 3)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)

@@ -295,37 +295,41 @@ void launch_fa(bg_ctx* ctx, const FaArgs& A, int bh, int nqb) {
 bool al(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
 
-// ---- v2: 64 queries per wavefront, DMA K/V ring, transpose reads for V^T --------------
+// ---- v2: 8 wavefronts x 32 queries, DMA K/V ring, software-pipelined S --------------
 //
-// One workgroup = 4 wavefronts x 64 queries of one (batch, head).  Keys are
-// processed in 64-key tiles held in a 4-stage LDS ring filled by
-// buffer_load_dwordx4 ... lds (three tiles in flight ahead of the MFMAs).
-//   S^T = K Q^T   v_mfma_f32_32x32x16 with A = K rows (ds_read_b128, rows
-//                 swizzled by (r >> 1) & 7), B = Q^T fragments kept in VGPRs;
-//                 a lane owns one query column, so max / sum are per lane.
-//   softmax       scores rounded to f16 in pairs (v_cvt_pk_f16_f32), max with
-//                 v_pk_max_f16, exponent argument with v_fma_mix_f32 straight
-//                 from the packed f16 scores, v_exp_f32, P packed to f16, row
-//                 sums with v_dot2_f32_f16 on the packed P (so the normaliser
-//                 sums exactly the P the MFMA uses).  O is rescaled only when
-//                 some lane's running max moved (wavefront vote).
-//   O^T += V^T P^T  A = V^T fragments read with ds_read_b64_tr_b16 (each
-//                 16-lane group transposes 4 key rows x 4 d-quads), which
-//                 lets V keep its natural [key][d] layout in LDS; B = P
-//                 straight from registers (the key order inside each 16-wide
-//                 k step is permuted identically on both operands).
+// One workgroup = 8 wavefronts x 32 queries = 256 queries of one (batch,
+// head), two wavefronts per SIMD (launch bounds 512 x 1 keep each at <= 256
+// registers).  Keys are processed in 64-key tiles held in a kFa2S-stage LDS
+// ring filled by buffer_load_dwordx4 ... lds (each wavefront moves one 1 KB
+// slice of K and one of V per tile).  Per tile t a wavefront
+//   1. issues the S^T MFMAs of tile t+1 (K fragments by ds_read_b128, rows
+//      swizzled by (r >> 1) & 7; Q^T fragments stay in VGPRs),
+//   2. runs the online softmax of tile t on the VALU while those MFMAs run:
+//      scores rounded to f16 in pairs (v_cvt_pk_f16_f32), max with
+//      v_pk_max_f16, exponent argument by v_fma_mix_f32 from the packed
+//      scores, v_exp_f32, P packed to 16 bits, row sums by v_dot2 on the
+//      packed P (the normaliser sums exactly the P the MFMA uses),
+//   3. accumulates O^T += V^T P^T (V^T fragments by ds_read_b64_tr_b16 from
+//      V's natural [key][d] layout; P straight from registers, the key order
+//      inside each 16-wide k step permuted identically on both operands).
+// The reference max moves only when a lane's max grows by more than 2^8
+// (log2 domain): P <= 256 is exact in f16/bf16 and the final 1/l normalises
+// it, so the O rescale runs a handful of times per row instead of per tile.
 typedef __attribute__((address_space(3))) void* fa_lds_ptr_t;
 typedef short fa_v4s __attribute__((ext_vector_type(4)));
 typedef _Float16 fa_h2 __attribute__((ext_vector_type(2)));
 typedef float fa_f2 __attribute__((ext_vector_type(2)));
 typedef uint32_t fa_u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kFa2QW = 64;              // queries per wavefront
-constexpr int kFa2BQ = 4 * kFa2QW;      // queries per workgroup
+constexpr int kFa2QW = 32;              // queries per wavefront
+constexpr int kFa2NW = 8;               // wavefronts per workgroup
+constexpr int kFa2BQ = kFa2NW * kFa2QW; // queries per workgroup
 constexpr int kFa2BK = 64;              // keys per tile
-constexpr int kFa2S = 4;                // LDS ring stages
+constexpr int kFa2S = 5;                // LDS ring stages
+constexpr int kFa2D = kFa2S - 2;        // tiles issued ahead of the one whose K is read
 constexpr int kFa2Tile = kFa2BK * 128;  // bytes of one K or V tile
-constexpr int kFa2NLD = 4;              // DMA instructions per wavefront per tile (2 K + 2 V)
+constexpr int kFa2NLD = 2;              // DMA instructions per wavefront per tile (K + V)
+constexpr float kFa2Slack = 8.f;        // log2 headroom before the reference max moves
 constexpr uint32_t kFa2Oob = 0x80000000u;
 
 struct Fa2Args {
@@ -394,8 +398,140 @@ __device__ __forceinline__ float fa2_hi(uint32_t p) {
   else return static_cast<float>(__builtin_bit_cast(fa_h2, p)[1]);
 }
 
+// S^T tile (64 keys x 32 queries) of the K tile at kt: s[kb] holds keys
+// 32kb + 8*(e/4) + 4*(lane/32) + e%4 for query lane%32.
+template <bool BF16>
+__device__ __forceinline__ void fa2_scores(const char* kt, const fa_u4 (&qf)[4], float16v (&s)[2]) {
+  const int lane = threadIdx.x & 63, hi = lane >> 5;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int r = kb * 32 + (lane & 31);
+    fa_u4 kf[4];
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) kf[dc] = *reinterpret_cast<const fa_u4*>(kt + fa2_k_unit(r, dc * 2 + hi) * 16);
+    s[kb] = fa2_mfma<BF16>(kf[0], qf[0], float16v{});
+#pragma unroll
+    for (int dc = 1; dc < 4; ++dc) s[kb] = fa2_mfma<BF16>(kf[dc], qf[dc], s[kb]);
+  }
+}
+
+// Online-softmax update of tile j0 for this lane's query qi; P (16-bit,
+// packed as MFMA B fragments) into pf[kb][mm].
 template <bool BF16, bool CAUSAL, bool ROUND_S>
-__global__ void __launch_bounds__(256) fa2_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
+__device__ __forceinline__ void fa2_softmax(float16v (&s)[2], int j0, int qi, int Sk, bool need_mask, float sl2,
+                                            float& m_run, float& l_run, float16v (&acc)[2], fa_u4 (&pf)[2][2]) {
+  const int hi = (threadIdx.x >> 5) & 1;
+  if (need_mask) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int kj = j0 + kb * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+        if (kj >= Sk || (CAUSAL && kj > qi)) s[kb][e] = -INFINITY;
+      }
+  }
+  uint32_t sp[2][8];  // rounded scores, packed pairs (ROUND_S)
+  float mt;
+  if constexpr (ROUND_S) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sp[kb][e] = fa2_pack<BF16>(s[kb][2 * e], s[kb][2 * e + 1]);
+    if constexpr (!BF16) {
+      fa_h2 m2 = __builtin_bit_cast(fa_h2, sp[0][0]);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(fa_h2, sp[kb][e]));
+      mt = fmaxf(static_cast<float>(m2[0]), static_cast<float>(m2[1]));
+    } else {
+      mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mt = fmaxf(mt, fmaxf(fa2_lo<true>(sp[kb][e]), fa2_hi<true>(sp[kb][e])));
+    }
+  } else {
+    mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[kb][e]);
+  }
+  mt = fmaxf(mt, fa2_xor32(mt));
+  const float mc = mt * sl2;
+  // Wavefront-uniform: move the reference max only when some lane's max
+  // exceeds it by more than kFa2Slack (always on the first tile: m_run = -inf).
+  if (__any(mc > m_run + kFa2Slack)) {
+    const float m_new = fmaxf(m_run, mc);
+    const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
+  }
+  const float m_use = m_run == -INFINITY ? 0.f : m_run;
+  const fa_h2 ones = {(_Float16)1.f, (_Float16)1.f};
+  float l_acc = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = mm * 8 + 2 * j;
+        float x0, x1;
+        if constexpr (ROUND_S) {
+          x0 = __builtin_fmaf(fa2_lo<BF16>(sp[kb][e / 2]), sl2, -m_use);
+          x1 = __builtin_fmaf(fa2_hi<BF16>(sp[kb][e / 2]), sl2, -m_use);
+        } else {
+          x0 = __builtin_fmaf(s[kb][e], sl2, -m_use);
+          x1 = __builtin_fmaf(s[kb][e + 1], sl2, -m_use);
+        }
+        pk[j] = fa2_pack<BF16>(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
+        if constexpr (BF16) l_acc += fa2_lo<true>(pk[j]) + fa2_hi<true>(pk[j]);
+        else l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_h2, pk[j]), ones, l_acc, false);
+      }
+      pf[kb][mm] = fa_u4{pk[0], pk[1], pk[2], pk[3]};
+    }
+  l_run += l_acc;
+}
+
+// O^T += V^T P^T over the V tile at vt.  V^T fragments by transpose reads:
+// for lane l (group g = l/16, s = l%16) rows 32kb + 16mm + 8r + 4*(l/32) +
+// s/4, d = 32db + 16*(g%2) + 4*(s%4).
+template <bool BF16>
+__device__ __forceinline__ void fa2_pv(const char* vt, const fa_u4 (&pf)[2][2], float16v (&acc)[2]) {
+  const int lane = threadIdx.x & 63, hi = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        fa_v4s part[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int row = kb * 32 + mm * 16 + r * 8 + 4 * hi + ((lane & 15) >> 2);
+          const int d = db * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+          const char* addr = vt + fa2_v_unit(row, d >> 3) * 16 + (d & 4) * 2;
+          part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) fa_v4s*)(reinterpret_cast<uintptr_t>(addr)));
+        }
+        // One bit-cast of the concatenated vector. (Rebuilding the halves
+        // element by element through _Float16 casts was miscompiled by
+        // this clang into a single element broadcast.)
+        const fa_u4 vf =
+            __builtin_bit_cast(fa_u4, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        acc[db] = fa2_mfma<BF16>(vf, pf[kb][mm], acc[db]);
+      }
+}
+
+template <bool BF16, bool CAUSAL, bool ROUND_S>
+__global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
   __shared__ fa_u4 smem[kFa2S * 2 * kFa2Tile / 16];
   char* sb = reinterpret_cast<char*>(smem);
 
@@ -407,6 +543,7 @@ __global__ void __launch_bounds__(256) fa2_fwd_kernel(Fa2Args P, uint32_t k_byte
   const int b = bh / P.H, h = bh % P.H;
   const int q0 = qblk * kFa2BQ;
   const int q0w = q0 + w * kFa2QW;
+  const int qi = q0w + (lane & 31);
 
   const uint16_t* Qp = P.q + b * P.q_sb + h * P.q_sh;
   const uint16_t* Kp = P.k + b * P.k_sb + h * P.k_sh;
@@ -417,220 +554,113 @@ __global__ void __launch_bounds__(256) fa2_fwd_kernel(Fa2Args P, uint32_t k_byte
 
   const int nt_all = (P.Sk + kFa2BK - 1) / kFa2BK;
   const int nt = CAUSAL ? min(nt_all, (q0 + kFa2BQ + kFa2BK - 1) / kFa2BK) : nt_all;
+  // Tiles this wavefront computes (causal: up to its own diagonal).
+  const int ntw = CAUSAL ? min(nt, (q0w + kFa2QW + kFa2BK - 1) / kFa2BK) : nt;
 
-  // Per-lane DMA offsets: instruction i of wavefront w fills 1 KB block
-  // blk = i*4 + w (8 rows); lane L writes unit blk*64 + L.
-  uint32_t koff[2], voff[2];
-  int krow[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int u = (i * 4 + w) * 64 + lane;
-    const int r = u >> 3, pc = u & 7;
-    krow[i] = r;
-    koff[i] = uint32_t((int64_t(r) * P.k_ss + ((pc ^ ((r >> 1) & 7)) * 8)) * 2);
-    voff[i] = uint32_t((int64_t(r) * P.v_ss + ((pc ^ ((r & 3) << 1)) * 8)) * 2);
-  }
+  // DMA: wavefront w fills the 1 KB slice w (rows 8w .. 8w+7) of each K and
+  // V tile; lane L writes 16-byte unit 64w + L = (row r, physical chunk pc),
+  // which holds logical chunk pc ^ swizzle(r).
+  const int u = w * 64 + lane;
+  const int krow = u >> 3, pc = u & 7;
+  const uint32_t koff = uint32_t((int64_t(krow) * P.k_ss + ((pc ^ ((krow >> 1) & 7)) * 8)) * 2);
+  const uint32_t voff = uint32_t((int64_t(krow) * P.v_ss + ((pc ^ ((krow & 3) << 1)) * 8)) * 2);
   auto issue_tile = [&](int t) {
     char* st = sb + (t % kFa2S) * 2 * kFa2Tile;
     const bool real = t < nt;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const bool ok = real && t * kFa2BK + krow[i] < P.Sk;
-      const uint32_t kso = real ? uint32_t(int64_t(t) * kFa2BK * P.k_ss * 2) : 0u;
-      const uint32_t vso = real ? uint32_t(int64_t(t) * kFa2BK * P.v_ss * 2) : 0u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? rk : r0, (fa_lds_ptr_t)(st + (i * 4 + w) * 1024), 16,
-                                               ok ? koff[i] : kFa2Oob, kso, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? rv : r0, (fa_lds_ptr_t)(st + kFa2Tile + (i * 4 + w) * 1024),
-                                               16, ok ? voff[i] : kFa2Oob, vso, 0, 0);
-    }
+    const bool ok = real && t * kFa2BK + krow < P.Sk;
+    const uint32_t kso = real ? uint32_t(int64_t(t) * kFa2BK * P.k_ss * 2) : 0u;
+    const uint32_t vso = real ? uint32_t(int64_t(t) * kFa2BK * P.v_ss * 2) : 0u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? rk : r0, (fa_lds_ptr_t)(st + w * 1024), 16,
+                                             ok ? koff : kFa2Oob, kso, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? rv : r0, (fa_lds_ptr_t)(st + kFa2Tile + w * 1024), 16,
+                                             ok ? voff : kFa2Oob, vso, 0, 0);
   };
 
+  // Q^T fragments (B operand of S^T = K Q^T): query qi, d = 16*dc + 8*hi .. +8.
+  fa_u4 qf[4];
 #pragma unroll
-  for (int t = 0; t < kFa2S - 1; ++t) issue_tile(t);
+  for (int dc = 0; dc < 4; ++dc)
+    qf[dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
+                       : fa_u4{0u, 0u, 0u, 0u};
+  // Tiles 0 .. kFa2D in flight; wait for tile 0 (and Q) only.
+#pragma unroll
+  for (int t = 0; t <= kFa2D; ++t) issue_tile(t);
+  fa2_wait_vm_lgkm0<kFa2NLD * kFa2D>();
+  __builtin_amdgcn_s_barrier();
 
-  // Q^T fragments (B operand of S^T = K Q^T): query q0w + 32*qb + lane%32,
-  // d = 16*dc + 8*hi .. +8.
-  fa_u4 qf[2][4];
+  float16v acc[2];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qi = q0w + 32 * qb + (lane & 31);
+  for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int dc = 0; dc < 4; ++dc)
-      qf[qb][dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
-                             : fa_u4{0u, 0u, 0u, 0u};
-  }
-
-  float16v acc[2][2];
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[qb][db][e] = 0.f;
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+    for (int e = 0; e < 16; ++e) acc[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = P.sl2;
-  const fa_h2 ones = {(_Float16)1.f, (_Float16)1.f};
 
-  for (int t = 0; t < nt; ++t) {
-    fa2_wait_vm_lgkm0<kFa2NLD * (kFa2S - 2)>();
+  float16v s_a[2], s_b[2];
+  if (ntw > 0) fa2_scores<BF16>(sb, qf, s_a);
+
+  // Tile t: K(t+1) and V(t) must be resident.  Outstanding DMA at the top:
+  // tiles t+1 .. t+kFa2D; wait until t+1 has landed, then (after the
+  // barrier every wavefront is done with tile t-1's stage) refill that stage
+  // with tile t+1+kFa2D.
+  auto step = [&](int t, float16v(&s_cur)[2], float16v(&s_nxt)[2]) {
+    fa2_wait_vm_lgkm0<kFa2NLD * (kFa2D - 1)>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue_tile(t + kFa2S - 1);
+    issue_tile(t + 1 + kFa2D);
+    if (t >= ntw) return;
+    const char* kt_next = sb + ((t + 1) % kFa2S) * 2 * kFa2Tile;
+    const char* vt = sb + (t % kFa2S) * 2 * kFa2Tile + kFa2Tile;
+    if (t + 1 < ntw) fa2_scores<BF16>(kt_next, qf, s_nxt);
     const int j0 = t * kFa2BK;
-    if (CAUSAL && j0 > q0w + kFa2QW - 1) continue;  // whole tile above this wavefront's diagonal
     const bool need_mask = (CAUSAL && j0 + kFa2BK - 1 > q0w) || (j0 + kFa2BK > P.Sk);
-    const char* kt = sb + (t % kFa2S) * 2 * kFa2Tile;
-    const char* vt = kt + kFa2Tile;
-
-    // S^T tiles: s[qb][kb] = K[32kb .. +32] Q^T[qb].
-    float16v s[2][2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[qb][kb][e] = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int dc = 0; dc < 4; ++dc) {
-        const int r = kb * 32 + (lane & 31);
-        const fa_u4 kf = *reinterpret_cast<const fa_u4*>(kt + fa2_k_unit(r, dc * 2 + hi) * 16);
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) s[qb][kb] = fa2_mfma<BF16>(kf, qf[qb][dc], s[qb][kb]);
-      }
-
-    // Online softmax per query block; P packed into B-operand fragments.
-    fa_u4 pf[2][2][2];  // [qb][kb][mm]
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int qi = q0w + 32 * qb + (lane & 31);
-      if (need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int kj = j0 + kb * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
-            if (kj >= P.Sk || (CAUSAL && kj > qi)) s[qb][kb][e] = -INFINITY;
-          }
-      }
-      uint32_t sp[2][8];  // rounded scores, packed pairs (ROUND_S)
-      float mt;
-      if constexpr (ROUND_S) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sp[kb][e] = fa2_pack<BF16>(s[qb][kb][2 * e], s[qb][kb][2 * e + 1]);
-        if constexpr (!BF16) {
-          fa_h2 m2 = __builtin_bit_cast(fa_h2, sp[0][0]);
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(fa_h2, sp[kb][e]));
-          mt = fmaxf(static_cast<float>(m2[0]), static_cast<float>(m2[1]));
-        } else {
-          mt = -INFINITY;
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) mt = fmaxf(mt, fmaxf(fa2_lo<true>(sp[kb][e]), fa2_hi<true>(sp[kb][e])));
-        }
-      } else {
-        mt = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[qb][kb][e]);
-      }
-      mt = fmaxf(mt, fa2_xor32(mt));
-      const float m_new = fmaxf(m_run[qb], mt * sl2);
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-      m_run[qb] = m_new;
-      l_run[qb] *= alpha;
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) acc[qb][db][e] *= alpha;
-      }
-      float l_acc = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-          uint32_t pk[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int e = mm * 8 + 2 * j;
-            float x0, x1;
-            if constexpr (ROUND_S) {
-              x0 = __builtin_fmaf(fa2_lo<BF16>(sp[kb][e / 2]), sl2, -m_new);
-              x1 = __builtin_fmaf(fa2_hi<BF16>(sp[kb][e / 2]), sl2, -m_new);
-            } else {
-              x0 = __builtin_fmaf(s[qb][kb][e], sl2, -m_new);
-              x1 = __builtin_fmaf(s[qb][kb][e + 1], sl2, -m_new);
-            }
-            pk[j] = fa2_pack<BF16>(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
-            if constexpr (BF16) l_acc += fa2_lo<true>(pk[j]) + fa2_hi<true>(pk[j]);
-            else l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_h2, pk[j]), ones, l_acc, false);
-          }
-          pf[qb][kb][mm] = fa_u4{pk[0], pk[1], pk[2], pk[3]};
-        }
-      l_run[qb] += l_acc;
-    }
-
-    // O^T += V^T P^T: V^T fragments by transpose reads.  For lane l (group
-    // g = l/16, s = l%16): rows 32kb + 16mm + 8r + 4*(l/32) + s/4,
-    // d = 32db + 16*(g%2) + 4*(s%4).
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-          fa_v4s part[2];
-#pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            const int row = kb * 32 + mm * 16 + r * 8 + 4 * hi + ((lane & 15) >> 2);
-            const int d = db * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-            const char* addr = vt + fa2_v_unit(row, d >> 3) * 16 + (d & 4) * 2;
-            part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) fa_v4s*)(
-                reinterpret_cast<uintptr_t>(addr)));
-          }
-          // One bit-cast of the concatenated vector. (Rebuilding the halves
-          // element by element through _Float16 casts was miscompiled by
-          // this clang into a single element broadcast.)
-          const fa_u4 vf = __builtin_bit_cast(fa_u4, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) acc[qb][db] = fa2_mfma<BF16>(vf, pf[qb][kb][mm], acc[qb][db]);
-        }
+    fa_u4 pf[2][2];
+    fa2_softmax<BF16, CAUSAL, ROUND_S>(s_cur, j0, qi, P.Sk, need_mask, sl2, m_run, l_run, acc, pf);
+    fa2_pv<BF16>(vt, pf, acc);
+  };
+  int t = 0;
+  for (; t + 1 < nt; t += 2) {
+    step(t, s_a, s_b);
+    step(t + 1, s_b, s_a);
   }
+  if (t < nt) step(t, s_a, s_b);
 
   // O = acc / l.  O^T layout: lane = query column, register e holds d row
   // 8*(e/4) + 4*hi + e%4 (+ 32*db): four consecutive d per (e/4) group.
+  const float lt = l_run + fa2_xor32(l_run);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (qi >= P.Sq) return;
   char* Ob = static_cast<char*>(P.o);
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qi = q0w + 32 * qb + (lane & 31);
-    const float lt = l_run[qb] + fa2_xor32(l_run[qb]);
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    if (qi >= P.Sq) continue;
-    const int64_t obase = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss;
+  const int64_t obase = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss;
+  if (P.out_dtype == 0) {
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = db * 32 + 8 * g + 4 * hi;
-        const float x0 = acc[qb][db][4 * g + 0] * inv, x1 = acc[qb][db][4 * g + 1] * inv;
-        const float x2 = acc[qb][db][4 * g + 2] * inv, x3 = acc[qb][db][4 * g + 3] * inv;
-        if (P.out_dtype == 0) {
-          *reinterpret_cast<float4*>(Ob + (obase + d0) * 4) = make_float4(x0, x1, x2, x3);
-        } else if (P.out_dtype == 1) {
-          *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) = make_uint2(fa2_pack<false>(x0, x1), fa2_pack<false>(x2, x3));
-        } else {
-          *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) = make_uint2(fa2_pack<true>(x0, x1), fa2_pack<true>(x2, x3));
-        }
+        *reinterpret_cast<float4*>(Ob + (obase + d0) * 4) =
+            make_float4(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv, acc[db][4 * g + 2] * inv,
+                        acc[db][4 * g + 3] * inv);
+      }
+  } else if (P.out_dtype == 1) {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * hi;
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<false>(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv),
+                       fa2_pack<false>(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv));
+      }
+  } else {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * hi;
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<true>(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv),
+                       fa2_pack<true>(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv));
       }
   }
 }
@@ -638,7 +668,7 @@ __global__ void __launch_bounds__(256) fa2_fwd_kernel(Fa2Args P, uint32_t k_byte
 template <bool BF16, bool CAUSAL, bool ROUND_S>
 void launch_fa2(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uint32_t vb) {
   dim3 grid(unsigned(bh), unsigned(nqb), 1);
-  bg::dispatch(ctx, fa2_fwd_kernel<BF16, CAUSAL, ROUND_S>, grid, dim3(256), 0, A, kb, vb);
+  bg::dispatch(ctx, fa2_fwd_kernel<BF16, CAUSAL, ROUND_S>, grid, dim3(kFa2NW * 64), 0, A, kb, vb);
 }
 
 }  // namespace

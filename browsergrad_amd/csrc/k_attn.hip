@@ -30,6 +30,7 @@
 //     multiply).
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "common.cuh"
 #include "core.h"
@@ -325,7 +326,7 @@ constexpr int kFa2QW = 32;              // queries per wavefront
 constexpr int kFa2NW = 8;               // wavefronts per workgroup
 constexpr int kFa2BQ = kFa2NW * kFa2QW; // queries per workgroup
 constexpr int kFa2BK = 64;              // keys per tile
-constexpr int kFa2S = 5;                // LDS ring stages
+constexpr int kFa2S = 4;                // LDS ring stages (the main loop is unrolled by this)
 constexpr int kFa2D = kFa2S - 2;        // tiles issued ahead of the one whose K is read
 constexpr int kFa2Tile = kFa2BK * 128;  // bytes of one K or V tile
 constexpr int kFa2NLD = 2;              // DMA instructions per wavefront per tile (K + V)
@@ -564,8 +565,8 @@ __global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint
   const int krow = u >> 3, pc = u & 7;
   const uint32_t koff = uint32_t((int64_t(krow) * P.k_ss + ((pc ^ ((krow >> 1) & 7)) * 8)) * 2);
   const uint32_t voff = uint32_t((int64_t(krow) * P.v_ss + ((pc ^ ((krow & 3) << 1)) * 8)) * 2);
-  auto issue_tile = [&](int t) {
-    char* st = sb + (t % kFa2S) * 2 * kFa2Tile;
+  auto issue_tile = [&](int t, int stage) {
+    char* st = sb + stage * 2 * kFa2Tile;
     const bool real = t < nt;
     const bool ok = real && t * kFa2BK + krow < P.Sk;
     const uint32_t kso = real ? uint32_t(int64_t(t) * kFa2BK * P.k_ss * 2) : 0u;
@@ -584,7 +585,7 @@ __global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint
                        : fa_u4{0u, 0u, 0u, 0u};
   // Tiles 0 .. kFa2D in flight; wait for tile 0 (and Q) only.
 #pragma unroll
-  for (int t = 0; t <= kFa2D; ++t) issue_tile(t);
+  for (int t = 0; t <= kFa2D; ++t) issue_tile(t, t);
   fa2_wait_vm_lgkm0<kFa2NLD * kFa2D>();
   __builtin_amdgcn_s_barrier();
 
@@ -602,15 +603,17 @@ __global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint
   // Tile t: K(t+1) and V(t) must be resident.  Outstanding DMA at the top:
   // tiles t+1 .. t+kFa2D; wait until t+1 has landed, then (after the
   // barrier every wavefront is done with tile t-1's stage) refill that stage
-  // with tile t+1+kFa2D.
-  auto step = [&](int t, float16v(&s_cur)[2], float16v(&s_nxt)[2]) {
+  // with tile t+1+kFa2D.  The ring stage of t is the compile-time STG, so
+  // every LDS address is a loop-invariant lane offset plus an immediate.
+  auto step = [&](auto stg, int t, float16v(&s_cur)[2], float16v(&s_nxt)[2]) {
+    constexpr int STG = decltype(stg)::value;
     fa2_wait_vm_lgkm0<kFa2NLD * (kFa2D - 1)>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue_tile(t + 1 + kFa2D);
+    issue_tile(t + 1 + kFa2D, (STG + 1 + kFa2D) % kFa2S);
     if (t >= ntw) return;
-    const char* kt_next = sb + ((t + 1) % kFa2S) * 2 * kFa2Tile;
-    const char* vt = sb + (t % kFa2S) * 2 * kFa2Tile + kFa2Tile;
+    const char* kt_next = sb + ((STG + 1) % kFa2S) * 2 * kFa2Tile;
+    const char* vt = sb + STG * 2 * kFa2Tile + kFa2Tile;
     if (t + 1 < ntw) fa2_scores<BF16>(kt_next, qf, s_nxt);
     const int j0 = t * kFa2BK;
     const bool need_mask = (CAUSAL && j0 + kFa2BK - 1 > q0w) || (j0 + kFa2BK > P.Sk);
@@ -618,12 +621,21 @@ __global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint
     fa2_softmax<BF16, CAUSAL, ROUND_S>(s_cur, j0, qi, P.Sk, need_mask, sl2, m_run, l_run, acc, pf);
     fa2_pv<BF16>(vt, pf, acc);
   };
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  using C3 = std::integral_constant<int, 3>;
+  static_assert(kFa2S == 4, "main loop unrolled by the ring size");
   int t = 0;
-  for (; t + 1 < nt; t += 2) {
-    step(t, s_a, s_b);
-    step(t + 1, s_b, s_a);
+  for (; t + 3 < nt; t += 4) {
+    step(C0{}, t, s_a, s_b);
+    step(C1{}, t + 1, s_b, s_a);
+    step(C2{}, t + 2, s_a, s_b);
+    step(C3{}, t + 3, s_b, s_a);
   }
-  if (t < nt) step(t, s_a, s_b);
+  if (t < nt) step(C0{}, t, s_a, s_b);
+  if (t + 1 < nt) step(C1{}, t + 1, s_b, s_a);
+  if (t + 2 < nt) step(C2{}, t + 2, s_a, s_b);
 
   // O = acc / l.  O^T layout: lane = query column, register e holds d row
   // 8*(e/4) + 4*hi + e%4 (+ 32*db): four consecutive d per (e/4) group.

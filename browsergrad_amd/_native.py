@@ -141,6 +141,9 @@ SIGNATURES = {
     "bg_reshape": (C.c_int, [ctx_p, handle_t, P64, C.c_int, PH]),
     "bg_reduce_last": (C.c_int, [ctx_p, handle_t, C.c_int64, C.c_int64, C.c_int, C.c_int, PH]),
     "bg_run_tensor_plan": (C.c_int, [ctx_p, C.c_char_p, P64, PH, C.c_int, C.c_int, C.c_void_p, C.c_size_t, PH]),
+    "bg_run_tensor_plan_semantic": (C.c_int, [ctx_p, C.c_char_p, C.c_char_p, P64, PH, C.c_int, C.c_int,
+                                              C.c_void_p, C.c_size_t, PH]),
+    "bg_softmax_last": (C.c_int, [ctx_p, handle_t, C.c_int64, C.c_int64, C.c_int, PH]),
     "bg_device_ptr": (C.c_int, [ctx_p, handle_t, C.POINTER(C.c_void_p)]),
     "bg_stream": (C.c_int, [ctx_p, C.POINTER(C.c_void_p)]),
 }

@@ -22,6 +22,7 @@ Handles are plain ints minted by the library (from 1, never reused).
 from __future__ import annotations
 
 import ctypes as C
+import json
 from typing import Any, Optional, Sequence, Tuple
 
 import numpy as np
@@ -59,7 +60,8 @@ class HipRealizerBridge:
         self._ctx = ctx
         self.device = device
         self.profiling = profiling
-        self.counters = {"upload": 0, "materialize": 0, "release": 0}
+        self.counters = {"upload": 0, "materialize": 0, "release": 0, "matmul": 0}
+        self._semantic_traces: dict = {}
 
     # -- lifecycle -----------------------------------------------------------
     def close(self) -> None:
@@ -147,6 +149,7 @@ class HipRealizerBridge:
 
     # -- compute (realizer.ts:1043-1151) ------------------------------------------
     def matmul(self, a: int, b: int, m: int, k: int, n: int, dtype: str) -> int:
+        self.counters["matmul"] += 1
         out = N.handle_t()
         self._check(self._lib.bg_matmul(self._ctx, int(a), int(b), int(m), int(k), int(n),
                                         _dtype_code(dtype, "matmul"), C.byref(out)))
@@ -288,6 +291,134 @@ class HipRealizerBridge:
         self._check(self._lib.bg_reduce_last(self._ctx, int(x), int(rows), int(cols), int(op),
                                              1 if keepdims else 0, C.byref(out)))
         return int(out.value)
+
+    def softmax_last(self, x: int, rows: int, cols: int, out_dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_softmax_last(self._ctx, int(x), int(rows), int(cols),
+                                              _dtype_code(out_dtype, "softmax"), C.byref(out)))
+        return int(out.value)
+
+    # -- tensor-plan route (realizer.ts:1557-1652) -------------------------------------
+    def _plan_inputs(self, plan: dict, inputs: Sequence[Any]) -> Tuple[list, list, list]:
+        """normalizeTensorPlanInputs (realizer.ts:857-892): each input is
+        {value_id|valueId, data: bytes} (uploaded here, released after the
+        run) or {value_id|valueId, handle} (resident, borrowed)."""
+        steps = {int(st.get("value_id", st.get("valueId"))): st for st in plan.get("steps", [])}
+        ids, handles, temps = [], [], []
+        try:
+            for i, inp in enumerate(inputs):
+                if not isinstance(inp, dict):
+                    raise KernelError(f"HIP bridge: tensor plan input {i} must be an object")
+                raw_id = inp.get("valueId", inp.get("value_id"))
+                if not isinstance(raw_id, (int, np.integer)) or isinstance(raw_id, bool):
+                    raise KernelError(f"HIP bridge: tensor plan input {i}.valueId must be an integer")
+                vid = int(raw_id)
+                if inp.get("handle") is not None:
+                    h = inp["handle"]
+                    if not isinstance(h, (int, np.integer)) or isinstance(h, bool):
+                        raise KernelError(f"HIP bridge: tensor plan input {i}.handle must be an integer")
+                    ids.append(vid)
+                    handles.append(int(h))
+                    continue
+                data = inp.get("data")
+                if not isinstance(data, (bytes, bytearray, memoryview)):
+                    raise KernelError(f"HIP bridge: tensor plan input {i}.data must be bytes")
+                step = steps.get(vid)
+                dtype = str(step["dtype"]) if step is not None else "float32"
+                width = N.DTYPE_SIZES[_dtype_code(dtype, "tensor plan input")]
+                nbytes = len(memoryview(data).cast("B"))
+                if nbytes % width:
+                    raise KernelError(
+                        f"HIP bridge: tensor plan input {i}.data byte length must be divisible by {width}")
+                shape = (nbytes // width,)
+                if step is not None and int(np.prod(step["shape"], dtype=np.int64)) == nbytes // width:
+                    shape = _shape(step["shape"])
+                h = self.upload(data, shape, dtype)
+                temps.append(h)
+                ids.append(vid)
+                handles.append(h)
+        except BaseException:
+            for h in temps:
+                self.release(h)
+            raise
+        return ids, handles, temps
+
+    @staticmethod
+    def _plan_json(plan: Any) -> Tuple[dict, bytes]:
+        """(parsed plan for input binding, wire text).  Text that does not
+        parse here still goes to the library, whose reader reports it."""
+        if isinstance(plan, (str, bytes)):
+            text = plan.decode() if isinstance(plan, bytes) else plan
+            try:
+                obj = json.loads(text)
+            except ValueError:
+                obj = {}
+            return (obj if isinstance(obj, dict) else {}), text.encode()
+        return plan, json.dumps(plan, separators=(",", ":")).encode()
+
+    def _run_plan(self, plan: Any, requests: Optional[Any], inputs: Sequence[Any], dtype: str,
+                  resident: bool) -> Any:
+        plan_obj, plan_text = self._plan_json(plan)
+        if requests is None:
+            req_text = None
+        elif isinstance(requests, bytes):
+            req_text = requests
+        elif isinstance(requests, str):
+            req_text = requests.encode()
+        else:
+            req_text = json.dumps(requests).encode()
+        code = _dtype_code(dtype, "run_tensor_plan")
+        ids, handles, temps = self._plan_inputs(plan_obj, inputs)
+        try:
+            root = N.handle_t()
+            if resident or "steps" not in plan_obj:
+                dst, nbytes = None, 0
+            else:
+                root_id = plan_obj.get("root_id", plan_obj.get("rootId"))
+                root_step = next((st for st in plan_obj["steps"]
+                                  if st.get("value_id", st.get("valueId")) == root_id), None)
+                if root_step is None:  # malformed plan: let the library name the problem
+                    raise KernelError(f"HIP bridge: tensor plan root {root_id} missing from steps")
+                shape = _shape(root_step["shape"])
+                n = int(np.prod(shape, dtype=np.int64)) if shape else 1
+                nbytes = n * N.DTYPE_SIZES[_dtype_code(root_step["dtype"], "run_tensor_plan")]
+                buf = C.create_string_buffer(max(nbytes, 1))
+                dst = C.cast(buf, C.c_void_p)
+            args = (N.i64_array(ids), N.handle_array(handles), len(ids), code, dst, nbytes, C.byref(root))
+            if req_text is None:
+                self._check(self._lib.bg_run_tensor_plan(self._ctx, plan_text, *args))
+            else:
+                self._check(self._lib.bg_run_tensor_plan_semantic(self._ctx, plan_text, req_text, *args))
+        finally:
+            for h in temps:
+                self.release(h)
+        if resident:
+            return int(root.value)
+        return bytes(buf.raw[:nbytes])
+
+    def run_tensor_plan(self, plan: Any, inputs: Sequence[Any], dtype: str) -> bytes:
+        return self._run_plan(plan, None, inputs, dtype, resident=False)
+
+    def run_tensor_plan_resident(self, plan: Any, inputs: Sequence[Any], dtype: str) -> int:
+        return self._run_plan(plan, None, inputs, dtype, resident=True)
+
+    def run_tensor_plan_semantic(self, plan: Any, semantic_requests: Any, inputs: Sequence[Any],
+                                 dtype: str) -> bytes:
+        return self._run_plan(plan, semantic_requests, inputs, dtype, resident=False)
+
+    def run_tensor_plan_resident_semantic(self, plan: Any, semantic_requests: Any, inputs: Sequence[Any],
+                                          dtype: str) -> int:
+        h = self._run_plan(plan, semantic_requests, inputs, dtype, resident=True)
+        req = json.loads(semantic_requests) if isinstance(semantic_requests, (str, bytes)) else semantic_requests
+        self._semantic_traces[h] = {"preparation": req}
+        return h
+
+    def semanticTensorPlanExecutionTrace(self, handle: int) -> dict:  # noqa: N802 - reference name
+        """realizer.ts:1654-1667: the preparation bound to a resident semantic root."""
+        trace = self._semantic_traces.get(int(handle))
+        if trace is None:
+            raise KernelError(f"HIP bridge: handle {handle} has no semantic tensor-plan execution trace")
+        return trace
 
     def synchronize(self) -> None:
         self._check(self._lib.bg_synchronize(self._ctx))

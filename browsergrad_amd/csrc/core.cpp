@@ -883,13 +883,16 @@ int bg_flash_attention(bg_ctx* ctx, bg_handle q, bg_handle k, bg_handle v,
   BG_API_END
 }
 
-int bg_run_tensor_plan(bg_ctx* ctx, const char* plan_json,
-                       const int64_t* input_ids, const bg_handle* input_handles,
-                       int n_inputs, int dtype, void* dst, size_t dst_nbytes,
-                       bg_handle* root_out) {
+static int run_plan_abi(bg_ctx* ctx, const char* plan_json, const char* requests_json,
+                        const int64_t* input_ids, const bg_handle* input_handles, int n_inputs,
+                        int dtype, void* dst, size_t dst_nbytes, bg_handle* root_out) {
   BG_API_BEGIN
   if (!plan_json) fail(BG_E_INVALID, "run_tensor_plan: plan is NULL");
-  bg_handle root = run_plan(ctx, plan_json, input_ids, input_handles, n_inputs, dtype);
+  if (n_inputs < 0 || (n_inputs > 0 && (!input_ids || !input_handles)))
+    fail(BG_E_INVALID, "run_tensor_plan: bad input arrays");
+  if (!dst && !root_out) fail(BG_E_INVALID, "run_tensor_plan: neither dst nor root_out given");
+  bg_handle root = run_plan(ctx, plan_json, requests_json, input_ids, input_handles, n_inputs, dtype,
+                            dst == nullptr);
   if (dst) {
     int rc = bg_materialize(ctx, root, dst, dst_nbytes);
     if (rc != BG_OK) {
@@ -900,12 +903,50 @@ int bg_run_tensor_plan(bg_ctx* ctx, const char* plan_json,
     bg_release(ctx, root);
     if (root_out) *root_out = 0;
   } else {
-    if (!root_out) {
-      bg_release(ctx, root);
-      fail(BG_E_INVALID, "run_tensor_plan: neither dst nor root_out given");
-    }
     *root_out = root;
   }
+  BG_API_END
+}
+
+int bg_run_tensor_plan(bg_ctx* ctx, const char* plan_json,
+                       const int64_t* input_ids, const bg_handle* input_handles,
+                       int n_inputs, int dtype, void* dst, size_t dst_nbytes,
+                       bg_handle* root_out) {
+  return run_plan_abi(ctx, plan_json, nullptr, input_ids, input_handles, n_inputs, dtype, dst, dst_nbytes,
+                      root_out);
+}
+
+int bg_run_tensor_plan_semantic(bg_ctx* ctx, const char* plan_json, const char* requests_json,
+                                const int64_t* input_ids, const bg_handle* input_handles, int n_inputs,
+                                int dtype, void* dst, size_t dst_nbytes, bg_handle* root_out) {
+  if (!requests_json) {
+    if (ctx) ctx->err = "run_tensor_plan_semantic: requests are NULL";
+    return BG_E_INVALID;
+  }
+  return run_plan_abi(ctx, plan_json, requests_json, input_ids, input_handles, n_inputs, dtype, dst,
+                      dst_nbytes, root_out);
+}
+
+int bg_softmax_last(bg_ctx* ctx, bg_handle x, int64_t rows, int64_t cols, int out_dtype, bg_handle* out) {
+  BG_API_BEGIN
+  if (!out) fail(BG_E_INVALID, "softmax: NULL output");
+  Record& rx = get(ctx, x, "softmax[x]");
+  if (rows < 0 || cols <= 0 || rows * cols != rx.numel()) fail(BG_E_SHAPE, "softmax: rows*cols does not match x");
+  if (rx.dtype != BG_F32 && rx.dtype != BG_F16 && rx.dtype != BG_BF16)
+    fail(BG_E_DTYPE, "softmax: x dtype not supported");
+  if (out_dtype != BG_F32 && out_dtype != BG_F16 && out_dtype != BG_BF16)
+    fail(BG_E_DTYPE, "softmax: out dtype not supported");
+  bg_handle o = mint(ctx, size_t(rows * cols * dtype_size(out_dtype)), rx.shape, out_dtype);
+  Record& ro = ctx->handles[o];
+  Record& rx2 = ctx->handles[x];
+  try {
+    Profile prof(ctx, "softmax", rows * cols * (dtype_size(rx2.dtype) + dtype_size(out_dtype)), 0);
+    launch_softmax_last(ctx, rx2.ptr(), rx2.dtype, ro.ptr(), out_dtype, rows, cols);
+  } catch (...) {
+    bg_release(ctx, o);
+    throw;
+  }
+  *out = o;
   BG_API_END
 }
 

@@ -162,6 +162,8 @@ void launch_layer_norm(bg_ctx* ctx, const void* x, int x_dtype,
                        int64_t rows, int64_t cols, float eps);
 void launch_reduce_last(bg_ctx* ctx, const void* x, int dtype, void* y,
                         int64_t rows, int64_t cols, int op);
+void launch_softmax_last(bg_ctx* ctx, const void* x, int x_dtype, void* y, int y_dtype,
+                         int64_t rows, int64_t cols);
 void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a,
                    const Record& b, const Record* bias, Record& out);
 void launch_attention(bg_ctx* ctx, const bg_attention_desc& d,
@@ -177,7 +179,9 @@ void launch_attention_masked_f32(bg_ctx* ctx, const float* q, const float* k,
                                  int64_t d, float scale);
 
 // Plan executor (plan.cpp).
-bg_handle run_plan(bg_ctx* ctx, const char* json, const int64_t* ids,
-                   const bg_handle* handles, int n, int dtype);
+// requests_json: the semantic permutation side table (NULL for the legacy
+// route); resident: the root must be an allocation of its own.
+bg_handle run_plan(bg_ctx* ctx, const char* json, const char* requests_json, const int64_t* ids,
+                   const bg_handle* handles, int n, int dtype, bool resident);
 
 }  // namespace bg

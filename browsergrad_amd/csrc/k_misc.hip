@@ -106,6 +106,66 @@ __global__ void __launch_bounds__(256) copy_strided_kernel(const T* __restrict__
   }
 }
 
+// ---- Softmax over the last axis (FUSED_SOFTMAX) -------------------------------
+// The reference kernel's order (kernels/softmax.ts:22-69): m = max(x);
+// e = exp(x - m); y = e * (1 / sum(e)).  One wavefront per row, the row held
+// in registers (PER values per lane); rows wider than 64*PER stream three
+// times through memory.
+
+template <int PER>
+__global__ void __launch_bounds__(256) softmax_rows_kernel(const void* __restrict__ x, int xd,
+                                                           void* __restrict__ y, int yd, int64_t rows,
+                                                           int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // no block-level barriers below
+  const int64_t base = row * cols;
+  float v[PER];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t c = int64_t(j) * 64 + lane;
+    v[j] = c < cols ? load_as_f32(x, xd, base + c) : -INFINITY;
+    m = fmaxf(m, v[j]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t c = int64_t(j) * 64 + lane;
+    const float e = c < cols ? expf(v[j] - m) : 0.f;
+    v[j] = e;
+    s += e;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t c = int64_t(j) * 64 + lane;
+    if (c < cols) store_from_f32(y, yd, base + c, v[j] * inv);
+  }
+}
+
+__global__ void __launch_bounds__(256) softmax_rows_wide_kernel(const void* __restrict__ x, int xd,
+                                                                void* __restrict__ y, int yd, int64_t rows,
+                                                                int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float m = -INFINITY;
+  for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, load_as_f32(x, xd, base + c));
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) s += expf(load_as_f32(x, xd, base + c) - m);
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float inv = 1.0f / s;
+  for (int64_t c = lane; c < cols; c += 64)
+    store_from_f32(y, yd, base + c, expf(load_as_f32(x, xd, base + c) - m) * inv);
+}
+
 // ---- LayerNorm -----------------------------------------------------------------
 // Same arithmetic as the oracle: mean = sum/cols; centered = x - mean;
 // var = sum(centered^2)/cols; inv = 1/sqrt(var + eps); y = centered*inv*w + b,
@@ -413,6 +473,20 @@ void launch_gelu_rows(bg_ctx* ctx, const float* src, int64_t ld_src, int64_t str
   const unsigned grid = unsigned(std::min<int64_t>(total, 65536));
   bg::dispatch(ctx, gelu_rows_kernel, dim3(grid), dim3(256), 0, src, ld_src, stride_src, dst, ld_dst,
                stride_dst, dst_dtype, rows, cols, total);
+}
+
+void launch_softmax_last(bg_ctx* ctx, const void* x, int xd, void* y, int yd, int64_t rows, int64_t cols) {
+  if (rows == 0) return;
+  const dim3 grid(unsigned((rows + 3) / 4));
+  if (cols <= 256) {
+    bg::dispatch(ctx, softmax_rows_kernel<4>, grid, dim3(256), 0, x, xd, y, yd, rows, cols);
+  } else if (cols <= 1024) {
+    bg::dispatch(ctx, softmax_rows_kernel<16>, grid, dim3(256), 0, x, xd, y, yd, rows, cols);
+  } else if (cols <= 2048) {
+    bg::dispatch(ctx, softmax_rows_kernel<32>, grid, dim3(256), 0, x, xd, y, yd, rows, cols);
+  } else {
+    bg::dispatch(ctx, softmax_rows_wide_kernel, grid, dim3(256), 0, x, xd, y, yd, rows, cols);
+  }
 }
 
 void launch_layer_norm(bg_ctx* ctx, const void* x, int xd, const float* w, const float* b,

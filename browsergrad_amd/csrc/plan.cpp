@@ -1,12 +1,916 @@
-// Tensor-plan executor (placeholder until the JSON plan route lands).
+// Tensor-plan executor: the run_tensor_plan* route of the bridge.
+//
+// Reference: packages/browsergrad-kernels/src/tensor_plan.ts
+//   normalizeTensorGpuPlan  :135-181   (snake_case or camelCase fields)
+//   executeTensorGpuPlan    :301-373   (value table, early release)
+//   releaseDeadOwnedBuffers :375-409
+//   executeStep             :424-707   (per-op lowering)
+//   validatePlan            :3173-3195
+//   expectAxes / expectReduceSpec / expectFusedOps / expectFusedSoftmaxAxis
+//                           :3965-4038
+// and the semantic permutation side table of tensor_plan_semantics.ts:
+//   parseRequestEnvelope / parseDensePermutationRequest :381-467,
+//   verifyPlanProjection / compareShape :313-379.
+//
+// Every step becomes one (or, for REDUCE over non-trailing axes, two) calls
+// of this library's own entry points on the context stream, so a plan runs
+// back to back on the GPU with no host round trip until the root is
+// materialised.  Values are handles; LOAD / RESHAPE / f32->f32 CAST are
+// zero-copy views sharing the producer's allocation (reference-counted), so
+// releasing a value at its last use frees memory exactly when the last view
+// of it dies -- the reference's buffer-identity liveness rule.
+//
+// Beyond the reference's op set (which refuses CONST, CMP, WHERE, batched
+// MATMUL, broadcasting elementwise inputs and non-f32 values) the executor
+// also lowers:
+//   CONST            -> fused program {IMM}
+//   CMP / WHERE      -> fused programs with numpy broadcasting (bool results)
+//   ADD/MUL/DIV with broadcastable (not only equal-numel) inputs
+//   MATMUL rank > 2  -> batched GEMM (bg_matmul_ex), numpy batch broadcasting
+//   CAST between f32 / f16 / bf16 / bool
+// CONV*, LAYER_NORM_BACKWARD_* and the optimizer updates are refused with
+// BG_E_UNSUPPORTED naming the op.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <set>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
 #include "core.h"
 
 namespace bg {
+namespace {
 
-bg_handle run_plan(bg_ctx* ctx, const char* json, const int64_t* ids,
-                   const bg_handle* handles, int n, int dtype) {
-  (void)ctx; (void)json; (void)ids; (void)handles; (void)n; (void)dtype;
-  fail(BG_E_UNSUPPORTED, "run_tensor_plan: not available in this build");
+// ---- a small JSON reader ---------------------------------------------------
+
+struct JVal {
+  enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
+  bool b = false;
+  double num = 0;
+  bool is_int = false;  // written without fraction / exponent
+  std::string str;
+  std::vector<JVal> arr;
+  std::vector<std::pair<std::string, JVal>> obj;
+
+  const JVal* get(const char* key) const {
+    if (kind != Obj) return nullptr;
+    for (const auto& kv : obj)
+      if (kv.first == key) return &kv.second;
+    return nullptr;
+  }
+  // snake_case or camelCase (tensor_plan.ts:139-180 accepts both)
+  const JVal* get2(const char* snake, const char* camel) const {
+    const JVal* v = get(camel);
+    return v && v->kind != Null ? v : get(snake);
+  }
+};
+
+class JsonReader {
+ public:
+  explicit JsonReader(const char* s, const char* what) : p_(s), what_(what) {}
+  JVal parse() {
+    JVal v = value(0);
+    ws();
+    if (*p_) err("trailing characters");
+    return v;
+  }
+
+ private:
+  const char* p_;
+  const char* what_;
+
+  [[noreturn]] void err(const char* m) { fail(BG_E_INVALID, std::string(what_) + " must be valid JSON: " + m); }
+  void ws() {
+    while (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r') ++p_;
+  }
+  bool lit(const char* w) {
+    size_t n = std::strlen(w);
+    if (std::strncmp(p_, w, n) == 0) {
+      p_ += n;
+      return true;
+    }
+    return false;
+  }
+  JVal value(int depth) {
+    if (depth > 64) err("nesting too deep");
+    ws();
+    JVal v;
+    if (*p_ == '{') {
+      ++p_;
+      v.kind = JVal::Obj;
+      ws();
+      if (*p_ == '}') {
+        ++p_;
+        return v;
+      }
+      for (;;) {
+        ws();
+        if (*p_ != '"') err("object key expected");
+        std::string k = string();
+        ws();
+        if (*p_ != ':') err("':' expected");
+        ++p_;
+        v.obj.emplace_back(std::move(k), value(depth + 1));
+        ws();
+        if (*p_ == ',') {
+          ++p_;
+          continue;
+        }
+        if (*p_ == '}') {
+          ++p_;
+          return v;
+        }
+        err("',' or '}' expected");
+      }
+    }
+    if (*p_ == '[') {
+      ++p_;
+      v.kind = JVal::Arr;
+      ws();
+      if (*p_ == ']') {
+        ++p_;
+        return v;
+      }
+      for (;;) {
+        v.arr.push_back(value(depth + 1));
+        ws();
+        if (*p_ == ',') {
+          ++p_;
+          continue;
+        }
+        if (*p_ == ']') {
+          ++p_;
+          return v;
+        }
+        err("',' or ']' expected");
+      }
+    }
+    if (*p_ == '"') {
+      v.kind = JVal::Str;
+      v.str = string();
+      return v;
+    }
+    if (lit("true")) {
+      v.kind = JVal::Bool;
+      v.b = true;
+      return v;
+    }
+    if (lit("false")) {
+      v.kind = JVal::Bool;
+      return v;
+    }
+    if (lit("null")) return v;
+    // Python's json.dumps writes these for non-finite floats.
+    if (lit("NaN")) {
+      v.kind = JVal::Num;
+      v.num = NAN;
+      return v;
+    }
+    if (lit("Infinity")) {
+      v.kind = JVal::Num;
+      v.num = INFINITY;
+      return v;
+    }
+    if (lit("-Infinity")) {
+      v.kind = JVal::Num;
+      v.num = -INFINITY;
+      return v;
+    }
+    const char* start = p_;
+    if (*p_ == '-') ++p_;
+    if (!(*p_ >= '0' && *p_ <= '9')) err("value expected");
+    bool integral = true;
+    while ((*p_ >= '0' && *p_ <= '9') || *p_ == '.' || *p_ == 'e' || *p_ == 'E' || *p_ == '+' || *p_ == '-') {
+      if (*p_ == '.' || *p_ == 'e' || *p_ == 'E') integral = false;
+      ++p_;
+    }
+    v.kind = JVal::Num;
+    v.num = std::strtod(std::string(start, p_).c_str(), nullptr);
+    v.is_int = integral;
+    return v;
+  }
+  std::string string() {
+    ++p_;  // opening quote
+    std::string out;
+    while (*p_ && *p_ != '"') {
+      if (*p_ == '\\') {
+        ++p_;
+        switch (*p_) {
+          case '"': out += '"'; break;
+          case '\\': out += '\\'; break;
+          case '/': out += '/'; break;
+          case 'b': out += '\b'; break;
+          case 'f': out += '\f'; break;
+          case 'n': out += '\n'; break;
+          case 'r': out += '\r'; break;
+          case 't': out += '\t'; break;
+          case 'u': {
+            unsigned cp = 0;
+            for (int i = 1; i <= 4; ++i) {
+              char c = p_[i];
+              cp <<= 4;
+              if (c >= '0' && c <= '9') cp |= unsigned(c - '0');
+              else if (c >= 'a' && c <= 'f') cp |= unsigned(c - 'a' + 10);
+              else if (c >= 'A' && c <= 'F') cp |= unsigned(c - 'A' + 10);
+              else err("bad \\u escape");
+            }
+            p_ += 4;
+            if (cp < 0x80) out += char(cp);
+            else if (cp < 0x800) {
+              out += char(0xC0 | (cp >> 6));
+              out += char(0x80 | (cp & 0x3F));
+            } else {
+              out += char(0xE0 | (cp >> 12));
+              out += char(0x80 | ((cp >> 6) & 0x3F));
+              out += char(0x80 | (cp & 0x3F));
+            }
+            break;
+          }
+          default: err("bad escape");
+        }
+        ++p_;
+      } else {
+        out += *p_++;
+      }
+    }
+    if (*p_ != '"') err("unterminated string");
+    ++p_;
+    return out;
+  }
+};
+
+// ---- plan model (tensor_plan.ts:63-97) -------------------------------------
+
+struct Step {
+  int64_t step = 0;
+  int64_t value_id = 0;
+  std::string op;
+  std::vector<int64_t> inputs;
+  std::vector<int64_t> shape;
+  std::string dtype;
+  const JVal* arg = nullptr;  // may be null / JSON null
+};
+
+struct Plan {
+  std::vector<Step> steps;
+  int64_t root_id = 0;
+  int64_t peak_live_bytes = 0;
+};
+
+[[noreturn]] void plan_fail(const std::string& m, int code = BG_E_INVALID) { fail(code, "tensor plan " + m); }
+
+int64_t expect_int(const JVal* v, const std::string& name) {
+  if (!v || v->kind != JVal::Num || !std::isfinite(v->num) || v->num != std::floor(v->num))
+    fail(BG_E_INVALID, name + " must be an integer");
+  return int64_t(v->num);
+}
+
+const JVal& expect_arr(const JVal* v, const std::string& name) {
+  if (!v || v->kind != JVal::Arr) fail(BG_E_INVALID, name + " must be an array");
+  return *v;
+}
+
+std::vector<int64_t> int_list(const JVal* v, const std::string& name) {
+  const JVal& a = expect_arr(v, name);
+  std::vector<int64_t> out;
+  for (size_t i = 0; i < a.arr.size(); ++i) out.push_back(expect_int(&a.arr[i], name + "[" + std::to_string(i) + "]"));
+  return out;
+}
+
+// Value dtypes this executor handles.  The reference accepts "float32" only
+// (expectFloat32, tensor_plan.ts:4040-4043); the others are extensions.
+int plan_dtype(const std::string& s, const std::string& where) {
+  if (s == "float32") return BG_F32;
+  if (s == "float16") return BG_F16;
+  if (s == "bfloat16") return BG_BF16;
+  if (s == "bool") return BG_BOOL;
+  fail(BG_E_DTYPE, where + " must be \"float32\" (or float16 / bfloat16 / bool), got \"" + s + "\"");
+}
+
+Plan normalize(const JVal& root) {
+  if (root.kind != JVal::Obj) plan_fail("must be an object");
+  Plan p;
+  const JVal& steps = expect_arr(root.get("steps"), "tensor plan.steps");
+  for (size_t i = 0; i < steps.arr.size(); ++i) {
+    const JVal& s = steps.arr[i];
+    const std::string at = "steps[" + std::to_string(i) + "]";
+    if (s.kind != JVal::Obj) fail(BG_E_INVALID, "tensor plan." + at + " must be an object");
+    Step st;
+    st.step = expect_int(s.get("step"), at + ".step");
+    st.value_id = expect_int(s.get2("value_id", "valueId"), at + ".valueId");
+    const JVal* op = s.get("op");
+    if (!op || op->kind != JVal::Str) fail(BG_E_INVALID, at + ".op must be a string");
+    st.op = op->str;
+    st.inputs = int_list(s.get2("input_ids", "inputIds"), at + ".inputIds");
+    st.shape = int_list(s.get("shape"), at + ".shape");
+    for (int64_t d : st.shape)
+      if (d < 0) fail(BG_E_INVALID, at + ".shape has a negative extent");
+    const JVal* dt = s.get("dtype");
+    if (!dt || dt->kind != JVal::Str) fail(BG_E_INVALID, at + ".dtype must be a string");
+    st.dtype = dt->str;
+    plan_dtype(st.dtype, at + ".dtype");
+    st.arg = s.get("arg");
+    p.steps.push_back(std::move(st));
+  }
+  // buffers[] carries liveness metadata the executor recomputes from steps;
+  // it is still validated for shape like the reference does.
+  expect_arr(root.get("buffers"), "tensor plan.buffers");
+  p.root_id = expect_int(root.get2("root_id", "rootId"), "tensor plan.rootId");
+  const JVal* mb = root.get2("materialization_boundary", "materializationBoundary");
+  if (!mb || mb->kind != JVal::Str || mb->str != "root")
+    fail(BG_E_INVALID, "tensor plan.materializationBoundary must be \"root\"");
+  p.peak_live_bytes = expect_int(root.get2("peak_live_bytes", "peakLiveBytes"), "tensor plan.peakLiveBytes");
+  const JVal* hc = root.get2("has_custom_ops", "hasCustomOps");
+  if (!hc || hc->kind != JVal::Bool || hc->b) fail(BG_E_INVALID, "tensor plan.hasCustomOps must be false");
+  // validatePlan (tensor_plan.ts:3173-3195)
+  std::set<int64_t> seen;
+  for (const Step& st : p.steps) {
+    if (seen.count(st.value_id)) plan_fail("value " + std::to_string(st.value_id) + " produced twice");
+    for (int64_t in : st.inputs)
+      if (!seen.count(in))
+        plan_fail("step " + std::to_string(st.step) + " reads " + std::to_string(in) + " before production");
+    seen.insert(st.value_id);
+  }
+  if (!seen.count(p.root_id)) plan_fail("root " + std::to_string(p.root_id) + " missing from steps");
+  return p;
+}
+
+// ---- semantic permutation requests (tensor_plan_semantics.ts:381-467) ------
+
+struct PermRequest {
+  int64_t value_id;
+  std::vector<int64_t> input_shape;
+  std::vector<int64_t> axes;
+};
+
+[[noreturn]] void sem_fail(const std::string& path, const std::string& m) {
+  fail(BG_E_INVALID, "tensor plan semantic requests " + path + ": " + m);
+}
+
+void expect_closed(const JVal& v, std::vector<std::string> keys, const std::string& path) {
+  if (v.kind != JVal::Obj) sem_fail(path, "expected an object");
+  std::vector<std::string> actual;
+  for (const auto& kv : v.obj) actual.push_back(kv.first);
+  std::sort(actual.begin(), actual.end());
+  std::sort(keys.begin(), keys.end());
+  if (actual != keys) {
+    std::string all;
+    for (size_t i = 0; i < keys.size(); ++i) all += (i ? ", " : "") + keys[i];
+    sem_fail(path, "expected closed fields " + all);
+  }
+}
+
+int64_t safe_int(const JVal* v, const std::string& path) {
+  if (!v || v->kind != JVal::Num || !v->is_int || std::fabs(v->num) > 9007199254740991.0)
+    sem_fail(path, "expected a safe integer");
+  return int64_t(v->num);
+}
+
+// A WireI64 is canonical base-10 ASCII in a JSON string.
+int64_t wire_i64(const JVal& v, const std::string& path) {
+  const std::string& s = v.str;
+  bool ok = v.kind == JVal::Str && !s.empty();
+  if (ok) {
+    size_t i = s[0] == '-' ? 1 : 0;
+    ok = i < s.size() && !(s[i] == '0' && s.size() > i + 1) && !(s == "-0");
+    for (size_t j = i; ok && j < s.size(); ++j) ok = s[j] >= '0' && s[j] <= '9';
+    ok = ok && s.size() <= 20;
+  }
+  if (!ok)
+    fail(BG_E_INVALID, "tensor plan semantic requests " + path +
+                           ": WireI64 must be canonical ASCII base-10 without +, whitespace, leading zeroes, or -0");
+  const long double x = std::strtold(s.c_str(), nullptr);
+  if (x <= 0 || x > 9007199254740991.0L)
+    sem_fail(path, "extent must be positive and exactly representable by the frozen plan");
+  return int64_t(x);
+}
+
+std::vector<PermRequest> parse_requests(const char* text) {
+  if (std::strlen(text) > 512 * 1024) sem_fail("$", "JSON request envelope exceeds 524288 code units");
+  JVal env = JsonReader(text, "tensor plan semantic requests").parse();
+  expect_closed(env, {"schema", "version", "requests"}, "$");
+  const JVal* schema = env.get("schema");
+  if (schema->kind != JVal::Str || schema->str != "browsergrad.jit.tensor-plan-semantic-requests")
+    sem_fail("$.schema", "expected browsergrad.jit.tensor-plan-semantic-requests");
+  const JVal* ver = env.get("version");
+  expect_closed(*ver, {"major", "minor"}, "$.version");
+  if (ver->get("major")->kind != JVal::Num || ver->get("major")->num != 1 ||
+      ver->get("minor")->kind != JVal::Num || ver->get("minor")->num != 0)
+    sem_fail("$.version", "only semantic request version 1.0 is supported");
+  const JVal* reqs = env.get("requests");
+  if (reqs->kind != JVal::Arr) sem_fail("$.requests", "requests must be an array");
+  if (reqs->arr.size() > 4096) sem_fail("$.requests", "request count exceeds 4096");
+  std::vector<PermRequest> out;
+  for (size_t i = 0; i < reqs->arr.size(); ++i) {
+    const std::string path = "$.requests[" + std::to_string(i) + "]";
+    const JVal& r = reqs->arr[i];
+    expect_closed(r, {"kind", "valueId", "inputShape", "axes", "dtype"}, path);
+    if (r.get("kind")->kind != JVal::Str || r.get("kind")->str != "dense-permutation-view-copy")
+      sem_fail(path + ".kind", "expected dense-permutation-view-copy");
+    PermRequest q;
+    q.value_id = safe_int(r.get("valueId"), path + ".valueId");
+    if (q.value_id < 0) sem_fail(path + ".valueId", "valueId must be non-negative");
+    if (r.get("dtype")->kind != JVal::Str || r.get("dtype")->str != "f32")
+      sem_fail(path + ".dtype", "initial semantic permutation request requires f32");
+    const JVal* is = r.get("inputShape");
+    if (is->kind != JVal::Arr) sem_fail(path + ".inputShape", "inputShape must be an array");
+    if (is->arr.size() != 2 && is->arr.size() != 3)
+      sem_fail(path + ".inputShape", "initial semantic permutation request requires rank 2 or 3");
+    for (size_t a = 0; a < is->arr.size(); ++a)
+      q.input_shape.push_back(wire_i64(is->arr[a], path + ".inputShape[" + std::to_string(a) + "]"));
+    const JVal* ax = r.get("axes");
+    if (ax->kind != JVal::Arr || ax->arr.size() != q.input_shape.size())
+      sem_fail(path + ".axes", "axes must contain exactly one entry per input rank");
+    std::set<int64_t> seen;
+    for (size_t a = 0; a < ax->arr.size(); ++a) {
+      int64_t v = safe_int(&ax->arr[a], path + ".axes[" + std::to_string(a) + "]");
+      if (v < 0 || v >= int64_t(q.input_shape.size()) || seen.count(v))
+        sem_fail(path + ".axes", "axes must be an exact non-negative permutation");
+      seen.insert(v);
+      q.axes.push_back(v);
+    }
+    out.push_back(std::move(q));
+  }
+  return out;
+}
+
+// The request side table must match the plan's PERMUTE steps one to one, in
+// order, with the legacy axes erased from the plan (verifyPlanProjection).
+std::unordered_map<int64_t, std::vector<int64_t>> bind_requests(const Plan& p, const std::vector<PermRequest>& reqs) {
+  std::vector<const Step*> perms;
+  std::unordered_map<int64_t, const Step*> by_id;
+  for (const Step& s : p.steps) {
+    by_id[s.value_id] = &s;
+    if (s.op == "PERMUTE") perms.push_back(&s);
+  }
+  if (reqs.size() != perms.size())
+    sem_fail("$.requests", "expected exactly " + std::to_string(perms.size()) +
+                               " request(s) for plan PERMUTE steps, got " + std::to_string(reqs.size()));
+  std::unordered_map<int64_t, std::vector<int64_t>> axes;
+  for (size_t i = 0; i < reqs.size(); ++i) {
+    const std::string path = "$.requests[" + std::to_string(i) + "]";
+    const PermRequest& q = reqs[i];
+    const Step& st = *perms[i];
+    if (q.value_id != st.value_id)
+      sem_fail(path + ".valueId", "request order/valueId must match plan PERMUTE value " + std::to_string(st.value_id));
+    if (st.inputs.size() != 1) sem_fail(path + ".valueId", "plan PERMUTE must have exactly one input");
+    auto src = by_id.find(st.inputs[0]);
+    if (src == by_id.end()) sem_fail(path + ".valueId", "plan PERMUTE source is missing");
+    if (src->second->dtype != "float32" || st.dtype != "float32")
+      sem_fail(path + ".dtype", "plan projection must remain float32");
+    if (st.arg && st.arg->kind != JVal::Null)
+      sem_fail(path + ".valueId", "semantic-route PERMUTE must erase legacy arg meaning from the scheduling plan");
+    auto cmp = [&](const std::vector<int64_t>& sem, const std::vector<int64_t>& plan, const std::string& where) {
+      if (sem.size() != plan.size()) sem_fail(where, "semantic request and plan projection ranks differ");
+      for (size_t a = 0; a < sem.size(); ++a) {
+        if (plan[a] <= 0) sem_fail(where, "plan extent " + std::to_string(a) + " must be a positive safe integer");
+        if (sem[a] != plan[a])
+          sem_fail(where, "semantic request and plan projection differ at axis " + std::to_string(a));
+      }
+    };
+    cmp(q.input_shape, src->second->shape, path + ".inputShape");
+    std::vector<int64_t> expect_out;
+    for (int64_t a : q.axes) expect_out.push_back(q.input_shape[size_t(a)]);
+    cmp(expect_out, st.shape, path + ".axes");
+    axes[st.value_id] = q.axes;
+  }
+  return axes;
+}
+
+// ---- execution -------------------------------------------------------------
+
+struct Runner {
+  bg_ctx* ctx;
+  std::unordered_map<int64_t, bg_handle> vals;   // value_id -> handle
+  std::set<bg_handle> owned;                     // handles this run minted
+  std::set<bg_handle> inputs;                    // caller's handles (borrowed)
+  const std::unordered_map<int64_t, std::vector<int64_t>>* sem_axes = nullptr;
+
+  void call(int rc) {
+    if (rc != BG_OK) fail(rc, ctx->err);
+  }
+  bg_handle own(bg_handle h) {
+    owned.insert(h);
+    return h;
+  }
+  bg_handle need(const Step& s, size_t i) {
+    if (i >= s.inputs.size()) plan_fail(s.op + " missing input");
+    auto it = vals.find(s.inputs[i]);
+    if (it == vals.end()) plan_fail(s.op + " input " + std::to_string(s.inputs[i]) + " not resident");
+    return it->second;
+  }
+  const Record& rec(bg_handle h) { return ctx->handles.at(h); }
+
+  bg_handle view(bg_handle src, const std::vector<int64_t>& shape) {
+    bg_handle out = 0;
+    call(bg_reshape(ctx, src, shape.data(), int(shape.size()), &out));
+    return own(out);
+  }
+
+  // numpy broadcasting strides of `in` against output shape `out`.
+  static std::vector<int64_t> bstrides(const std::vector<int64_t>& in, const std::vector<int64_t>& out,
+                                       const std::string& op) {
+    if (in.size() > out.size()) plan_fail(op + " input rank exceeds output rank");
+    std::vector<int64_t> st(out.size(), 0);
+    int64_t stride = 1;
+    for (size_t k = 0; k < in.size(); ++k) {
+      size_t ii = in.size() - 1 - k, oo = out.size() - 1 - k;
+      if (in[ii] == out[oo]) st[oo] = in[ii] == 1 ? 0 : stride;
+      else if (in[ii] == 1) st[oo] = 0;
+      else plan_fail(op + " incompatible broadcast dim " + std::to_string(ii));
+      stride *= in[ii];
+    }
+    return st;
+  }
+
+  bg_handle fused(const Step& s, std::vector<bg_handle> ins, const std::vector<bg_fused_op>& ops,
+                  const std::vector<double>& imms, int out_dtype) {
+    std::vector<int64_t> strides;
+    bool all_equal = true;
+    for (bg_handle h : ins)
+      if (rec(h).numel() != numel(s.shape)) all_equal = false;
+    if (!all_equal)
+      for (bg_handle h : ins) {
+        auto st = bstrides(rec(h).shape, s.shape, s.op);
+        strides.insert(strides.end(), st.begin(), st.end());
+      }
+    bg_fused_desc d{};
+    d.n_inputs = int(ins.size());
+    d.inputs = ins.data();
+    d.in_strides = all_equal ? nullptr : strides.data();
+    d.n_ops = int(ops.size());
+    d.ops = ops.data();
+    d.n_imms = int(imms.size());
+    d.imms = imms.data();
+    std::vector<int64_t> shape = s.shape.empty() ? std::vector<int64_t>{1} : s.shape;
+    d.rank = int(shape.size());
+    d.shape = shape.data();
+    d.out_dtype = out_dtype;
+    bg_handle out = 0;
+    call(bg_fused_ex(ctx, &d, &out));
+    if (s.shape.empty()) ctx->handles[out].shape.clear();
+    return own(out);
+  }
+
+  static int opcode(const std::string& name, const std::string& where) {
+    static const std::unordered_map<std::string, int> m = {
+        {"ADD", BG_OP_ADD}, {"MUL", BG_OP_MUL}, {"DIV", BG_OP_DIV}, {"NEG", BG_OP_NEG},
+        {"EXP", BG_OP_EXP}, {"LOG", BG_OP_LOG},
+        // extensions
+        {"MAX", BG_OP_MAX}, {"MIN", BG_OP_MIN}, {"SUB", BG_OP_SUB}, {"TANH", BG_OP_TANH},
+        {"SQRT", BG_OP_SQRT}, {"ABS", BG_OP_ABS}, {"WHERE", BG_OP_WHERE},
+        {"CMP_EQ", BG_OP_CMP_EQ}, {"CMP_NE", BG_OP_CMP_NE}, {"CMP_LT", BG_OP_CMP_LT},
+        {"CMP_LE", BG_OP_CMP_LE}, {"CMP_GT", BG_OP_CMP_GT}, {"CMP_GE", BG_OP_CMP_GE}};
+    auto it = m.find(name);
+    if (it == m.end()) plan_fail(where + " unsupported fused opcode \"" + name + "\"");
+    return it->second;
+  }
+
+  static int cmp_code(const std::string& c) {
+    if (c == "eq") return BG_OP_CMP_EQ;
+    if (c == "ne") return BG_OP_CMP_NE;
+    if (c == "lt") return BG_OP_CMP_LT;
+    if (c == "le") return BG_OP_CMP_LE;
+    if (c == "gt") return BG_OP_CMP_GT;
+    if (c == "ge") return BG_OP_CMP_GE;
+    plan_fail("CMP unknown comparison \"" + c + "\"");
+  }
+
+  static std::vector<int64_t> axes_arg(const Step& s, size_t rank) {
+    if (!s.arg || s.arg->kind != JVal::Obj) plan_fail(s.op + ".arg must be an object");
+    const JVal& a = expect_arr(s.arg->get("axes"), "tensor plan " + s.op + ".arg.axes");
+    if (a.arr.size() != rank) plan_fail(s.op + " axes length must equal rank");
+    std::vector<int64_t> out;
+    std::set<int64_t> seen;
+    for (size_t i = 0; i < a.arr.size(); ++i) {
+      int64_t n = expect_int(&a.arr[i], "tensor plan " + s.op + ".arg.axes[" + std::to_string(i) + "]");
+      if (n < 0 || n >= int64_t(rank))
+        plan_fail(s.op + " axis " + std::to_string(n) + " out of range for rank " + std::to_string(rank));
+      if (seen.count(n)) plan_fail(s.op + " duplicate axis " + std::to_string(n));
+      seen.insert(n);
+      out.push_back(n);
+    }
+    return out;
+  }
+
+  bg_handle permute(bg_handle src, const std::vector<int64_t>& axes) {
+    const Record& r = rec(src);
+    std::vector<int64_t> cstr(r.shape.size(), 1);
+    for (int i = int(r.shape.size()) - 2; i >= 0; --i) cstr[i] = cstr[i + 1] * r.shape[i + 1];
+    std::vector<int64_t> shape, strides;
+    for (int64_t a : axes) {
+      shape.push_back(r.shape[size_t(a)]);
+      strides.push_back(cstr[size_t(a)]);
+    }
+    bg_handle out = 0;
+    call(bg_copy_strided(ctx, src, 0, shape.data(), strides.data(), int(shape.size()), &out));
+    return own(out);
+  }
+
+  bg_handle exec(const Step& s) {
+    const std::string& op = s.op;
+    const int dt = plan_dtype(s.dtype, "steps[" + std::to_string(s.step) + "].dtype");
+    if (op == "BUFFER") {
+      auto it = vals.find(s.value_id);  // pre-bound by the caller
+      if (it == vals.end()) plan_fail("missing BUFFER input " + std::to_string(s.value_id));
+      const Record& r = rec(it->second);
+      if (r.numel() != numel(s.shape))
+        fail(BG_E_SHAPE, "BUFFER " + std::to_string(s.value_id) + " data length " + std::to_string(r.numel()) +
+                             " does not match shape (" + std::to_string(numel(s.shape)) + ")");
+      if (r.dtype != dt) fail(BG_E_DTYPE, "BUFFER " + std::to_string(s.value_id) + " dtype differs from the plan");
+      return it->second;
+    }
+    if (op == "LOAD" || op == "RESHAPE") {
+      bg_handle src = need(s, 0);
+      if (rec(src).numel() != numel(s.shape)) plan_fail(op + " cannot change numel");
+      return view(src, s.shape);
+    }
+    if (op == "CAST") {
+      bg_handle src = need(s, 0);
+      const Record& r = rec(src);
+      if (r.dtype == dt) return view(src, s.shape);
+      bg_handle out = 0;
+      call(bg_cast(ctx, src, r.dtype, dt, s.shape.data(), int(s.shape.size()), &out));
+      return own(out);
+    }
+    if (op == "CONST") {
+      if (!s.arg || s.arg->kind != JVal::Obj) plan_fail("CONST.arg must be an object");
+      const JVal* v = s.arg->get("value");
+      if (!v || (v->kind != JVal::Num && v->kind != JVal::Bool)) plan_fail("CONST.arg.value must be a number");
+      double x = v->kind == JVal::Bool ? (v->b ? 1.0 : 0.0) : v->num;
+      return fused(s, {}, {{BG_OP_IMM, 0, 0, 0}}, {x}, dt);
+    }
+    if (op == "ADD" || op == "MUL" || op == "DIV") {
+      if (s.inputs.size() != 2) plan_fail(op + " expected 2 inputs");
+      return fused(s, {need(s, 0), need(s, 1)}, {{opcode(op, op), -1, -2, 0}}, {}, dt);
+    }
+    if (op == "NEG" || op == "EXP" || op == "LOG") {
+      if (s.inputs.size() != 1) plan_fail(op + " expected 1 inputs");
+      return fused(s, {need(s, 0)}, {{opcode(op, op), -1, -1, 0}}, {}, dt);
+    }
+    if (op == "CMP") {
+      if (s.inputs.size() != 2) plan_fail("CMP expected 2 inputs");
+      if (!s.arg || s.arg->kind != JVal::Obj || !s.arg->get("op") || s.arg->get("op")->kind != JVal::Str)
+        plan_fail("CMP.arg.op must be a string");
+      return fused(s, {need(s, 0), need(s, 1)}, {{cmp_code(s.arg->get("op")->str), -1, -2, 0}}, {}, BG_BOOL);
+    }
+    if (op == "WHERE") {
+      if (s.inputs.size() != 3) plan_fail("WHERE expected 3 inputs");
+      return fused(s, {need(s, 0), need(s, 1), need(s, 2)}, {{BG_OP_WHERE, -1, -2, -3}}, {}, dt);
+    }
+    if (op == "FUSED_ELEMENTWISE") {
+      if (!s.arg || s.arg->kind != JVal::Obj) plan_fail("FUSED_ELEMENTWISE.arg must be an object");
+      const JVal& ops = expect_arr(s.arg->get("ops"), "tensor plan FUSED_ELEMENTWISE.arg.ops");
+      std::vector<bg_fused_op> prog;
+      for (size_t i = 0; i < ops.arr.size(); ++i) {
+        const std::string at = "FUSED_ELEMENTWISE.arg.ops[" + std::to_string(i) + "]";
+        const JVal& it = ops.arr[i];
+        if (it.kind != JVal::Arr || it.arr.size() < 2 || it.arr.size() > 4)
+          plan_fail(at + " must be [opcode, lhs, rhs?]");
+        if (it.arr[0].kind != JVal::Str) plan_fail(at + "[0] must be a string");
+        int code = opcode(it.arr[0].str, at);
+        int32_t a = int32_t(expect_int(&it.arr[1], "tensor plan " + at + "[1]"));
+        int32_t b = a, c = 0;
+        if (it.arr.size() >= 3 && it.arr[2].kind != JVal::Null) b = int32_t(expect_int(&it.arr[2], "tensor plan " + at + "[2]"));
+        if (it.arr.size() == 4 && it.arr[3].kind != JVal::Null) c = int32_t(expect_int(&it.arr[3], "tensor plan " + at + "[3]"));
+        prog.push_back({code, a, b, c});
+      }
+      std::vector<bg_handle> ins;
+      for (size_t i = 0; i < s.inputs.size(); ++i) ins.push_back(need(s, i));
+      return fused(s, ins, prog, {}, dt);
+    }
+    if (op == "MATMUL") return matmul(s, dt);
+    if (op == "PERMUTE") {
+      bg_handle src = need(s, 0);
+      std::vector<int64_t> axes;
+      if (sem_axes) {
+        auto it = sem_axes->find(s.value_id);
+        if (it == sem_axes->end())
+          plan_fail("PERMUTE value " + std::to_string(s.value_id) + " is missing its prepared semantic request");
+        axes = it->second;
+      } else {
+        axes = axes_arg(s, rec(src).shape.size());
+      }
+      bg_handle out = permute(src, axes);
+      if (rec(out).shape != s.shape) plan_fail("PERMUTE output shape differs from the plan");
+      return out;
+    }
+    if (op == "BROADCAST_TO") {
+      bg_handle src = need(s, 0);
+      auto st = bstrides(rec(src).shape, s.shape, op);
+      bg_handle out = 0;
+      call(bg_copy_strided(ctx, src, 0, s.shape.data(), st.data(), int(s.shape.size()), &out));
+      return own(out);
+    }
+    if (op == "REDUCE") return reduce(s);
+    if (op == "FUSED_SOFTMAX") {
+      bg_handle src = need(s, 0);
+      const Record& r = rec(src);
+      const int64_t rank = int64_t(r.shape.size());
+      int64_t axis = rank - 1;
+      if (s.arg && s.arg->kind == JVal::Obj && s.arg->get("axis") && s.arg->get("axis")->kind != JVal::Null)
+        axis = expect_int(s.arg->get("axis"), "tensor plan FUSED_SOFTMAX.arg.axis");
+      if (axis < 0) axis += rank;
+      if (rank == 0) plan_fail("FUSED_SOFTMAX scalar input is unsupported");
+      if (axis != rank - 1) plan_fail("FUSED_SOFTMAX currently supports last-axis softmax only");
+      const int64_t cols = r.shape.back();
+      bg_handle out = 0;
+      call(bg_softmax_last(ctx, src, cols == 0 ? 0 : r.numel() / cols, cols, dt, &out));
+      return own(out);
+    }
+    if (op == "LAYER_NORM") {
+      if (!s.arg || s.arg->kind != JVal::Obj) plan_fail("LAYER_NORM.arg must be an object");
+      const int64_t rows = expect_int(s.arg->get("rows"), "LAYER_NORM.rows");
+      const int64_t cols = expect_int(s.arg->get("cols"), "LAYER_NORM.cols");
+      double eps = 1e-5;
+      if (const JVal* e = s.arg->get("eps"); e && e->kind != JVal::Null) {
+        if (e->kind != JVal::Num || !std::isfinite(e->num)) plan_fail("LAYER_NORM.eps must be finite");
+        eps = e->num;
+      }
+      if (rows <= 0 || cols <= 0) plan_fail("LAYER_NORM.rows and cols must be positive");
+      if (eps <= 0) plan_fail("LAYER_NORM.eps must be > 0");
+      bg_handle out = 0;
+      call(bg_layer_norm(ctx, need(s, 0), need(s, 1), need(s, 2), rows, cols, float(eps), dt, &out));
+      ctx->handles[out].shape = s.shape;
+      return own(out);
+    }
+    fail(BG_E_UNSUPPORTED, "tensor plan op " + op + " is not available in this build");
+  }
+
+  bg_handle matmul(const Step& s, int dt) {
+    bg_handle a = need(s, 0), b = need(s, 1);
+    const Record &ra = rec(a), &rb = rec(b);
+    if (ra.shape.size() < 2 || rb.shape.size() < 2 || s.shape.size() < 2)
+      plan_fail("MATMUL supports operands of rank >= 2");
+    const int64_t m = ra.shape[ra.shape.size() - 2], k = ra.shape.back();
+    const int64_t k2 = rb.shape[rb.shape.size() - 2], n = rb.shape.back();
+    if (k != k2 || s.shape[s.shape.size() - 2] != m || s.shape.back() != n)
+      plan_fail("MATMUL shape mismatch");
+    if (ra.dtype != rb.dtype) fail(BG_E_DTYPE, "tensor plan MATMUL operands differ in dtype");
+    const int64_t bo = numel(s.shape) / (m * n);
+    const int64_t ba = ra.numel() / (m * k), bb = rb.numel() / (k * n);
+    if ((ba != bo && ba != 1) || (bb != bo && bb != 1))
+      plan_fail("MATMUL batch dims must match or broadcast from a single matrix");
+    bg_matmul_desc d{};
+    d.a = a;
+    d.b = b;
+    d.batch = bo;
+    d.m = m;
+    d.n = n;
+    d.k = k;
+    d.lda = k;
+    d.ldb = n;
+    d.ldc = n;
+    d.stride_a = ba == 1 ? 0 : m * k;
+    d.stride_b = bb == 1 ? 0 : k * n;
+    d.stride_c = m * n;
+    d.in_dtype = ra.dtype;
+    d.out_dtype = dt;
+    bg_handle out = 0;
+    call(bg_matmul_ex(ctx, &d, &out));
+    ctx->handles[out].shape = s.shape;
+    return own(out);
+  }
+
+  bg_handle reduce(const Step& s) {
+    bg_handle src = need(s, 0);
+    const Record& r = rec(src);
+    const int64_t rank = int64_t(r.shape.size());
+    if (!s.arg || s.arg->kind != JVal::Obj) plan_fail("REDUCE.arg must be an object");
+    const JVal* opv = s.arg->get("op");
+    if (!opv || opv->kind != JVal::Str) fail(BG_E_INVALID, "tensor plan REDUCE.arg.op must be a string");
+    int rop;
+    if (opv->str == "sum") rop = BG_RED_SUM;
+    else if (opv->str == "mean") rop = BG_RED_MEAN;
+    else if (opv->str == "max") rop = BG_RED_MAX;  // extension
+    else if (opv->str == "min") rop = BG_RED_MIN;  // extension
+    else plan_fail("REDUCE supports sum/mean in v0 (got " + opv->str + ")");
+    std::vector<int64_t> axes;
+    const JVal* ax = s.arg->get("axis");
+    auto norm = [&](int64_t a) {
+      int64_t n = a < 0 ? a + rank : a;
+      if (n < 0 || n >= rank)
+        plan_fail("REDUCE axis " + std::to_string(a) + " out of range for rank " + std::to_string(rank));
+      return n;
+    };
+    if (!ax || ax->kind == JVal::Null) {
+      for (int64_t i = 0; i < rank; ++i) axes.push_back(i);
+    } else if (ax->kind == JVal::Arr) {
+      for (size_t i = 0; i < ax->arr.size(); ++i)
+        axes.push_back(norm(expect_int(&ax->arr[i], "tensor plan REDUCE.arg.axis[" + std::to_string(i) + "]")));
+    } else {
+      axes.push_back(norm(expect_int(ax, "tensor plan REDUCE.arg.axis")));
+    }
+    std::set<int64_t> red(axes.begin(), axes.end());
+    if (red.size() != axes.size()) plan_fail("REDUCE duplicate axis");
+    int64_t cols = 1;
+    for (int64_t a : red) cols *= r.shape[size_t(a)];
+    const int64_t rows = cols == 0 ? 0 : r.numel() / std::max<int64_t>(cols, 1);
+    // Move the reduced axes innermost (one strided copy) unless they already
+    // are the trailing axes.
+    bool trailing = true;
+    for (int64_t i = 0; i < int64_t(red.size()); ++i)
+      if (!red.count(rank - 1 - i)) trailing = false;
+    bg_handle x = src;
+    if (!trailing) {
+      std::vector<int64_t> perm;
+      for (int64_t i = 0; i < rank; ++i)
+        if (!red.count(i)) perm.push_back(i);
+      for (int64_t a : red) perm.push_back(a);
+      x = permute(src, perm);
+    }
+    if (cols == 0 || rows == 0) plan_fail("REDUCE over an empty axis is unsupported");
+    bg_handle out = 0;
+    call(bg_reduce_last(ctx, x, rows, cols, rop, 0, &out));
+    if (x != src) {
+      bg_release(ctx, x);
+      owned.erase(x);
+    }
+    if (numel(s.shape) != rows) plan_fail("REDUCE output shape differs from the plan");
+    ctx->handles[out].shape = s.shape;
+    if (rec(out).dtype != plan_dtype(s.dtype, "REDUCE dtype")) fail(BG_E_DTYPE, "tensor plan REDUCE dtype differs");
+    return own(out);
+  }
+
+  void release_all() {
+    for (bg_handle h : owned) bg_release(ctx, h);
+    owned.clear();
+  }
+};
+
+}  // namespace
+
+bg_handle run_plan(bg_ctx* ctx, const char* json, const char* requests_json, const int64_t* ids,
+                   const bg_handle* handles, int n, int dtype, bool resident) {
+  if (dtype != BG_F32 && dtype != BG_F16 && dtype != BG_BF16 && dtype != BG_BOOL)
+    fail(BG_E_DTYPE, "run_tensor_plan: dtype not supported");
+  JVal doc = JsonReader(json, "tensor plan").parse();
+  Plan plan = normalize(doc);
+  std::unordered_map<int64_t, std::vector<int64_t>> sem;
+  if (requests_json) sem = bind_requests(plan, parse_requests(requests_json));
+
+  Runner R{ctx};
+  if (requests_json) R.sem_axes = &sem;
+  for (int i = 0; i < n; ++i) {
+    if (R.vals.count(ids[i])) plan_fail("input " + std::to_string(ids[i]) + " provided twice");
+    get(ctx, handles[i], "tensor_plan[input]");
+    R.vals[ids[i]] = handles[i];
+    R.inputs.insert(handles[i]);
+  }
+  // Last step that reads each value (liveness, tensor_plan.ts:375-409).
+  std::unordered_map<int64_t, size_t> last_use;
+  for (size_t i = 0; i < plan.steps.size(); ++i)
+    for (int64_t in : plan.steps[i].inputs) last_use[in] = i;
+
+  try {
+    for (size_t i = 0; i < plan.steps.size(); ++i) {
+      const Step& s = plan.steps[i];
+      bg_handle h = R.exec(s);
+      R.vals[s.value_id] = h;
+      // Values whose last reader was this step (never the root).
+      for (int64_t in : s.inputs) {
+        if (in == plan.root_id || last_use[in] != i) continue;
+        bg_handle hin = R.vals[in];
+        if (R.owned.count(hin)) {
+          bg_release(ctx, hin);
+          R.owned.erase(hin);
+        }
+      }
+      // A value nobody reads (dead code) is released right away.
+      if (s.value_id != plan.root_id && !last_use.count(s.value_id) && R.owned.count(h)) {
+        bg_release(ctx, h);
+        R.owned.erase(h);
+      }
+    }
+  } catch (...) {
+    R.release_all();
+    throw;
+  }
+  bg_handle root = R.vals.at(plan.root_id);
+  if (resident) {
+    // The root must be an allocation of its own (runTensorGpuPlanResident).
+    const Alloc* ra = ctx->handles.at(root).alloc;
+    bool aliases = !R.owned.count(root);
+    for (bg_handle in : R.inputs)
+      if (ctx->handles.count(in) && ctx->handles.at(in).alloc == ra) aliases = true;
+    if (aliases) {
+      R.release_all();
+      plan_fail("root " + std::to_string(plan.root_id) +
+                " aliases an input buffer; resident output requires an owned root");
+    }
+  }
+  R.owned.erase(root);
+  R.release_all();
+  if (!R.inputs.count(root)) return root;
+  // Root is a caller's input (materialising plan): hand back a view so the
+  // caller may release it like any other root.
+  bg_handle v = 0;
+  const Record& rr = ctx->handles.at(root);
+  if (bg_reshape(ctx, root, rr.shape.data(), int(rr.shape.size()), &v) != BG_OK) fail(BG_E_HIP, ctx->err);
+  return v;
 }
 
 }  // namespace bg

@@ -293,17 +293,34 @@ int bg_reshape(bg_ctx* ctx, bg_handle h, const int64_t* shape, int rank,
 /* Reduction over the last axis (REDUCE sum/max/mean/min, tensor_plan.ts:999-1115). */
 int bg_reduce_last(bg_ctx* ctx, bg_handle x, int64_t rows, int64_t cols,
                    int op, int keepdims, bg_handle* out);
+/* Last-axis softmax (FUSED_SOFTMAX; softmax.ts:102-119, tensor_plan.ts:
+ * 573-586): rows x cols, x f32/f16/bf16, output out_dtype. */
+int bg_softmax_last(bg_ctx* ctx, bg_handle x, int64_t rows, int64_t cols,
+                    int out_dtype, bg_handle* out);
 /* Plan executor (run_tensor_plan / run_tensor_plan_resident,
  * realizer.ts:1557-1620; tensor_plan.ts:183-373).  `plan_json` uses the
  * reference wire format (snake_case or camelCase).  `input_ids[i]` is a
  * plan value_id and `input_handles[i]` a live handle bound to it (the
  * bindings upload host bytes first).  When `dst` is non-NULL the root is
  * materialised into it (dst_nbytes must match) and released; otherwise
- * the root handle is returned in *root_out and stays resident. */
+ * the root handle is returned in *root_out and stays resident (the root
+ * must then be an allocation of its own, not a view of an input:
+ * tensor_plan.ts:238-266). */
 int bg_run_tensor_plan(bg_ctx* ctx, const char* plan_json,
                        const int64_t* input_ids, const bg_handle* input_handles,
                        int n_inputs, int dtype, void* dst, size_t dst_nbytes,
                        bg_handle* root_out);
+/* Semantic route (run_tensor_plan_semantic / _resident_semantic,
+ * realizer.ts:1588-1652; tensor_plan_semantics.ts:96-260): as above, with the
+ * PERMUTE meaning taken from `requests_json`, the versioned
+ * dense-permutation-view-copy side table, which must match the plan's
+ * PERMUTE steps one to one (their legacy `arg` erased to null). */
+int bg_run_tensor_plan_semantic(bg_ctx* ctx, const char* plan_json,
+                                const char* requests_json,
+                                const int64_t* input_ids,
+                                const bg_handle* input_handles, int n_inputs,
+                                int dtype, void* dst, size_t dst_nbytes,
+                                bg_handle* root_out);
 
 /* Raw device pointer of a handle (extension; for harnesses that time
  * kernels with their own events).  Valid until the handle is released. */

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the HIP realizer on 1 MI355X (the BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,c4 | copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,c4,c5 | copy]
 
 Prints ONE JSON line.  ``value`` is configs[1] of BASELINE.json -- the fused
 elementwise + row-reduction chain ``relu(a*b+c)*exp(-a*a) -> sum(axis=1)`` on
@@ -261,6 +261,54 @@ def bench_c1(br, steps, warmup):
             "parity": O.report(y, ref, 1e-4)}
 
 
+# --------------------------------------------------------------------------- C5
+
+C5_FLOPS = 128_861_601_792  # linear 115,964,116,992 + causal attention 12,897,484,800
+
+
+def bench_c5(br, steps, warmup):
+    """One GPT-2 block (B8 S1024 E768 H12, autocast f16) through the walker:
+    the graph is prepared once (cast insertion + rewrites + fusion), seed
+    buffers stay resident in the GpuBufferTable, and each step walks the
+    graph to a device-resident root.  Wall time includes the host walk."""
+    from browsergrad_amd.jit import configs
+    from browsergrad_amd.jit.buffers import GpuBufferTable
+    from browsergrad_amd.jit.realize import prepare, walk
+    s, y = configs.c5()
+    g = prepare(y.uop, s.buffers)
+    gbt = GpuBufferTable(br)
+
+    def step():
+        br.release(walk(g, s.buffers, gbt, materialize=False))
+
+    for _ in range(warmup):
+        step()
+    br.synchronize()
+    n0 = len(br.flushProfiles()["passProfiles"])
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    br.synchronize()
+    t1 = time.perf_counter()
+    profs = br.flushProfiles()["passProfiles"][n0:]
+    by_label = {}
+    for p in profs:
+        by_label[p["label"]] = by_label.get(p["label"], 0.0) + p["gpuMs"] / steps
+    gpu_ms = sum(by_label.values())
+    wall_ms = (t1 - t0) * 1e3 / steps
+    out = walk(g, s.buffers, gbt, materialize=True)
+    gbt.release_all()
+    from oracle import graph as G  # checker only
+    from oracle import ops as O
+    ref = G.evaluate(y.uop, s.buffers)
+    return {"wall_ms": wall_ms, "gpu_kernel_ms": gpu_ms,
+            "tflops_wall": C5_FLOPS / (wall_ms * 1e-3) / 1e12,
+            "tflops_kernels": C5_FLOPS / (gpu_ms * 1e-3) / 1e12,
+            "frac_of_peak_kernels": C5_FLOPS / (gpu_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
+            "kernel_ms_by_label": {k: round(v, 4) for k, v in sorted(by_label.items(), key=lambda kv: -kv[1])},
+            "parity": O.report(out, ref, 2e-2)}
+
+
 def copy_probe(br, reps=5):
     """A plain copy kernel of known size (256 MiB read + 256 MiB written per
     launch): the calibration point for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -280,7 +328,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c1,c2,c3,c4")
+    ap.add_argument("--only", default="c1,c2,c3,c4,c5")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -310,6 +358,10 @@ def main() -> int:
         log("c4 causal attention B8 H16 S2048 D64 fp16")
         extra["c4_attention_fp16"] = bench_c4(br, max(10, a.steps // 2), a.warmup)
         log(f"  {extra['c4_attention_fp16']}")
+    if "c5" in only:
+        log("c5 gpt-2 block B8 S1024 E768 H12 autocast f16 (walker)")
+        extra["c5_gpt2_block_fp16"] = bench_c5(br, max(10, a.steps // 5), max(3, a.warmup // 2))
+        log(f"  {extra['c5_gpt2_block_fp16']}")
     if "c1" in only:
         log("c1 mlp 784-128-10 batch 64 f32")
         extra["c1_mlp_fp32"] = bench_c1(br, a.steps, a.warmup)

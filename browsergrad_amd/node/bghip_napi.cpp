@@ -1,0 +1,429 @@
+// N-API binding of libbghip: the native half of createHipRealizerBridge
+// (index.js), the Node twin of the reference's createWebGpuRealizerBridge
+// (packages/browsergrad-kernels/src/realizer.ts:902-1005).
+//
+// Every export is a thin wrapper over one C-ABI entry point of
+// include/bghip.h; the context is a napi External owned by the JS bridge
+// object.  Failures become a JS Error named "KernelError" whose message is
+// bg_last_error(ctx), like the reference's op-qualified KernelError
+// (types.ts:87-92).  Everything here is synchronous; index.js wraps the
+// methods the reference declares async (materialize, flash_attention, the
+// plan runs, flushProfiles) in Promises.
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "bghip.h"
+
+namespace {
+
+struct Ctx {
+  bg_ctx* ctx = nullptr;
+};
+
+void finalize_ctx(napi_env, void* data, void*) {
+  auto* c = static_cast<Ctx*>(data);
+  if (c->ctx) bg_ctx_destroy(c->ctx);
+  delete c;
+}
+
+napi_value throw_kernel_error(napi_env env, const std::string& msg) {
+  napi_value m, err, name;
+  napi_create_string_utf8(env, msg.c_str(), msg.size(), &m);
+  napi_create_error(env, nullptr, m, &err);
+  napi_create_string_utf8(env, "KernelError", NAPI_AUTO_LENGTH, &name);
+  napi_set_named_property(env, err, "name", name);
+  napi_throw(env, err);
+  return nullptr;
+}
+
+// Throws (and returns false) when rc is not BG_OK.
+bool check(napi_env env, bg_ctx* ctx, int rc) {
+  if (rc == BG_OK) return true;
+  throw_kernel_error(env, ctx ? bg_last_error(ctx) : "HIP bridge: null context");
+  return false;
+}
+
+struct Args {
+  napi_env env;
+  std::vector<napi_value> v;
+  bool ok = true;
+  Args(napi_env e, napi_callback_info info, size_t n) : env(e), v(n) {
+    size_t argc = n;
+    napi_get_cb_info(e, info, &argc, v.data(), nullptr, nullptr);
+    if (argc < n) {
+      throw_kernel_error(e, "HIP bridge: expected " + std::to_string(n) + " arguments");
+      ok = false;
+    }
+  }
+  bg_ctx* ctx(size_t i = 0) {
+    void* p = nullptr;
+    if (napi_get_value_external(env, v[i], &p) != napi_ok || !p) {
+      throw_kernel_error(env, "HIP bridge: bad context");
+      ok = false;
+      return nullptr;
+    }
+    return static_cast<Ctx*>(p)->ctx;
+  }
+  double num(size_t i) {
+    double d = 0;
+    if (napi_get_value_double(env, v[i], &d) != napi_ok) {
+      throw_kernel_error(env, "HIP bridge: argument " + std::to_string(i) + " must be a number");
+      ok = false;
+    }
+    return d;
+  }
+  int64_t i64(size_t i) { return static_cast<int64_t>(num(i)); }
+  bg_handle handle(size_t i) { return static_cast<bg_handle>(num(i)); }
+  bool is_nullish(size_t i) {
+    napi_valuetype t;
+    napi_typeof(env, v[i], &t);
+    return t == napi_null || t == napi_undefined;
+  }
+  std::string str(size_t i) {
+    size_t n = 0;
+    if (napi_get_value_string_utf8(env, v[i], nullptr, 0, &n) != napi_ok) {
+      throw_kernel_error(env, "HIP bridge: argument " + std::to_string(i) + " must be a string");
+      ok = false;
+      return {};
+    }
+    std::string s(n, '\0');
+    napi_get_value_string_utf8(env, v[i], &s[0], n + 1, &n);
+    return s;
+  }
+  std::vector<double> nums(size_t i) {
+    std::vector<double> out;
+    bool is_arr = false;
+    napi_is_array(env, v[i], &is_arr);
+    if (!is_arr) {
+      throw_kernel_error(env, "HIP bridge: argument " + std::to_string(i) + " must be an array");
+      ok = false;
+      return out;
+    }
+    uint32_t n = 0;
+    napi_get_array_length(env, v[i], &n);
+    for (uint32_t k = 0; k < n; ++k) {
+      napi_value e;
+      double d = 0;
+      napi_get_element(env, v[i], k, &e);
+      if (napi_get_value_double(env, e, &d) != napi_ok) {
+        throw_kernel_error(env, "HIP bridge: array elements must be numbers");
+        ok = false;
+        return {};
+      }
+      out.push_back(d);
+    }
+    return out;
+  }
+  std::vector<int64_t> shape(size_t i) {
+    std::vector<int64_t> s;
+    for (double d : nums(i)) s.push_back(static_cast<int64_t>(d));
+    return s;
+  }
+  int dtype(size_t i) {
+    std::string s = str(i);
+    int d = bg_dtype_from_name(s.c_str());
+    if (ok && d < 0) {
+      throw_kernel_error(env, "HIP bridge: unknown dtype " + s);
+      ok = false;
+    }
+    return d;
+  }
+};
+
+napi_value number(napi_env env, double d) {
+  napi_value r;
+  napi_create_double(env, d, &r);
+  return r;
+}
+
+napi_value bytes(napi_env env, const void* src, size_t n) {
+  void* data = nullptr;
+  napi_value ab, u8;
+  napi_create_arraybuffer(env, n, &data, &ab);
+  if (n) std::memcpy(data, src, n);
+  napi_create_typedarray(env, napi_uint8_array, n, ab, 0, &u8);
+  return u8;
+}
+
+// ---- lifecycle ------------------------------------------------------------
+
+napi_value CtxCreate(napi_env env, napi_callback_info info) {  // (device, profiling)
+  Args a(env, info, 2);
+  if (!a.ok) return nullptr;
+  int device = static_cast<int>(a.num(0));
+  bool prof = false;
+  napi_get_value_bool(env, a.v[1], &prof);
+  auto* c = new Ctx;
+  int rc = bg_ctx_create(device, prof ? 1 : 0, &c->ctx);
+  if (rc != BG_OK) {
+    delete c;
+    return throw_kernel_error(env, "HIP bridge: cannot open HIP device " + std::to_string(device) +
+                                       " (status " + std::to_string(rc) + "); the HIP realizer has no CPU fallback");
+  }
+  napi_value ext;
+  napi_create_external(env, c, finalize_ctx, nullptr, &ext);
+  return ext;
+}
+
+napi_value CtxDestroy(napi_env env, napi_callback_info info) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  void* p = nullptr;
+  napi_get_value_external(env, a.v[0], &p);
+  auto* c = static_cast<Ctx*>(p);
+  if (c && c->ctx) {
+    bg_ctx_destroy(c->ctx);
+    c->ctx = nullptr;
+  }
+  return nullptr;
+}
+
+// ---- data movement (realizer.ts:1007-1041) ---------------------------------
+
+napi_value Upload(napi_env env, napi_callback_info info) {  // (ctx, Uint8Array, shape, dtype)
+  Args a(env, info, 4);
+  bg_ctx* ctx = a.ctx();
+  if (!a.ok) return nullptr;
+  bool is_ta = false;
+  napi_is_typedarray(env, a.v[1], &is_ta);
+  if (!is_ta) return throw_kernel_error(env, "WebGPU bridge: upload data must be a Uint8Array");
+  napi_typedarray_type t;
+  size_t len = 0, off = 0;
+  void* data = nullptr;
+  napi_value ab;
+  napi_get_typedarray_info(env, a.v[1], &t, &len, &data, &ab, &off);
+  size_t esz = t == napi_float32_array || t == napi_int32_array || t == napi_uint32_array ? 4
+               : t == napi_float64_array ? 8 : t == napi_int16_array || t == napi_uint16_array ? 2 : 1;
+  auto shape = a.shape(2);
+  int dt = a.dtype(3);
+  if (!a.ok) return nullptr;
+  bg_handle h = 0;
+  if (!check(env, ctx, bg_upload(ctx, data, len * esz, shape.data(), int(shape.size()), dt, &h))) return nullptr;
+  return number(env, double(h));
+}
+
+napi_value Materialize(napi_env env, napi_callback_info info) {  // (ctx, h) -> Uint8Array
+  Args a(env, info, 2);
+  bg_ctx* ctx = a.ctx();
+  bg_handle h = a.handle(1);
+  if (!a.ok) return nullptr;
+  int64_t shp[16];
+  int rank = 0, dt = 0;
+  int64_t nb = 0;
+  if (!check(env, ctx, bg_handle_info(ctx, h, shp, &rank, &dt, &nb))) return nullptr;
+  std::vector<uint8_t> buf(static_cast<size_t>(nb));
+  if (!check(env, ctx, bg_materialize(ctx, h, buf.data(), buf.size()))) return nullptr;
+  return bytes(env, buf.data(), buf.size());
+}
+
+napi_value Release(napi_env env, napi_callback_info info) {
+  Args a(env, info, 2);
+  bg_ctx* ctx = a.ctx();
+  bg_handle h = a.handle(1);
+  if (!a.ok) return nullptr;
+  check(env, ctx, bg_release(ctx, h));
+  return nullptr;
+}
+
+napi_value HandleInfo(napi_env env, napi_callback_info info) {
+  Args a(env, info, 2);
+  bg_ctx* ctx = a.ctx();
+  bg_handle h = a.handle(1);
+  if (!a.ok) return nullptr;
+  int64_t shp[16];
+  int rank = 0, dt = 0;
+  int64_t nb = 0;
+  if (!check(env, ctx, bg_handle_info(ctx, h, shp, &rank, &dt, &nb))) return nullptr;
+  napi_value o, arr, s;
+  napi_create_object(env, &o);
+  napi_create_array_with_length(env, size_t(rank), &arr);
+  for (int i = 0; i < rank; ++i) napi_set_element(env, arr, uint32_t(i), number(env, double(shp[i])));
+  napi_set_named_property(env, o, "shape", arr);
+  napi_create_int32(env, dt, &s);
+  napi_set_named_property(env, o, "dtypeCode", s);
+  napi_set_named_property(env, o, "byteLength", number(env, double(nb)));
+  return o;
+}
+
+// ---- compute (realizer.ts:1043-1151) ---------------------------------------
+
+napi_value Matmul(napi_env env, napi_callback_info info) {  // (ctx, a, b, m, k, n, dtype)
+  Args a(env, info, 7);
+  bg_ctx* ctx = a.ctx();
+  bg_handle x = a.handle(1), y = a.handle(2);
+  int64_t m = a.i64(3), k = a.i64(4), n = a.i64(5);
+  int dt = a.dtype(6);
+  if (!a.ok) return nullptr;
+  bg_handle out = 0;
+  if (!check(env, ctx, bg_matmul(ctx, x, y, m, k, n, dt, &out))) return nullptr;
+  return number(env, double(out));
+}
+
+// (ctx, inputs[], opsFlat[] = [code, a, b, ...], shape[], dtype)
+napi_value FusedElementwise(napi_env env, napi_callback_info info) {
+  Args a(env, info, 5);
+  bg_ctx* ctx = a.ctx();
+  auto ins_d = a.nums(1);
+  auto ops_d = a.nums(2);
+  auto shape = a.shape(3);
+  int dt = a.dtype(4);
+  if (!a.ok) return nullptr;
+  std::vector<bg_handle> ins(ins_d.begin(), ins_d.end());
+  std::vector<bg_fused_op> ops;
+  for (size_t i = 0; i + 2 < ops_d.size(); i += 3)
+    ops.push_back({int32_t(ops_d[i]), int32_t(ops_d[i + 1]), int32_t(ops_d[i + 2]), 0});
+  bg_handle out = 0;
+  if (!check(env, ctx, bg_fused_elementwise(ctx, ins.data(), int(ins.size()), ops.data(), int(ops.size()),
+                                            shape.data(), int(shape.size()), dt, &out)))
+    return nullptr;
+  return number(env, double(out));
+}
+
+napi_value Cast(napi_env env, napi_callback_info info) {  // (ctx, h, src, dst, shape)
+  Args a(env, info, 5);
+  bg_ctx* ctx = a.ctx();
+  bg_handle h = a.handle(1);
+  int sd = a.dtype(2), dd = a.dtype(3);
+  auto shape = a.shape(4);
+  if (!a.ok) return nullptr;
+  bg_handle out = 0;
+  if (!check(env, ctx, bg_cast(ctx, h, sd, dd, shape.data(), int(shape.size()), &out))) return nullptr;
+  return number(env, double(out));
+}
+
+// (ctx, q, k, v, mask|null, b, h, sq, sk, d, scale, dtype)
+napi_value FlashAttention(napi_env env, napi_callback_info info) {
+  Args a(env, info, 12);
+  bg_ctx* ctx = a.ctx();
+  bg_handle q = a.handle(1), k = a.handle(2), v = a.handle(3);
+  bg_handle mask = a.is_nullish(4) ? 0 : a.handle(4);
+  int64_t b = a.i64(5), h = a.i64(6), sq = a.i64(7), sk = a.i64(8), d = a.i64(9);
+  double scale = a.num(10);
+  int dt = a.dtype(11);
+  if (!a.ok) return nullptr;
+  bg_handle out = 0;
+  if (!check(env, ctx, bg_flash_attention(ctx, q, k, v, mask, b, h, sq, sk, d, float(scale), dt, &out)))
+    return nullptr;
+  return number(env, double(out));
+}
+
+// (ctx, planJson, requestsJson|null, ids[], handles[], dtype, resident, rootBytes)
+napi_value RunTensorPlan(napi_env env, napi_callback_info info) {
+  Args a(env, info, 8);
+  bg_ctx* ctx = a.ctx();
+  std::string plan = a.str(1);
+  bool semantic = !a.is_nullish(2);
+  std::string req = semantic ? a.str(2) : std::string();
+  auto ids_d = a.nums(3);
+  auto hs_d = a.nums(4);
+  int dt = a.dtype(5);
+  bool resident = false;
+  napi_get_value_bool(env, a.v[6], &resident);
+  int64_t nbytes = resident ? 0 : a.i64(7);
+  if (!a.ok) return nullptr;
+  std::vector<int64_t> ids(ids_d.begin(), ids_d.end());
+  std::vector<bg_handle> hs(hs_d.begin(), hs_d.end());
+  std::vector<uint8_t> buf(resident ? 0 : size_t(nbytes));
+  bg_handle root = 0;
+  void* dst = resident ? nullptr : static_cast<void*>(buf.data());
+  int rc = semantic ? bg_run_tensor_plan_semantic(ctx, plan.c_str(), req.c_str(), ids.data(), hs.data(),
+                                                  int(ids.size()), dt, dst, buf.size(), &root)
+                    : bg_run_tensor_plan(ctx, plan.c_str(), ids.data(), hs.data(), int(ids.size()), dt, dst,
+                                         buf.size(), &root);
+  if (!check(env, ctx, rc)) return nullptr;
+  if (resident) return number(env, double(root));
+  return bytes(env, buf.data(), buf.size());
+}
+
+// ---- diagnostics (realizer.ts:275-298) ---------------------------------------
+
+napi_value AliveHandles(napi_env env, napi_callback_info info) {
+  Args a(env, info, 1);
+  bg_ctx* ctx = a.ctx();
+  if (!a.ok) return nullptr;
+  int64_t n = 0;
+  if (!check(env, ctx, bg_alive_handles(ctx, &n))) return nullptr;
+  return number(env, double(n));
+}
+
+napi_value ResourceSnapshot(napi_env env, napi_callback_info info) {
+  Args a(env, info, 1);
+  bg_ctx* ctx = a.ctx();
+  if (!a.ok) return nullptr;
+  bg_snapshot s{};
+  if (!check(env, ctx, bg_resource_snapshot(ctx, &s))) return nullptr;
+  napi_value o, tm, tq;
+  napi_create_object(env, &o);
+  napi_create_string_utf8(env, s.timing_mode == 1 ? "hip-event" : "unavailable", NAPI_AUTO_LENGTH, &tm);
+  napi_set_named_property(env, o, "timingMode", tm);
+  napi_get_boolean(env, s.timestamp_query_available != 0, &tq);
+  napi_set_named_property(env, o, "timestampQueryAvailable", tq);
+  napi_set_named_property(env, o, "currentOwnedGpuBytes", number(env, double(s.current_owned_bytes)));
+  napi_set_named_property(env, o, "peakOwnedGpuBytes", number(env, double(s.peak_owned_bytes)));
+  napi_set_named_property(env, o, "totalAllocatedGpuBytes", number(env, double(s.total_allocated_bytes)));
+  napi_set_named_property(env, o, "totalReleasedGpuBytes", number(env, double(s.total_released_bytes)));
+  napi_set_named_property(env, o, "aliveHandleCount", number(env, double(s.alive_handle_count)));
+  napi_set_named_property(env, o, "pendingProfileCount", number(env, double(s.pending_profile_count)));
+  napi_set_named_property(env, o, "passProfileCount", number(env, double(s.pass_profile_count)));
+  return o;
+}
+
+napi_value FlushProfiles(napi_env env, napi_callback_info info) {
+  Args a(env, info, 1);
+  bg_ctx* ctx = a.ctx();
+  if (!a.ok) return nullptr;
+  int n = 0;
+  if (!check(env, ctx, bg_flush_profiles(ctx, nullptr, 0, &n))) return nullptr;
+  std::vector<bg_pass_profile> ps(size_t(n > 0 ? n : 1));
+  int got = 0;
+  if (!check(env, ctx, bg_flush_profiles(ctx, ps.data(), n, &got))) return nullptr;
+  napi_value arr;
+  napi_create_array_with_length(env, size_t(got), &arr);
+  for (int i = 0; i < got && i < n; ++i) {
+    napi_value o, label;
+    napi_create_object(env, &o);
+    napi_create_string_utf8(env, ps[i].label, NAPI_AUTO_LENGTH, &label);
+    napi_set_named_property(env, o, "label", label);
+    napi_set_named_property(env, o, "gpuMs", number(env, ps[i].gpu_ms));
+    napi_set_named_property(env, o, "bytes", number(env, double(ps[i].bytes)));
+    napi_set_named_property(env, o, "flops", number(env, double(ps[i].flops)));
+    napi_set_element(env, arr, uint32_t(i), o);
+  }
+  return arr;
+}
+
+napi_value Version(napi_env env, napi_callback_info) {
+  napi_value s;
+  napi_create_string_utf8(env, bg_version(), NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  struct {
+    const char* name;
+    napi_callback fn;
+  } fns[] = {
+      {"ctxCreate", CtxCreate},       {"ctxDestroy", CtxDestroy},
+      {"upload", Upload},             {"materialize", Materialize},
+      {"release", Release},           {"handleInfo", HandleInfo},
+      {"matmul", Matmul},             {"fusedElementwise", FusedElementwise},
+      {"cast", Cast},                 {"flashAttention", FlashAttention},
+      {"runTensorPlan", RunTensorPlan}, {"aliveHandles", AliveHandles},
+      {"resourceSnapshot", ResourceSnapshot}, {"flushProfiles", FlushProfiles},
+      {"version", Version},
+  };
+  for (auto& f : fns) {
+    napi_value v;
+    napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.fn, nullptr, &v);
+    napi_set_named_property(env, exports, f.name, v);
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

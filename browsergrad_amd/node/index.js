@@ -1,0 +1,154 @@
+'use strict';
+// createHipRealizerBridge: the HIP realizer behind the reference's
+// WebGpuRealizerBridge interface (packages/browsergrad-kernels/src/
+// realizer.ts:77-280), for Node hosts.  Method names, argument meaning and
+// return types are the reference's; device work runs through bghip.node
+// (N-API over libbghip.so).  Methods the reference declares async return
+// Promises resolved after the blocking native call.
+//
+//   const { createHipRealizerBridge } = require('./browsergrad_amd/node');
+//   const bridge = createHipRealizerBridge({ device: 0 });
+//   pyodide.registerJsModule('_bg_webgpu_bridge', bridge);
+
+const path = require('path');
+
+let native = null;
+function loadNative() {
+  if (native === null) native = require(path.join(__dirname, 'bghip.node'));
+  return native;
+}
+
+class KernelError extends Error {
+  constructor(message) {
+    super(message);
+    this.name = 'KernelError';
+  }
+}
+
+// fused_elementwise.ts:83-90 opcodes, as the C ABI numbers them.
+const OPCODES = { ADD: 0, MUL: 1, DIV: 2, NEG: 3, EXP: 4, LOG: 5 };
+
+function asBytes(data, name) {
+  if (!(data instanceof Uint8Array)) throw new KernelError(`WebGPU bridge: ${name}.data must be Uint8Array bytes`);
+  return data;
+}
+
+function wrap(fn) {
+  try {
+    return fn();
+  } catch (e) {
+    if (e && e.name === 'KernelError') throw new KernelError(e.message);
+    throw e;
+  }
+}
+
+function createHipRealizerBridge(options = {}) {
+  const n = loadNative();
+  const ctx = n.ctxCreate(options.device || 0, !!options.profiling);
+  const traces = new Map();
+
+  function uploadPlanInputs(plan, inputs) {
+    const steps = new Map();
+    for (const st of plan.steps || []) steps.set(st.valueId !== undefined ? st.valueId : st.value_id, st);
+    const ids = [];
+    const handles = [];
+    const temps = [];
+    try {
+      inputs.forEach((input, i) => {
+        if (input === null || typeof input !== 'object' || Array.isArray(input)) {
+          throw new KernelError(`WebGPU bridge: tensor plan input ${i} must be an object`);
+        }
+        const id = input.valueId !== undefined ? input.valueId : input.value_id;
+        if (!Number.isInteger(id)) throw new KernelError(`WebGPU bridge: tensor plan input ${i}.valueId must be an integer`);
+        if (input.handle !== undefined) {
+          if (!Number.isInteger(input.handle)) throw new KernelError(`WebGPU bridge: tensor plan input ${i}.handle must be an integer`);
+          ids.push(id);
+          handles.push(input.handle);
+          return;
+        }
+        const data = asBytes(input.data, `tensor plan input ${i}`);
+        const st = steps.get(id);
+        const dtype = st ? st.dtype : 'float32';
+        const width = dtype === 'float16' || dtype === 'bfloat16' ? 2 : dtype === 'bool' ? 1 : 4;
+        if (data.byteLength % width !== 0) {
+          throw new KernelError(`WebGPU bridge: tensor plan input ${i}.data byte length must be divisible by ${width}`);
+        }
+        const h = n.upload(ctx, data, [data.byteLength / width], dtype);
+        temps.push(h);
+        ids.push(id);
+        handles.push(h);
+      });
+    } catch (e) {
+      for (const h of temps) n.release(ctx, h);
+      throw e;
+    }
+    return { ids, handles, temps };
+  }
+
+  function rootBytes(plan) {
+    const rootId = plan.rootId !== undefined ? plan.rootId : plan.root_id;
+    const st = (plan.steps || []).find((s) => (s.valueId !== undefined ? s.valueId : s.value_id) === rootId);
+    if (!st) return 0;
+    const numel = st.shape.reduce((a, b) => a * b, 1);
+    const width = st.dtype === 'float16' || st.dtype === 'bfloat16' ? 2 : st.dtype === 'bool' ? 1 : 4;
+    return numel * width;
+  }
+
+  function runPlan(plan, requests, inputs, dtype, resident) {
+    const obj = typeof plan === 'string' ? JSON.parse(plan) : plan;
+    const text = typeof plan === 'string' ? plan : JSON.stringify(plan);
+    const req = requests === null || requests === undefined ? null
+      : (typeof requests === 'string' ? requests : JSON.stringify(requests));
+    const { ids, handles, temps } = uploadPlanInputs(obj, inputs);
+    try {
+      return wrap(() => n.runTensorPlan(ctx, text, req, ids, handles, dtype, resident, rootBytes(obj)));
+    } finally {
+      for (const h of temps) n.release(ctx, h);
+    }
+  }
+
+  const bridge = {
+    upload: (data, shape, dtype) => wrap(() => n.upload(ctx, asBytes(data, 'upload'), shape, dtype)),
+    materialize: async (h, _shape, _dtype) => wrap(() => n.materialize(ctx, h)),
+    release: (h) => wrap(() => n.release(ctx, h)),
+    matmul: (a, b, m, k, nn, dtype) => wrap(() => n.matmul(ctx, a, b, m, k, nn, dtype)),
+    fused_elementwise: (inputs, ops, shape, dtype) => wrap(() => {
+      const flat = [];
+      for (const [op, lhs, rhs] of ops) {
+        if (!(op in OPCODES)) throw new KernelError(`fused_elementwise: unsupported opcode ${JSON.stringify(op)}`);
+        flat.push(OPCODES[op], lhs, rhs === null || rhs === undefined ? lhs : rhs);
+      }
+      return n.fusedElementwise(ctx, inputs, flat, shape, dtype);
+    }),
+    cast: (h, srcDtype, dstDtype, shape) => wrap(() => n.cast(ctx, h, srcDtype, dstDtype, shape)),
+    flash_attention: async (q, k, v, mask, b, h, sq, sk, d, scale, dtype) =>
+      wrap(() => n.flashAttention(ctx, q, k, v, mask, b, h, sq, sk, d, scale, dtype)),
+    run_tensor_plan: async (plan, inputs, dtype) => runPlan(plan, null, inputs, dtype, false),
+    run_tensor_plan_semantic: async (plan, requests, inputs, dtype) => runPlan(plan, requests, inputs, dtype, false),
+    run_tensor_plan_resident: (plan, inputs, dtype) => runPlan(plan, null, inputs, dtype, true),
+    run_tensor_plan_resident_semantic: async (plan, requests, inputs, dtype) => {
+      const h = runPlan(plan, requests, inputs, dtype, true);
+      traces.set(h, { preparation: typeof requests === 'string' ? JSON.parse(requests) : requests });
+      return h;
+    },
+    semanticTensorPlanExecutionTrace: async (h) => {
+      const t = traces.get(h);
+      if (!t) throw new KernelError(`WebGPU bridge: handle ${h} has no semantic tensor-plan execution trace`);
+      return t;
+    },
+    aliveHandleCount: () => wrap(() => n.aliveHandles(ctx)),
+    resourceSnapshot: () => wrap(() => n.resourceSnapshot(ctx)),
+    flushProfiles: async () => wrap(() => ({ ...n.resourceSnapshot(ctx), passProfiles: n.flushProfiles(ctx) })),
+    close: () => n.ctxDestroy(ctx),
+  };
+  const outOfScope = (name) => () => {
+    throw new KernelError(`HIP bridge: ${name} is not part of the HIP realizer's hot path`);
+  };
+  for (const name of ['conv1d', 'conv1d_backward_input', 'conv1d_backward_weight', 'conv1d_backward_bias',
+    'conv2d', 'conv2d_backward_input', 'conv2d_backward_weight', 'conv2d_backward_bias', 'run_user_kernel']) {
+    bridge[name] = outOfScope(name);
+  }
+  return bridge;
+}
+
+module.exports = { createHipRealizerBridge, KernelError, version: () => loadNative().version() };

@@ -31,6 +31,9 @@
 // (NN and NT), the same staged epilogue.
 #include <algorithm>
 
+#include <cstdlib>
+#include <string>
+
 #include "common.cuh"
 #include "core.h"
 
@@ -712,6 +715,40 @@ void launch32(bg_ctx* ctx, const GemmArgs& P, int64_t batch, bool trans_b, bool 
 
 bool aligned_to(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
+// Tile shapes / pipeline depths of the direct-to-LDS kernel.  LDS per
+// workgroup = S * (BM + BN) * BK * 2 bytes (<= 160 KB); loads run S-1 stages
+// ahead, so short stages (small tiles or BK = 32) need more of them to cover
+// HBM latency.
+enum class LdsCfg { T256x256x64s2, T256x256x32s4, T256x128x64s3, T128x256x64s3, T128x128x64s4, T128x128x32s4,
+                    T128x128x64s2 };
+
+template <int BM_, int BN_, int BK_, int S_>
+struct CfgTag {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, S = S_;
+};
+
+LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch) {
+  // Diagnostic override for tuning sweeps: BG_GEMM_TILE=BMxBNxBKsS.
+  if (const char* e = std::getenv("BG_GEMM_TILE")) {
+    const std::string v(e);
+    if (v == "256x256x64s2") return LdsCfg::T256x256x64s2;
+    if (v == "256x256x32s4") return LdsCfg::T256x256x32s4;
+    if (v == "256x128x64s3") return LdsCfg::T256x128x64s3;
+    if (v == "128x256x64s3") return LdsCfg::T128x256x64s3;
+    if (v == "128x128x64s4") return LdsCfg::T128x128x64s4;
+    if (v == "128x128x32s4") return LdsCfg::T128x128x32s4;
+    if (v == "128x128x64s2") return LdsCfg::T128x128x64s2;
+  }
+  // Measured on MI355X (wall clock, 50 back-to-back launches): 256x256 tiles
+  // win only for deep-K problems with at least one tile per CU (4096^3:
+  // 146 vs 159 us); for the GPT-2 shapes (M = 8192, N in {768, 2304, 3072},
+  // K in {768, 3072}) 128x128 tiles with two stages -- two workgroups per CU
+  // -- are fastest (e.g. 8192x2304x768: 43.8 vs 57.5 us); deeper pipelines
+  // (3-4 stages, BK 32) measured slower at every shape.
+  const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
+  return (t256 >= 256 && k >= 2048) ? LdsCfg::T256x256x64s2 : LdsCfg::T128x128x64s2;
+}
+
 }  // namespace
 
 namespace bg {
@@ -779,13 +816,6 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
   const bool vec = aligned_to(P.A, 16) && aligned_to(P.B, 16) && d.k % 8 == 0 && P.lda % 8 == 0 &&
                    P.ldb % 8 == 0 && P.sa % 8 == 0 && P.sb % 8 == 0;
   const bool bf = d.in_dtype == BG_BF16;
-  // Large problems: 256x256 tiles (one tile per CU at 4096^2); otherwise 128x128.
-  const int64_t t256 = ((d.m + 255) / 256) * ((d.n + 255) / 256) * d.batch;
-  const bool big = t256 >= 192;
-  const int BMN = big ? 256 : 128;
-  P.tiles_m = int((d.m + BMN - 1) / BMN);
-  P.tiles_n = int((d.n + BMN - 1) / BMN);
-  const bool full = vec && d.m % BMN == 0 && d.n % BMN == 0 && d.k % BK16 == 0 && P.vec_store;
   Profile prof(ctx, bf ? "gemm_bf16" : "gemm_f16", bytes, flops);
   // Direct-to-LDS path: operand byte ranges addressable with 32-bit offsets.
   const int64_t a_span = ((d.m - 1) * P.lda + d.k) * es;
@@ -793,18 +823,32 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
   const bool lds_ok = vec && a_span < (int64_t(1) << 31) && b_span < (int64_t(1) << 31);
   if (lds_ok) {
     const uint32_t ab = uint32_t(a_span), bb = uint32_t(b_span);
-    // BK = 64 with two LDS stages measured faster than BK = 32 with four
-    // (4096^3 f16: 132 vs 135 us) and keeps 128-byte LDS rows, whose
-    // swizzle is bank-conflict free.
-    if (big) {
-      if (bf) launch16_lds<256, 256, 64, 2, true>(ctx, P, d.batch, ab, bb);
-      else launch16_lds<256, 256, 64, 2, false>(ctx, P, d.batch, ab, bb);
-    } else {
-      if (bf) launch16_lds<128, 128, 64, 2, true>(ctx, P, d.batch, ab, bb);
-      else launch16_lds<128, 128, 64, 2, false>(ctx, P, d.batch, ab, bb);
+    const LdsCfg cfg = choose_lds_cfg(d.m, d.n, d.k, d.batch);
+    auto go = [&](auto tag) {
+      using T = decltype(tag);
+      P.tiles_m = int((d.m + T::BM - 1) / T::BM);
+      P.tiles_n = int((d.n + T::BN - 1) / T::BN);
+      if (bf) launch16_lds<T::BM, T::BN, T::BK, T::S, true>(ctx, P, d.batch, ab, bb);
+      else launch16_lds<T::BM, T::BN, T::BK, T::S, false>(ctx, P, d.batch, ab, bb);
+    };
+    switch (cfg) {
+      case LdsCfg::T256x256x64s2: go(CfgTag<256, 256, 64, 2>{}); break;
+      case LdsCfg::T256x256x32s4: go(CfgTag<256, 256, 32, 4>{}); break;
+      case LdsCfg::T256x128x64s3: go(CfgTag<256, 128, 64, 3>{}); break;
+      case LdsCfg::T128x256x64s3: go(CfgTag<128, 256, 64, 3>{}); break;
+      case LdsCfg::T128x128x64s4: go(CfgTag<128, 128, 64, 4>{}); break;
+      case LdsCfg::T128x128x32s4: go(CfgTag<128, 128, 32, 4>{}); break;
+      default: go(CfgTag<128, 128, 64, 2>{}); break;
     }
     return;
   }
+  // Large problems: 256x256 tiles (one tile per CU at 4096^2); otherwise 128x128.
+  const int64_t t256 = ((d.m + 255) / 256) * ((d.n + 255) / 256) * d.batch;
+  const bool big = t256 >= 192;
+  const int BMN = big ? 256 : 128;
+  P.tiles_m = int((d.m + BMN - 1) / BMN);
+  P.tiles_n = int((d.n + BMN - 1) / BMN);
+  const bool full = vec && d.m % BMN == 0 && d.n % BMN == 0 && d.k % BK16 == 0 && P.vec_store;
   if (big) {
     if (bf) launch16<256, 256, true, 0>(ctx, P, d.batch, full, vec);
     else launch16<256, 256, false, 0>(ctx, P, d.batch, full, vec);

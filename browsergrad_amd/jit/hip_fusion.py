@@ -36,8 +36,9 @@ import numpy as np
 from .buffers import BufferTable
 from .fusion import _match_softmax, consumers_of, fuse, substitute
 from .ir import (
-    OP_ADD, OP_BUFFER, OP_CAST, OP_CMP, OP_CONST, OP_DIV, OP_EXP, OP_HIP_ATTENTION, OP_HIP_LINEAR,
-    OP_HIP_REDUCE_FUSED, OP_LOAD, OP_MATMUL, OP_MUL, OP_NEG, OP_PERMUTE, OP_REDUCE, OP_WHERE, UOp, toposort,
+    OP_ADD, OP_BUFFER, OP_CAST, OP_CMP, OP_CONST, OP_DIV, OP_EXP, OP_HIP_ATTENTION, OP_HIP_LINEAR, OP_LAYER_NORM,
+    OP_HIP_REDUCE_FUSED, OP_LOAD, OP_MATMUL, OP_MUL, OP_NEG, OP_PERMUTE, OP_REDUCE, OP_RESHAPE, OP_SLICE, OP_WHERE,
+    UOp, toposort,
 )
 from .program import NotLowerable, ProgramTooLarge, compile_program, lowerable
 
@@ -313,6 +314,123 @@ def _match_linear(add: UOp, cons: Dict[int, List[UOp]]) -> Optional[Tuple[UOp, U
     return None
 
 
+# ---- dtype refresh ---------------------------------------------------------------
+
+_PASS_THROUGH = frozenset({"LOAD", "RESHAPE", "PERMUTE", "SLICE", "BROADCAST_TO"})
+
+
+def refresh_dtypes(root: UOp) -> UOp:
+    """Give pass-through ops the dtype their input actually carries and drop
+    CASTs that became no-ops.  After cast insertion a PERMUTE / RESHAPE /
+    SLICE keeps the dtype it was built with while its input turned narrow;
+    the reference realizer follows numpy's array dtype there (the value is
+    what the array holds), so rewriting the IR to the carried dtype changes
+    no value and lets later rewrites see the real layout."""
+    new: Dict[int, UOp] = {}
+    for n in toposort(root):
+        if not n.inputs:
+            new[id(n)] = n
+            continue
+        ins = tuple(new.get(id(i), i) for i in n.inputs)
+        dtype = n.dtype
+        if n.op in _PASS_THROUGH:
+            dtype = ins[0].dtype
+        elif n.op == OP_WHERE and not (isinstance(n.arg, dict) and n.arg.get("autocast_hint")):
+            from .tensor import promote
+            dtype = promote(ins[1].dtype, ins[2].dtype)
+        if n.op == OP_CAST and ins[0].dtype == n.dtype:
+            new[id(n)] = ins[0]
+            continue
+        if dtype == n.dtype and all(a is b for a, b in zip(ins, n.inputs)):
+            new[id(n)] = n
+        else:
+            new[id(n)] = UOp(n.op, ins, n.shape, dtype, n.arg)
+    return new[id(root)]
+
+
+# ---- head split / merge as strided views of the QKV GEMM -------------------------
+
+def _head_split(x: UOp, narrow: str):
+    """x = CAST_narrow(PERMUTE(0,2,1,3)(RESHAPE(B,S,H,D)(SLICE(L, last axis))))
+    -> (L, start, interior nodes) or None."""
+    if x.op != OP_CAST or x.dtype != narrow:
+        return None
+    p = x.inputs[0]
+    if p.op != OP_PERMUTE or tuple(p.arg["axes"]) != (0, 2, 1, 3):
+        return None
+    r = p.inputs[0]
+    if r.op != OP_RESHAPE or len(r.shape) != 4:
+        return None
+    sl = r.inputs[0]
+    if sl.op != OP_SLICE:
+        return None
+    src = sl.inputs[0]
+    slices = sl.arg["slices"]
+    if len(src.shape) != 3 or any(tuple(t) != (0, d, 1) for t, d in zip(slices[:-1], src.shape[:-1])):
+        return None
+    start, stop, step = slices[-1]
+    b, s, h, d = r.shape
+    if step != 1 or stop - start != h * d or (b, s) != src.shape[:2]:
+        return None
+    return src, int(start), [x, p, r, sl]
+
+
+def _rewrite_attention_views(root: UOp) -> UOp:
+    cons = consumers_of(root)
+    subs: Dict[int, UOp] = {}
+    for att in toposort(root):
+        if att.op != OP_HIP_ATTENTION or not att.arg.get("round_scores") or att.dtype not in NARROW:
+            continue
+        parts = [_head_split(x, att.dtype) for x in att.inputs]
+        if any(p is None for p in parts) or len({id(p[0]) for p in parts}) != 1:
+            continue
+        lin = parts[0][0]
+        if lin.op != OP_HIP_LINEAR or lin.dtype != "float32":
+            continue
+        interior = [n for p in parts for n in p[2]]
+        allowed = {id(n) for n in interior} | {id(att)}
+        if not all(_only_consumers(n, cons, allowed) for n in interior + [lin]):
+            continue
+        b, s, f = lin.shape
+        _, h, _, d = att.inputs[0].shape
+        lin16 = UOp(OP_HIP_LINEAR, lin.inputs, lin.shape, att.dtype, {**lin.arg, "out_dtype": att.dtype})
+        views = [(p[1], s * f, d, f) for p in parts]
+        arg = {**att.arg, "views": views, "o_layout": "bhsd"}
+        out_node = att
+        ac = cons.get(id(att), [])
+        if len(ac) == 1 and ac[0].op == OP_PERMUTE and tuple(ac[0].arg["axes"]) == (0, 2, 1, 3):
+            perm = ac[0]
+            pc = cons.get(id(perm), [])
+            if len(pc) == 1 and pc[0].op == OP_RESHAPE and pc[0].shape == (b, s, h * d):
+                new_att = UOp(OP_HIP_ATTENTION, (lin16, lin16, lin16), (b, s, h, d), att.dtype,
+                              {**arg, "o_layout": "bshd"})
+                subs[id(pc[0])] = UOp(OP_RESHAPE, (new_att,), pc[0].shape, att.dtype, pc[0].arg)
+                continue
+        subs[id(out_node)] = UOp(OP_HIP_ATTENTION, (lin16, lin16, lin16), att.shape, att.dtype, arg)
+    return substitute(root, subs)
+
+
+def _rewrite_narrow_stores(root: UOp) -> UOp:
+    """A linear or LayerNorm whose only reader casts it to a narrow dtype
+    stores that dtype directly (the cast's rounding is the store's rounding;
+    both compute in float32 up to the store)."""
+    cons = consumers_of(root)
+    subs: Dict[int, UOp] = {}
+    for n in toposort(root):
+        if n.op not in (OP_HIP_LINEAR, OP_LAYER_NORM) or n.dtype != "float32":
+            continue
+        c = cons.get(id(n), [])
+        if len(c) == 1 and c[0].op == OP_CAST and c[0].dtype in NARROW:
+            arg = {**n.arg, "out_dtype": c[0].dtype} if n.op == OP_HIP_LINEAR else n.arg
+            subs[id(c[0])] = UOp(n.op, n.inputs, n.shape, c[0].dtype, arg)
+    return substitute(root, subs)
+
+
+def _is_seed_cast(n: UOp) -> bool:
+    """CAST of a seed buffer: left to the walker, which caches the result."""
+    return n.op == OP_CAST and _buffer_of(n.inputs[0]) is not None
+
+
 # ---- elementwise DAGs (+ last-axis reduce) --------------------------------------
 
 def _grow_dag(top: UOp, cons: Dict[int, List[UOp]], taken: Set[int]) -> List[UOp]:
@@ -324,7 +442,7 @@ def _grow_dag(top: UOp, cons: Dict[int, List[UOp]], taken: Set[int]) -> List[UOp
     while frontier:
         n = frontier.pop()
         for i in n.inputs:
-            if id(i) in inside or id(i) in taken or not lowerable(i) or i.op == OP_CONST:
+            if id(i) in inside or id(i) in taken or not lowerable(i) or i.op == OP_CONST or _is_seed_cast(i):
                 continue
             if all(id(c) in inside for c in cons.get(id(i), [])):
                 inside.add(id(i))
@@ -337,6 +455,7 @@ def _grow_dag(top: UOp, cons: Dict[int, List[UOp]], taken: Set[int]) -> List[UOp
 
 
 def hip_fuse(root: UOp, bt: BufferTable) -> UOp:
+    root = refresh_dtypes(root)
     # 1. attention
     cons = consumers_of(root)
     subs: Dict[int, UOp] = {}
@@ -362,6 +481,8 @@ def hip_fuse(root: UOp, bt: BufferTable) -> UOp:
         taken.update(id(x) for x in interior)
         taken.add(id(out))
     root = substitute(root, subs)
+    root = _rewrite_attention_views(root)
+    root = _rewrite_narrow_stores(root)
     # 3. softmax outside attention: the reference matcher
     root = fuse(root, include_elementwise=False)
     # 4. elementwise DAGs, with a last-axis reduction where one ends in REDUCE
@@ -389,7 +510,7 @@ def hip_fuse(root: UOp, bt: BufferTable) -> UOp:
                     taken.update(id(x) for x in dag)
                     taken.add(id(n))
                     continue
-        if lowerable(n) and n.op != OP_CONST:
+        if lowerable(n) and n.op != OP_CONST and not _is_seed_cast(n):
             dag = _grow_dag(n, cons, taken)
             if len(dag) == 1 and n.op == OP_CAST and n.inputs[0].op == OP_CONST:
                 continue  # constant folding is done by the consumer's program

@@ -69,6 +69,7 @@ class _Walk:
         self.gbt = gbt
         self.bt = bt
         self.vt: Dict[int, int] = {}
+        self.borrowed: set = set()  # handles owned by the GpuBufferTable
 
     def h(self, u: UOp) -> int:
         return self.vt[id(u)]
@@ -146,6 +147,17 @@ def _h_cast(n: UOp, w: _Walk) -> int:
     actual = w.dtype_of(src)
     if actual == n.dtype:  # astype to the dtype the array already has
         return w.br.reshape(w.h(src), n.shape or (1,))
+    seed = src.inputs[0] if src.op == OP_LOAD and src.inputs[0].op == OP_BUFFER else None
+    if seed is not None:
+        # A seed buffer's cast is kept resident beside it (weights are cast
+        # once per session, like the upload itself).
+        key = f"{seed.arg}::{n.dtype}"
+        h = w.gbt.get(key)
+        if h is None:
+            h = w.br.cast(w.h(src), actual, n.dtype, n.shape)
+            w.gbt.register(key, h)
+        w.borrowed.add(h)
+        return h
     return w.br.cast(w.h(src), actual, n.dtype, n.shape)
 
 
@@ -291,12 +303,32 @@ def _h_attention_forward(n: UOp, w: _Walk) -> int:
 
 def _h_hip_attention(n: UOp, w: _Walk) -> int:
     q, k, v = n.inputs
-    b, h, sq, d = q.shape
-    sk = k.shape[2]
     a = n.arg
-    return w.br.attention_ex(w.h(q), w.h(k), w.h(v), batch=b, heads=h, sq=sq, sk=sk, d=d, scale=a["scale"],
-                             causal=a["causal"], in_dtype=q.dtype, out_dtype=n.dtype,
-                             round_scores=a["round_scores"])
+    views = a.get("views")
+    if views is None:
+        b, h, sq, d = q.shape
+        sk = k.shape[2]
+        return w.br.attention_ex(w.h(q), w.h(k), w.h(v), batch=b, heads=h, sq=sq, sk=sk, d=d, scale=a["scale"],
+                                 causal=a["causal"], in_dtype=q.dtype, out_dtype=n.dtype,
+                                 round_scores=a["round_scores"])
+    # Q / K / V are strided views of one [B, S, 3E] buffer; the output is
+    # written [B, H, S, D] or, with o_layout "bshd", [B, S, H, D].
+    b, s = q.shape[0], q.shape[1]
+    if a["o_layout"] == "bshd":
+        _, _, h, d = n.shape
+        o_strides = (s * h * d, d, h * d)
+    else:
+        _, h, _, d = n.shape
+        o_strides = (0, 0, 0)
+    out = w.br.attention_ex(w.h(q), w.h(k), w.h(v), batch=b, heads=h, sq=s, sk=s, d=d, scale=a["scale"],
+                            causal=a["causal"], in_dtype=q.dtype, out_dtype=n.dtype,
+                            round_scores=a["round_scores"], q_view=tuple(views[0]), k_view=tuple(views[1]),
+                            v_view=tuple(views[2]), o_strides=o_strides)
+    if a["o_layout"] == "bshd":
+        view = w.br.reshape(out, n.shape)
+        w.br.release(out)
+        return view
+    return out
 
 
 def _h_hip_linear(n: UOp, w: _Walk) -> int:
@@ -306,7 +338,8 @@ def _h_hip_linear(n: UOp, w: _Walk) -> int:
     m = a.numel // k
     nn = wt.shape[0] if arg["trans_b"] else wt.shape[1]
     hnd = w.br.matmul_ex(w.h(a), w.h(wt), m=m, n=nn, k=k, trans_b=arg["trans_b"], in_dtype=arg["in_dtype"],
-                         out_dtype="float32", bias=w.h(bias), round_out=arg["round_out"], act=arg["act"])
+                         out_dtype=arg.get("out_dtype", "float32"), bias=w.h(bias), round_out=arg["round_out"],
+                         act=arg["act"])
     out = w.br.reshape(hnd, n.shape)
     w.br.release(hnd)
     return out
@@ -381,7 +414,7 @@ def walk(root: UOp, bt: BufferTable, gbt: GpuBufferTable, *, materialize: bool =
             except Exception as e:  # noqa: BLE001 - wrapped like _realize_webgpu.py:415-424
                 raise RealizationError(f"HIP realizer: {n.op} (shape={n.shape}, dtype={n.dtype}) failed: {e}") from e
             w.vt[id(n)] = hnd
-            if n.op not in (OP_BUFFER, OP_LOAD) and hnd is not None:
+            if n.op not in (OP_BUFFER, OP_LOAD) and hnd is not None and hnd not in w.borrowed:
                 owned[id(n)] = hnd
             for inp in n.inputs:
                 if last.get(id(inp)) == i and id(inp) in owned and inp is not root:

@@ -107,6 +107,10 @@ __device__ __forceinline__ void store_elem(char* p, float v) {
 // 8*(e/4) + 4*(l/32) + e%4, column l%32, so each store instruction writes 32
 // consecutive columns of two rows.  Addresses are a uniform per-row base plus
 // one 32-bit per-lane offset; nothing in the loop waits on memory.
+// Largest per-wavefront accumulator tile count (TM * TN) whose epilogue
+// evaluates GELU in registers.
+constexpr int kGeluEpilogueTiles = 8;
+
 template <int TM, int TN, bool FULL, int OUT>
 __device__ __forceinline__ void epilogue_tiles(const GemmArgs& P, char* C, float16v (&acc)[TM][TN],
                                                int64_t row0, int64_t col0, const float (&bz)[TN]) {
@@ -138,6 +142,14 @@ __device__ __forceinline__ void epilogue_tiles(const GemmArgs& P, char* C, float
       if (P.act == BG_ACT_RELU) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) v[e] = v[e] > 0.f ? v[e] : 0.f;
+      } else if constexpr (TM * TN <= kGeluEpilogueTiles) {
+        // tanh-GELU on 16 values at a time (the tile fence below keeps the
+        // compiler from interleaving tiles); wider wavefront tiles leave no
+        // registers for it and take the separate f32 pass instead.
+        if (P.act == BG_ACT_GELU_TANH) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) v[e] = gelu_tanh_ref(v[e]);
+        }
       }
       const bool col_ok = FULL || cl + j * 32 < P.N;
 #pragma unroll
@@ -754,6 +766,22 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch) {
 namespace bg {
 
 // GEMM launch with C described by (c, ldc, stride_c, out_dtype, act).
+// True when run_gemm would pick a kernel whose epilogue applies GELU (the
+// direct-to-LDS kernel with 128-wide wavefront tiles).
+static bool gelu_in_epilogue(const bg_matmul_desc& d, const Record& a, const Record& b) {
+  if (d.in_dtype == BG_F32 || !d.trans_b) return false;
+  const int64_t es = dtype_size(d.in_dtype);
+  const void* A = a.ptr() + d.offset_a * es;
+  const void* B = b.ptr() + d.offset_b * es;
+  const bool vec = aligned_to(A, 16) && aligned_to(B, 16) && d.k % 8 == 0 && d.lda % 8 == 0 &&
+                   d.ldb % 8 == 0 && d.stride_a % 8 == 0 && d.stride_b % 8 == 0;
+  const int64_t a_span = ((d.m - 1) * d.lda + d.k) * es;
+  const int64_t b_span = ((d.n - 1) * d.ldb + d.k) * es;
+  if (!vec || a_span >= (int64_t(1) << 31) || b_span >= (int64_t(1) << 31)) return false;
+  const LdsCfg c = choose_lds_cfg(d.m, d.n, d.k, d.batch);
+  return c != LdsCfg::T256x256x64s2 && c != LdsCfg::T256x256x32s4;
+}
+
 static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
                      const Record* bias, void* c, int64_t ldc, int64_t stride_c, int out_dtype, int act) {
   const int64_t es = dtype_size(d.in_dtype);
@@ -861,7 +889,7 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
 void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
                    const Record* bias, Record& out) {
   if (d.batch > 65535) fail(BG_E_UNSUPPORTED, "matmul: batch > 65535");
-  if (d.act != BG_ACT_GELU_TANH) {
+  if (d.act != BG_ACT_GELU_TANH || gelu_in_epilogue(d, a, b)) {
     run_gemm(ctx, d, a, b, bias, out.ptr(), d.ldc, d.stride_c, d.out_dtype, d.act);
     return;
   }

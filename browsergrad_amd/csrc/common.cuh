@@ -69,4 +69,40 @@ __device__ __forceinline__ float gelu_tanh_ref(float x) {
   return half_x * one_plus;
 }
 
+// Raw buffer descriptor in four SGPRs: 48-bit base, stride 0, size in bytes
+// (offsets at or beyond it read zeros), gfx950 raw-buffer format word.
+typedef uint32_t sgpr4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ sgpr4_t buffer_rsrc(const void* base, uint32_t nbytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return sgpr4_t{uint32_t(a), uint32_t(a >> 32) & 0xffffu, nbytes, 0x00020000u};
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
+}
+
+// buffer_load_dwordx4 ... lds: lane L copies the 16 bytes at voffset +
+// soffset of the buffer to LDS byte lds_base + 16 L (lds_base wave-uniform).
+// Issued as inline assembly on purpose: the compiler cannot tell which LDS
+// bytes such a copy writes, so for the builtin form it makes every later LDS
+// read wait for all outstanding copies (vmcnt(0)), which serialises a
+// multi-stage prefetch ring.  Callers order LDS reads after the copies they
+// need with s_waitcnt vmcnt(N) and a workgroup barrier themselves.
+// M0 holds the LDS base (set by the compiler for the asm operand).  The
+// compiler does not look inside the asm for hazards, so the asm opens with
+// five wait states: a VMEM instruction must not read an SGPR (descriptor,
+// soffset) fewer than five wait states after a VALU wrote it (for example a
+// v_readlane restoring a spilled SGPR), and M0 needs one after its write.
+__device__ __forceinline__ void dma16_to_lds(uint32_t lds_base, uint32_t voffset, sgpr4_t rsrc,
+                                             uint32_t soffset) {
+  asm volatile(
+      "s_nop 4\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds"
+      :
+      : "{m0}"(lds_base), "v"(voffset), "s"(rsrc), "s"(soffset)
+      : "memory");
+}
+
 }  // namespace bgk

@@ -30,6 +30,7 @@
 //     multiply).
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.cuh"
@@ -439,11 +440,11 @@ __device__ __forceinline__ void fa2_softmax(float16v (&s)[2], int j0, int qi, in
 #pragma unroll
       for (int e = 0; e < 8; ++e) sp[kb][e] = fa2_pack<BF16>(s[kb][2 * e], s[kb][2 * e + 1]);
     if constexpr (!BF16) {
+      // IEEE maximum (NaN-propagating, like NumPy's max) pairs into
+      // v_pk_maximum3_f16: 8 instructions for the 16 packed pairs.
       fa_h2 m2 = __builtin_bit_cast(fa_h2, sp[0][0]);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(fa_h2, sp[kb][e]));
+      for (int i = 1; i < 16; ++i) m2 = __builtin_elementwise_maximum(m2, __builtin_bit_cast(fa_h2, sp[i >> 3][i & 7]));
       mt = fmaxf(static_cast<float>(m2[0]), static_cast<float>(m2[1]));
     } else {
       mt = -INFINITY;
@@ -636,6 +637,7 @@ __global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint
   if (t < nt) step(C0{}, t, s_a, s_b);
   if (t + 1 < nt) step(C1{}, t + 1, s_b, s_a);
   if (t + 2 < nt) step(C2{}, t + 2, s_a, s_b);
+  fa2_wait_vm_lgkm0<0>();  // no DMA into this workgroup's LDS outlives it
 
   // O = acc / l.  O^T layout: lane = query column, register e holds d row
   // 8*(e/4) + 4*hi + e%4 (+ 32*db): four consecutive d per (e/4) group.
@@ -675,6 +677,273 @@ __global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint
                        fa2_pack<true>(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv));
       }
   }
+}
+
+// ---- v6: 32-key halves, softmax folded into the MFMA, two workgroups per CU --
+//
+// One workgroup = 8 wavefronts x 32 queries of one (batch, head); K and V
+// tiles of 64 keys stream through a 4-slot LDS ring (buffer_load ... lds,
+// each wavefront copies a 1 KB slice of K and of V per tile; tile j lives in
+// slot j % 4, step t refills the slot of tile t-1 with tile t+3 after the
+// step's barrier).  Each wavefront works through a tile in two 32-key halves:
+//   x  = K Q'^T + (-m)       4 MFMAs (32x32x16), Q' = Q * scale * log2(e)
+//   P  = exp2(x)             packed to 16 bits, row sum by v_dot2 on the packed P
+//   O^T += V^T P^T           4 MFMAs, V^T fragments by ds_read_b64_tr_b16
+// Q' is rounded to the input dtype once per wavefront, and the S chain starts
+// from an accumulator block holding -m (the wavefront's reference max per
+// query), so the fast path has no per-score FMA and no per-tile max.  The
+// reference max only has to keep P finite in 16 bits: it is set exactly on
+// the first half a wavefront sees and moved again only when some P of a half
+// overflows (its f32 row sum then exceeds 2^20); that slow path takes the
+// exact max, rescales O and l and recomputes P.  At 124 registers two
+// workgroups share a CU, four wavefronts per SIMD, which hides MFMA, LDS and
+// transcendental latency across wavefronts.
+// Numerics: S is not rounded to 16 bits before scaling (the reference's AMP
+// matmul rounds it); Q' carries one 16-bit rounding instead.  Both are below
+// the input precision; the parity tests bound the result at the 16-bit tolerance.
+constexpr int kFa6Ring = 4;
+
+__device__ __forceinline__ float fa6_muse(float m_run) { return m_run == -INFINITY ? 0.f : m_run; }
+
+// Per-lane LDS byte offsets of the K and V fragment reads within a tile.
+// K: row r = 32 kb + lane % 32, chunk 2 dc + lane / 32, swizzled by
+// (r >> 1) & 7 (the same for both kb), so kb only adds 4096.  V (transpose
+// reads): row = 32 kb + 16 mm + 8 r + rl with rl = 4 (lane / 32) +
+// (lane % 16) / 4 and row % 4 = (lane / 4) % 4, so kb, mm and r only add
+// multiples of 1024; d = 32 db + 16 ((lane / 16) % 2) + 4 (lane % 4).
+struct Fa6Offs {
+  uint32_t k[4];
+  uint32_t v[2];
+  __device__ __forceinline__ Fa6Offs() {
+    const int lane = threadIdx.x & 63, hi = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) k[dc] = uint32_t(fa2_k_unit(l32, dc * 2 + hi) * 16);
+    const int rl = 4 * hi + ((lane & 15) >> 2);
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const int d = db * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      v[db] = uint32_t(fa2_v_unit(rl, d >> 3) * 16 + (d & 4) * 2);
+    }
+  }
+};
+
+template <bool BF16>
+__device__ __forceinline__ void fa6_pv_half(const char* vt, const Fa6Offs& o, const fa_u4 (&pf)[2], float16v (&acc)[2],
+                                            int h) {
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      fa_v4s part[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const char* addr = vt + o.v[db] + (h * 32 + mm * 16 + r * 8) * 128;
+        part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) fa_v4s*)(reinterpret_cast<uintptr_t>(addr)));
+      }
+      const fa_u4 vf = __builtin_bit_cast(fa_u4, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+      acc[db] = fa2_mfma<BF16>(vf, pf[mm], acc[db]);
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t fa6_scale2(uint32_t w, float sl2) {
+  return fa2_pack<BF16>(fa2_lo<BF16>(w) * sl2, fa2_hi<BF16>(w) * sl2);
+}
+
+template <bool BF16>
+__device__ __forceinline__ float16v fa6_scores_half(const char* kt, const Fa6Offs& o, const fa_u4 (&qf)[4],
+                                                    const float16v& mneg, int h) {
+  fa_u4 kf[4];
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc) kf[dc] = *reinterpret_cast<const fa_u4*>(kt + o.k[dc] + h * 4096);
+  float16v s = fa2_mfma<BF16>(kf[0], qf[0], mneg);
+#pragma unroll
+  for (int dc = 1; dc < 4; ++dc) s = fa2_mfma<BF16>(kf[dc], qf[dc], s);
+  return s;
+}
+
+// P = exp2(x + delta) packed as two B fragments; returns the row sum of the
+// packed values.
+template <bool BF16, bool ADD>
+__device__ __forceinline__ float fa6_exp(const float16v& x, float delta, fa_u4 (&pf)[2]) {
+  const fa_h2 ones = {(_Float16)1.f, (_Float16)1.f};
+  float l_acc = 0.f;
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm) {
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = mm * 8 + 2 * j;
+      const float x0 = ADD ? x[e] + delta : x[e];
+      const float x1 = ADD ? x[e + 1] + delta : x[e + 1];
+      pk[j] = fa2_pack<BF16>(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
+      if constexpr (BF16) l_acc += fa2_lo<true>(pk[j]) + fa2_hi<true>(pk[j]);
+      else l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_h2, pk[j]), ones, l_acc, false);
+    }
+    pf[mm] = fa_u4{pk[0], pk[1], pk[2], pk[3]};
+  }
+  return l_acc;
+}
+
+template <bool BF16, bool CAUSAL>
+__global__ void __launch_bounds__(kFa2NW * 64, 2) fa6_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
+  __shared__ fa_u4 smem[2 * kFa6Ring * kFa2Tile / 16];
+  char* sb = reinterpret_cast<char*>(smem);
+  char* kring = sb;
+  char* vring = sb + kFa6Ring * kFa2Tile;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hi = lane >> 5;
+  const int bh = blockIdx.x;
+  const int qblk = P.n_qblocks - 1 - int(blockIdx.y);  // heavy query blocks first
+  const int b = bh / P.H, h = bh % P.H;
+  const int q0 = qblk * kFa2BQ;
+  const int q0w = q0 + w * kFa2QW;
+  const int qi = q0w + (lane & 31);
+
+  const uint16_t* Qp = P.q + b * P.q_sb + h * P.q_sh;
+  const uint16_t* Kp = P.k + b * P.k_sb + h * P.k_sh;
+  const uint16_t* Vp = P.v + b * P.v_sb + h * P.v_sh;
+  const bgk::sgpr4_t rk = bgk::buffer_rsrc(Kp, k_bytes);
+  const bgk::sgpr4_t rv = bgk::buffer_rsrc(Vp, v_bytes);
+
+  const int nt_all = (P.Sk + kFa2BK - 1) / kFa2BK;
+  const int nt = CAUSAL ? min(nt_all, (q0 + kFa2BQ + kFa2BK - 1) / kFa2BK) : nt_all;
+  const int ntw = CAUSAL ? min(nt, (q0w + kFa2QW + kFa2BK - 1) / kFa2BK) : nt;
+
+  const int u = w * 64 + lane;
+  const int krow = u >> 3, pc = u & 7;
+  const uint32_t koff = uint32_t((int64_t(krow) * P.k_ss + ((pc ^ ((krow >> 1) & 7)) * 8)) * 2);
+  const uint32_t voff = uint32_t((int64_t(krow) * P.v_ss + ((pc ^ ((krow & 3) << 1)) * 8)) * 2);
+  const uint32_t kstep = uint32_t(int64_t(kFa2BK) * P.k_ss * 2);
+  const uint32_t vstep = uint32_t(int64_t(kFa2BK) * P.v_ss * 2);
+  const uint32_t kl = bgk::lds_addr(kring) + uint32_t(w) * 1024u;
+  const uint32_t vl = bgk::lds_addr(vring) + uint32_t(w) * 1024u;
+  auto issue = [&](int j) {
+    const bool real = j >= 0 && j < nt;
+    const bool ok = real && j * kFa2BK + krow < P.Sk;
+    const uint32_t sl = uint32_t(j & 3) * kFa2Tile;
+    bgk::dma16_to_lds(kl + sl, ok ? koff : kFa2Oob, rk, real ? uint32_t(j) * kstep : 0u);
+    bgk::dma16_to_lds(vl + sl, ok ? voff : kFa2Oob, rv, real ? uint32_t(j) * vstep : 0u);
+  };
+
+  const float sl2 = P.sl2;
+  fa_u4 qf[4];
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc)
+    qf[dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
+                       : fa_u4{0u, 0u, 0u, 0u};
+  issue(0);
+  issue(1);
+  issue(2);
+  fa2_wait_vm_lgkm0<0>();  // also retires the Q loads in the compiler's bookkeeping
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qf[dc][i] = fa6_scale2<BF16>(qf[dc][i], sl2);
+
+  float16v acc[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[db][e] = 0.f;
+  float16v mneg;  // -m_use in every row of this lane's query column
+#pragma unroll
+  for (int e = 0; e < 16; ++e) mneg[e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const Fa6Offs offs;
+
+  for (int t = 0; t < nt; ++t) {
+    if (t > 0) {
+      fa2_wait_vm_lgkm0<4>();
+      __builtin_amdgcn_s_barrier();
+    }
+    issue(t + 3);
+    if (t < ntw) {
+      const char* kt = kring + (t & 3) * kFa2Tile;
+      const char* vt = vring + (t & 3) * kFa2Tile;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j0 = t * kFa2BK + hh * 32;
+        float16v x = fa6_scores_half<BF16>(kt, offs, qf, mneg, hh);
+        if ((CAUSAL && j0 + 31 > q0w) || (j0 + 32 > P.Sk)) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kj = j0 + 8 * (e >> 2) + 4 * hi + (e & 3);
+            if (kj >= P.Sk || (CAUSAL && kj > qi)) x[e] = -INFINITY;
+          }
+        }
+        fa_u4 pf[2];
+        float l_acc = fa6_exp<BF16, false>(x, 0.f, pf);
+        if (__any(l_acc > 1048576.f || m_run == -INFINITY)) {  // wave-uniform
+          // Exact max of this half (x = scores - m_use), moved reference.
+          float mt = -INFINITY;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mt = fmaxf(mt, x[e]);
+          mt = fmaxf(mt, fa2_xor32(mt));
+          const float m_use = fa6_muse(m_run);
+          const float m_tile = mt + m_use;
+          const float m_new = fmaxf(m_run, m_tile);
+          const float alpha = m_run == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
+          const float m_use_new = fa6_muse(m_run);
+          l_acc = fa6_exp<BF16, true>(x, m_use - m_use_new, pf);
+          l_run *= alpha;
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mneg[e] = -m_use_new;
+        }
+        l_run += l_acc;
+        fa6_pv_half<BF16>(vt, offs, pf, acc, hh);
+      }
+    }
+  }
+  fa2_wait_vm_lgkm0<0>();
+
+  const float lt = l_run + fa2_xor32(l_run);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (qi >= P.Sq) return;
+  char* Ob = static_cast<char*>(P.o);
+  const int64_t obase = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d0 = db * 32 + 8 * gq + 4 * hi;
+      const float y0 = acc[db][4 * gq] * inv, y1 = acc[db][4 * gq + 1] * inv;
+      const float y2 = acc[db][4 * gq + 2] * inv, y3 = acc[db][4 * gq + 3] * inv;
+      if (P.out_dtype == 0)
+        *reinterpret_cast<float4*>(Ob + (obase + d0) * 4) = make_float4(y0, y1, y2, y3);
+      else if (P.out_dtype == 1)
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<false>(y0, y1), fa2_pack<false>(y2, y3));
+      else
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<true>(y0, y1), fa2_pack<true>(y2, y3));
+    }
+}
+
+template <bool BF16, bool CAUSAL, bool ROUND_S>
+void launch_fa6(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uint32_t vb) {
+  (void)ROUND_S;  // v6 has one numerics for both (see the kernel's header)
+  bg::dispatch(ctx, fa6_fwd_kernel<BF16, CAUSAL>, dim3(unsigned(bh), unsigned(nqb), 1),
+               dim3(kFa2NW * 64), 0, A, kb, vb);
+}
+
+// BG_ATTN_KERNEL=2 selects the v2 kernel (reference rounding of S to 16
+// bits, one workgroup per CU) instead of v6, for comparisons.
+int attn_version() {
+  static const int v = [] {
+    const char* e = std::getenv("BG_ATTN_KERNEL");
+    return e && e[0] == '2' ? 2 : 6;
+  }();
+  return v;
 }
 
 template <bool BF16, bool CAUSAL, bool ROUND_S>
@@ -747,7 +1016,9 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     const bool r = d.round_scores != 0;
     const uint32_t kb = uint32_t(k_head), vb = uint32_t(v_head);
     Profile prof(ctx, bf ? "attention_bf16" : "attention_f16", bytes, flops);
-#define BG_FA2(B_, C_, R_) launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb)
+#define BG_FA2(B_, C_, R_)                                              \
+  (attn_version() == 6 ? launch_fa6<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb) \
+                       : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
     if (bf) {
       if (c) { if (r) BG_FA2(true, true, true); else BG_FA2(true, true, false); }
       else { if (r) BG_FA2(true, false, true); else BG_FA2(true, false, false); }

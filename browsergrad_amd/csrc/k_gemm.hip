@@ -61,6 +61,8 @@ struct GemmArgs {
   int act;          // BG_ACT_*
   int out_dtype;    // BG_F32 / BG_F16 / BG_BF16
   int vec_store;    // C rows can take 4-element vector stores (ldc % 4, alignment)
+  int64_t k_chunk;  // f32 split-K: K elements per blockIdx.y slice (0: no split)
+  float* ws;        // f32 split-K: [splits][M][N] partial sums
 };
 
 // XCD-aware tile index -> (tile_m, tile_n).  Workgroups are dispatched
@@ -566,6 +568,9 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  // Split-K: this workgroup sums k in [kbeg, kend) only.
+  const int64_t kbeg = P.k_chunk ? int64_t(blockIdx.y) * P.k_chunk : 0;
+  const int64_t kend = P.k_chunk ? min(P.K, kbeg + P.k_chunk) : P.K;
 
   float16v acc[TM][TN];
 #pragma unroll
@@ -590,14 +595,14 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
       if (ALIGNED) {
         const int64_t kc = gk < P.K ? gk : P.K - 4;
         const float4 x = *reinterpret_cast<const float4*>(base + rr * ld + kc);
-        regs[i] = (gr < rows && gk < P.K) ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+        regs[i] = (gr < rows && gk < kend) ? x : make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
         float e[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t kc = gk + j < P.K ? gk + j : P.K - 1;
           const float x = base[rr * ld + kc];
-          e[j] = (gr < rows && gk + j < P.K) ? x : 0.f;
+          e[j] = (gr < rows && gk + j < kend) ? x : 0.f;
         }
         regs[i] = make_float4(e[0], e[1], e[2], e[3]);
       }
@@ -614,14 +619,14 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
       if (ALIGNED) {
         const int64_t nc = gn < P.N ? gn : P.N - 4;
         const float4 x = *reinterpret_cast<const float4*>(B + kc * P.ldb + nc);
-        regs[i] = (gk < P.K && gn < P.N) ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+        regs[i] = (gk < kend && gn < P.N) ? x : make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
         float e[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t nc = gn + j < P.N ? gn + j : P.N - 1;
           const float x = B[kc * P.ldb + nc];
-          e[j] = (gk < P.K && gn + j < P.N) ? x : 0.f;
+          e[j] = (gk < kend && gn + j < P.N) ? x : 0.f;
         }
         regs[i] = make_float4(e[0], e[1], e[2], e[3]);
       }
@@ -660,14 +665,14 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
     }
   };
 
-  const int nk = int((P.K + BK32 - 1) / BK32);
-  fetch(0);
+  const int nk = int((kend - kbeg + BK32 - 1) / BK32);
+  fetch(kbeg);
   commit(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const float* As = smem + (kt & 1) * STAGE_FLOATS;
     const float* Bs = As + A_FLOATS;
-    if (kt + 1 < nk) fetch(int64_t(kt + 1) * BK32);
+    if (kt + 1 < nk) fetch(kbeg + int64_t(kt + 1) * BK32);
 #pragma unroll
     for (int s = 0; s < BK32 / 2; ++s) {
       const int k = 2 * s + (lane >> 5);
@@ -686,7 +691,31 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
     __syncthreads();
   }
 
+  if (P.k_chunk) {
+    // Partial sums, plain f32, into this slice of the workspace.
+    GemmArgs Q = P;
+    Q.bias = nullptr;
+    Q.round_dtype = 0;
+    Q.act = BG_ACT_NONE;
+    Q.out_dtype = BG_F32;
+    Q.ldc = P.N;
+    direct_epilogue<TM, TN, false>(Q, reinterpret_cast<char*>(P.ws + int64_t(blockIdx.y) * P.M * P.N), acc,
+                                   m0 + wm * WTM, n0 + wn * WTN);
+    return;
+  }
   direct_epilogue<TM, TN, false>(P, C, acc, m0 + wm * WTM, n0 + wn * WTN);
+}
+
+// Split-K finish: C = epilogue(sum over slices in slice order).
+template <int OUT>
+__global__ void __launch_bounds__(256) gemm32_splitk_reduce(GemmArgs P, int splits) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= P.M * P.N) return;
+  const int64_t m = i / P.N, n = i % P.N;
+  float s = P.ws[i];
+  for (int k = 1; k < splits; ++k) s += P.ws[int64_t(k) * P.M * P.N + i];
+  const float v = epilogue_value(P, s, P.bias ? P.bias[n] : 0.f);
+  store_elem<OUT>(static_cast<char*>(P.C) + (m * P.ldc + n) * (OUT == BG_F32 ? 4 : 2), v);
 }
 
 template <int BM, int BN, bool BF16, int SWZ>
@@ -817,6 +846,32 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
                          d.ldb % 4 == 0 && d.k % 4 == 0 && (d.trans_b || d.n % 4 == 0) &&
                          d.stride_a % 4 == 0 && d.stride_b % 4 == 0;
     Profile prof(ctx, "gemm_f32", bytes, flops);
+    // Few output tiles and a long K (C1's 64 x 784 x 128): one workgroup
+    // would walk K alone, one global-memory latency per 16-wide k step.
+    // Split K over blockIdx.y (two k steps per slice), write f32
+    // partials, and finish with one summing pass that applies the epilogue.
+    const int64_t nk = (d.k + BK32 - 1) / BK32;
+    const int64_t tiles = int64_t(P.tiles_m) * P.tiles_n;
+    if (d.batch == 1 && tiles <= 16 && nk >= 8) {
+      const int64_t splits = std::min<int64_t>(64, (nk + 1) / 2);
+      P.k_chunk = ((nk + splits - 1) / splits) * BK32;
+      const int64_t used = (d.k + P.k_chunk - 1) / P.k_chunk;
+      P.ws = static_cast<float*>(scratch(ctx, size_t(used * d.m * d.n * 4)));
+      dim3 grid(unsigned(tiles), unsigned(used), 1);
+      if (d.trans_b) {
+        if (aligned) bg::dispatch(ctx, gemm32_kernel<128, 128, true, true>, grid, dim3(256), 0, P);
+        else bg::dispatch(ctx, gemm32_kernel<128, 128, true, false>, grid, dim3(256), 0, P);
+      } else {
+        if (aligned) bg::dispatch(ctx, gemm32_kernel<128, 128, false, true>, grid, dim3(256), 0, P);
+        else bg::dispatch(ctx, gemm32_kernel<128, 128, false, false>, grid, dim3(256), 0, P);
+      }
+      const dim3 rg(unsigned((d.m * d.n + 255) / 256));
+      const int sp = int(used);
+      if (out_dtype == BG_F32) bg::dispatch(ctx, gemm32_splitk_reduce<BG_F32>, rg, dim3(256), 0, P, sp);
+      else if (out_dtype == BG_F16) bg::dispatch(ctx, gemm32_splitk_reduce<BG_F16>, rg, dim3(256), 0, P, sp);
+      else bg::dispatch(ctx, gemm32_splitk_reduce<BG_BF16>, rg, dim3(256), 0, P, sp);
+      return;
+    }
     launch32<128, 128>(ctx, P, d.batch, d.trans_b != 0, aligned);
     return;
   }

@@ -22,6 +22,8 @@ realizers do), so no structural hash cache is needed.
 """
 from __future__ import annotations
 
+from ..errors import ShapeError  # the reference's _errors.ShapeError (one class package-wide)
+
 from dataclasses import dataclass
 from typing import Any, FrozenSet, List, Tuple
 
@@ -73,8 +75,6 @@ KNOWN_DTYPES: FrozenSet[str] = frozenset({
 MAX_ELEMENTS = 2 ** 34  # sized for one MI355X (288 GB HBM); the reference caps at 2**30
 
 
-class ShapeError(ValueError):
-    """Malformed UOp (the reference's _errors.ShapeError)."""
 
 
 @dataclass(frozen=True, eq=False)

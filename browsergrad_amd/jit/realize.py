@@ -34,6 +34,7 @@ import numpy as np
 from .. import _native as N
 from ..errors import JitNotImplementedError, KernelError
 from .amp import insert_cast_pass
+from .attention_forward import validate_attention_forward_node
 from .buffers import BufferTable, GpuBufferTable
 from .fusion import fuse
 from .gpu_plan import build_gpu_execution_submission
@@ -290,15 +291,12 @@ def _h_fused_elementwise(n: UOp, w: _Walk) -> int:
 
 
 def _h_attention_forward(n: UOp, w: _Walk) -> int:
+    """ATTENTION_FORWARD (_realize_webgpu.py:280-302): the node must pass the
+    typed contract; then the bridge's attention with no mask."""
+    c = validate_attention_forward_node(n)
     q, k, v = n.inputs
-    b, h, sq, d = q.shape
-    sk = k.shape[2]
-    arg = n.arg if isinstance(n.arg, dict) else {}
-    scale = float(arg.get("scale", 1.0 / np.sqrt(d)))
-    if arg.get("is_causal") or arg.get("causal"):
-        return w.br.attention_ex(w.h(q), w.h(k), w.h(v), batch=b, heads=h, sq=sq, sk=sk, d=d, scale=scale,
-                                 causal=True, in_dtype=q.dtype, out_dtype=n.dtype)
-    return w.br.flash_attention(w.h(q), w.h(k), w.h(v), None, b, h, sq, sk, d, scale, n.dtype)
+    return w.br.flash_attention(w.h(q), w.h(k), w.h(v), None, c.batch, c.heads, c.query_length, c.key_length,
+                                c.depth, c.scale, n.dtype)
 
 
 def _h_hip_attention(n: UOp, w: _Walk) -> int:

@@ -30,6 +30,7 @@ from typing import Any, Optional, Sequence, Tuple
 
 import numpy as np
 
+from ..errors import JitNotImplementedError
 from .buffers import BufferTable
 from .ir import (
     OP_ADD, OP_CAST, OP_CMP, OP_CONST, OP_DIV, OP_EXP, OP_LAYER_NORM, OP_LOG, OP_MATMUL, OP_MUL,
@@ -368,7 +369,37 @@ def scaled_dot_product_attention(q: Tensor, k: Tensor, v: Tensor, is_causal: boo
     return attn @ v
 
 
+def attention_forward(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """Typed dense rank-4 float32 attention forward (bg.kernels.attention_forward,
+    packages/browsergrad-jit/src/python/index.ts:212-245): the contract is
+    inferred (shape / dtype / ceilings) and the ATTENTION_FORWARD node carries
+    the canonical scale and mask "none"."""
+    from .attention_forward import infer_attention_forward_contract, validate_attention_forward_node
+    from .ir import OP_ATTENTION_FORWARD
+    if any(type(t) is not Tensor for t in (q, k, v)):
+        raise TypeError("bg.kernels.attention_forward requires Tensor inputs for query, key, and value")
+    if k.session is not q.session or v.session is not q.session:
+        raise ShapeError("bg.kernels.attention_forward inputs must belong to one session")
+    c = infer_attention_forward_contract(q.uop, k.uop, v.uop)
+    uop = UOp(OP_ATTENTION_FORWARD, (q.uop, k.uop, v.uop), c.output_shape, "float32",
+              {"scale": c.scale, "mask": "none"})
+    validate_attention_forward_node(uop)
+    return Tensor(uop, q.session)
+
+
+def flash_attention(q: Tensor, k: Tensor, v: Tensor, mask: Any = None, scale: Any = None) -> Tensor:
+    """Compatibility alias of attention_forward (index.ts:248-265): masks and
+    custom scales are refused."""
+    if mask is not None or scale is not None:
+        raise JitNotImplementedError(
+            "bg.kernels.flash_attention now aliases the exact typed attention_forward v1 profile and accepts "
+            "neither additive masks nor custom scale. Use torch.nn.functional.scaled_dot_product_attention for "
+            "those semantics.")
+    return attention_forward(q, k, v)
+
+
 __all__ = [
     "Tensor", "Session", "autocast", "active_autocast", "promote", "broadcast_shape",
     "where", "relu", "tanh", "gelu", "softmax", "linear", "layer_norm", "scaled_dot_product_attention",
+    "attention_forward", "flash_attention",
 ]

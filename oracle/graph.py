@@ -14,6 +14,8 @@ _realize.py (`realize`, :1854-1923) handler by handler:
   WHERE  np.where(cond, a, b) in the node dtype            :1453-1459
   FUSED_ELEMENTWISE  the op list in order                  :1557-1600
   FUSED_SOFTMAX  e = exp(x - max); e / sum(e)              :1603-1614
+  ATTENTION_FORWARD  execute_attention_forward_arrays
+                 (_framework_contracts.py:2881-2932)          :1440-1450
 
 Only cast insertion (browsergrad_amd.jit.amp, which mirrors _amp.py) is
 applied before evaluation; fusion does not change values.  Two restatement
@@ -36,7 +38,7 @@ from browsergrad_amd.jit.amp import insert_cast_pass
 from browsergrad_amd.jit.buffers import BufferTable
 from browsergrad_amd.jit.ir import UOp, toposort
 
-from .ops import round_bf16
+from .ops import attention_forward_f32, round_bf16
 
 _CMP = {"eq": np.equal, "ne": np.not_equal, "lt": np.less, "le": np.less_equal, "gt": np.greater,
         "ge": np.greater_equal}
@@ -135,6 +137,8 @@ def evaluate(root: UOp, bt: BufferTable, *, amp: bool = True) -> np.ndarray:
             m = x.max(axis=ax, keepdims=True)
             e = np.exp(x - m)
             out = e / e.sum(axis=ax, keepdims=True)
+        elif op == "ATTENTION_FORWARD":
+            out = attention_forward_f32(ins[0], ins[1], ins[2], n.arg["scale"])
         elif op == "FUSED_ELEMENTWISE":
             steps = []
             for code, l, r in n.arg["ops"]:

@@ -257,6 +257,20 @@ def attention_online_f32(q, k, v, scale, mask=None):
     return ((p @ v.astype(np.float64)) * inv).astype(F32)
 
 
+def attention_forward_f32(q, k, v, scale):
+    """Typed ATTENTION_FORWARD in float32, step for step as
+    _framework_contracts.py:2906-2929 (execute_attention_forward_arrays):
+    scores = q @ k^T (f32 matmul), * f32(scale), row max, exp(scores - max),
+    f32 row sum, divide, @ v.  Pinned by attention_f64 (tests)."""
+    q, k, v = (np.asarray(t, dtype=F32) for t in (q, k, v))
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        scores = np.matmul(q, np.swapaxes(k, -1, -2))
+        scores = np.asarray(scores * np.float32(scale), dtype=F32)
+        e = np.exp(scores - scores.max(axis=-1, keepdims=True))
+        den = e.sum(axis=-1, keepdims=True, dtype=F32)
+        return np.array(np.matmul(e / den, v), dtype=F32)
+
+
 def attention_f64(q, k, v, scale, causal=False):
     """Brute-force float64 softmax attention (the mathematical definition)."""
     q, k, v = (np.asarray(t, dtype=np.float64) for t in (q, k, v))

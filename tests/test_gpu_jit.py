@@ -237,3 +237,29 @@ def test_plan_executor_refusals(bridge, rng):
     with pytest.raises(KernelError, match="aliases an input buffer"):
         bridge.run_tensor_plan_resident(plan_load, [data], "float32")
     assert bridge.aliveHandleCount() >= 0
+
+
+# ---- typed ATTENTION_FORWARD (_framework_contracts.py:2792-2932) -------------------
+
+def test_attention_forward_typed(bridge, table, rng):
+    from browsergrad_amd.errors import ShapeError
+    from browsergrad_amd.jit.attention_forward import (
+        execute_attention_forward_hip, infer_attention_forward_contract, validate_attention_forward_node,
+    )
+    from browsergrad_amd.jit.tensor import attention_forward
+    s = Session()
+    arrs = [rng.standard_normal((2, 3, 37, 64), dtype=np.float32) for _ in range(3)]
+    q, k, v = (s.from_numpy(a) for a in arrs)
+    y = attention_forward(q, k, v)
+    ref = G.evaluate(y.uop, s.buffers)
+    alive = bridge.aliveHandleCount()
+    out = realize_hip(y.uop, s.buffers, table)
+    _check(out, ref, 1e-4)
+    c = validate_attention_forward_node(y.uop)
+    _check(execute_attention_forward_hip(c, tuple(arrs), bridge), ref, 1e-4)
+    assert bridge.aliveHandleCount() == alive + table.stats()["handles_alive"]
+    # Scores that overflow float32 surface as a non-finite output and are refused.
+    big = np.full((1, 1, 2, 4), 1e20, np.float32)
+    c2 = infer_attention_forward_contract(big, big, big)
+    with pytest.raises(ShapeError, match="output must remain finite"):
+        execute_attention_forward_hip(c2, (big, big, big), bridge)

@@ -336,9 +336,9 @@ __global__ void __launch_bounds__(256) gemm16_kernel(GemmArgs P) {
 //     Operand fragments are double buffered in registers across sub-steps.
 //   * LDS layout: the tile is viewed as 128-byte lines (RPL = 128 / (2*BK)
 //     rows per line); a line's eight 16-byte units are XOR-permuted by the
-//     line index so that ds_read_b128 -- which serves the even lanes of a
-//     16-lane group in one cycle and the odd lanes in the next -- reads eight
-//     distinct units per cycle (measured: zero SQ_LDS_BANK_CONFLICT).
+//     line index so that the 16 lanes ds_read_b128 serves per cycle hit 16
+//     distinct 4-bank groups (measured: zero SQ_LDS_BANK_CONFLICT for BK=64;
+//     BK=32's earlier line & 7 permutation measured 2-way conflicts).
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -348,8 +348,14 @@ template <int BK>
 struct LdsLayout {
   static constexpr int CPR = BK / 8;    // 16-byte chunks per row
   static constexpr int RPL = 8 / CPR;   // rows per 128-byte line
+  // ds_read_b128 serves 16 lanes per cycle across 64 banks (16 groups of
+  // four): the 16 rows a group reads must land in 16 distinct groups, i.e.
+  // unit % 16 must be a permutation.  128-byte rows: unit % 16 =
+  // 8 (r & 1) + (c ^ ((r >> 1) & 7)).  64-byte rows (two per line): the two
+  // rows of a line differ in bit 2 of the slot, so lines of one parity need
+  // distinct low two bits: (line >> 1) & 3.
   __device__ static __forceinline__ int perm(int line) {
-    return RPL == 1 ? ((line >> 1) & 7) : (line & 7);
+    return RPL == 1 ? ((line >> 1) & 7) : ((line >> 1) & 3);
   }
   // 16-byte unit holding (row r, chunk c).
   __device__ static __forceinline__ int unit(int r, int c) {

@@ -384,19 +384,19 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 // outside the matrix get kOob (the load returns zeros).  The k offset of a
 // stage is added through the scalar soffset, so issuing a stage costs one
 // instruction per 1 KB block.
-template <int R, int BK>
+template <int R, int BK, int NW = 4>
 struct TileLoads {
   static constexpr int INSTR = R * BK * 2 / 1024;  // wavefront instructions per tile
-  static_assert(INSTR % 4 == 0, "tile must split over four wavefronts");
-  uint32_t voff[INSTR / 4];
-  uint32_t chunk_k[INSTR / 4];  // k offset of the lane's chunk (elements), for K tails
+  static_assert(INSTR % NW == 0, "tile must split evenly over the wavefronts");
+  uint32_t voff[INSTR / NW];
+  uint32_t chunk_k[INSTR / NW];  // k offset of the lane's chunk (elements), for K tails
 
   __device__ __forceinline__ void init(int w, int64_t ld, int64_t row0, int64_t rows) {
     using L = LdsLayout<BK>;
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < INSTR / 4; ++i) {
-      const int u = (i * 4 + w) * 64 + lane;
+    for (int i = 0; i < INSTR / NW; ++i) {
+      const int u = (i * NW + w) * 64 + lane;
       const int line = u >> 3;
       const int sl = (u & 7) ^ L::perm(line);
       const int r = line * L::RPL + sl / L::CPR;
@@ -412,10 +412,10 @@ struct TileLoads {
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, char* lds_tile, int w, int64_t k0,
                                         int64_t K) const {
 #pragma unroll
-    for (int i = 0; i < INSTR / 4; ++i) {
+    for (int i = 0; i < INSTR / NW; ++i) {
       uint32_t off = voff[i];
       if constexpr (KTAIL) off = (k0 + chunk_k[i] < K) ? off : kOob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(lds_tile + (i * 4 + w) * 1024), 16, off,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(lds_tile + (i * NW + w) * 1024), 16, off,
                                                uint32_t(k0 * 2), 0, 0);
     }
   }
@@ -434,14 +434,19 @@ __device__ __forceinline__ void sched_pattern() {
   }
 }
 
-template <int BM, int BN, int BK, int S, bool BF16, bool FULL, bool KTAIL>
-__global__ void __launch_bounds__(256) gemm16_lds_kernel(GemmArgs P, uint32_t a_bytes, uint32_t b_bytes) {
+// WGM x WGN wavefronts per workgroup, each owning a (BM / WGM) x (BN / WGN)
+// block of C: 2 x 2 (one wavefront per SIMD) or 2 x 4 (two per SIMD, half
+// the accumulators each, so one wavefront's fragment-read waits overlap the
+// other's MFMAs).
+template <int BM, int BN, int BK, int S, bool BF16, bool FULL, bool KTAIL, int WGM = 2, int WGN = 2>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm16_lds_kernel(GemmArgs P, uint32_t a_bytes, uint32_t b_bytes) {
   using L = LdsLayout<BK>;
-  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int NW = WGM * WGN;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int KK = BK / 16;                         // 16-wide sub-steps per stage
+  constexpr int KK = BK / 16;                          // 16-wide sub-steps per stage
   constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
-  constexpr int NLD = (BM + BN) * BK * 2 / 1024 / 4;  // loads per wavefront per stage
+  constexpr int NLD = (BM + BN) * BK * 2 / 1024 / NW;  // loads per wavefront per stage
   static_assert(KK % 2 == 0, "fragment double buffering needs an even sub-step count");
   static_assert(NLD * (S - 1) < 64, "vmcnt range");
   __shared__ u32x4 smem[S * STAGE_BYTES / 16];
@@ -461,9 +466,9 @@ __global__ void __launch_bounds__(256) gemm16_lds_kernel(GemmArgs P, uint32_t a_
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  TileLoads<BM, BK> la;
-  TileLoads<BN, BK> lb;
+  const int wm = wave / WGN, wn = wave % WGN;
+  TileLoads<BM, BK, NW> la;
+  TileLoads<BN, BK, NW> lb;
   la.init(wave, P.lda, m0, P.M);
   lb.init(wave, P.ldb, n0, P.N);
 
@@ -735,17 +740,21 @@ void launch16(bg_ctx* ctx, const GemmArgs& P, int64_t batch, bool full, bool vec
     bg::dispatch(ctx, gemm16_kernel<BM, BN, BF16, false, false, SWZ>, grid, dim3(256), 0, P);
 }
 
-template <int BM, int BN, int BK, int S, bool BF16>
+template <int BM, int BN, int BK, int S, bool BF16, int WGM = 2, int WGN = 2>
 void launch16_lds(bg_ctx* ctx, const GemmArgs& P, int64_t batch, uint32_t a_bytes, uint32_t b_bytes) {
   dim3 grid(unsigned(P.tiles_m * P.tiles_n), 1, unsigned(batch));
+  const dim3 block(64 * WGM * WGN);
   const bool full = P.M % BM == 0 && P.N % BN == 0;
   const bool ktail = P.K % BK != 0;
   if (full && !ktail)
-    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, true, false>, grid, dim3(256), 0, P, a_bytes, b_bytes);
+    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, true, false, WGM, WGN>, grid, block, 0, P, a_bytes,
+                 b_bytes);
   else if (!ktail)
-    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, false, false>, grid, dim3(256), 0, P, a_bytes, b_bytes);
+    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, false, false, WGM, WGN>, grid, block, 0, P, a_bytes,
+                 b_bytes);
   else
-    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, false, true>, grid, dim3(256), 0, P, a_bytes, b_bytes);
+    bg::dispatch(ctx, gemm16_lds_kernel<BM, BN, BK, S, BF16, false, true, WGM, WGN>, grid, block, 0, P, a_bytes,
+                 b_bytes);
 }
 
 template <int BM, int BN>
@@ -767,14 +776,14 @@ bool aligned_to(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p)
 // ahead, so short stages (small tiles or BK = 32) need more of them to cover
 // HBM latency.
 enum class LdsCfg { T256x256x64s2, T256x256x32s4, T256x128x64s3, T128x256x64s3, T128x128x64s4, T128x128x32s4,
-                    T128x128x64s2 };
+                    T128x128x64s2, T256x256x64s2w8, T256x256x32s4w8, T256x128x64s3w8 };
 
-template <int BM_, int BN_, int BK_, int S_>
+template <int BM_, int BN_, int BK_, int S_, int WGM_ = 2, int WGN_ = 2>
 struct CfgTag {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, S = S_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, S = S_, WGM = WGM_, WGN = WGN_;
 };
 
-LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch) {
+LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch, int act) {
   // Diagnostic override for tuning sweeps: BG_GEMM_TILE=BMxBNxBKsS.
   if (const char* e = std::getenv("BG_GEMM_TILE")) {
     const std::string v(e);
@@ -785,15 +794,30 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch) {
     if (v == "128x128x64s4") return LdsCfg::T128x128x64s4;
     if (v == "128x128x32s4") return LdsCfg::T128x128x32s4;
     if (v == "128x128x64s2") return LdsCfg::T128x128x64s2;
+    if (v == "256x256x64s2w8") return LdsCfg::T256x256x64s2w8;
+    if (v == "256x256x32s4w8") return LdsCfg::T256x256x32s4w8;
+    if (v == "256x128x64s3w8") return LdsCfg::T256x128x64s3w8;
   }
-  // Measured on MI355X (wall clock, 50 back-to-back launches): 256x256 tiles
-  // win only for deep-K problems with at least one tile per CU (4096^3:
-  // 146 vs 159 us); for the GPT-2 shapes (M = 8192, N in {768, 2304, 3072},
-  // K in {768, 3072}) 128x128 tiles with two stages -- two workgroups per CU
-  // -- are fastest (e.g. 8192x2304x768: 43.8 vs 57.5 us); deeper pipelines
-  // (3-4 stages, BK 32) measured slower at every shape.
+  // Measured on MI355X (wall clock, 50 back-to-back launches per shape):
+  //   4096^3:          256x256x32/4 stages, 8 wavefronts  135.0 us
+  //                    (256x256x64/2, 4 wavefronts 148.5; 128x128x64/2 160.0)
+  //   8192x3072x768:   256x256x64/2, 8 wavefronts         51.9 us (128x128: 54.0)
+  //   8192x2304x768:   128x128x64/2                        44.5 us (256x256 w8: 45.7)
+  //   8192x768x768:    256x128x64/3, 8 wavefronts         16.7 us (128x128: 17.6)
+  //   8192x768x3072:   256x128x64/3, 8 wavefronts         49.4 us (128x128: 50.0)
+  // Deep K with a full wave of 256x256 tiles takes the deepest pipeline;
+  // 1.25+ waves of 256x256 tiles take them with two wavefronts per SIMD;
+  // narrow outputs (N <= 1024) take 256x128; the rest 128x128, two
+  // workgroups per CU.
+  // With tanh-GELU in the epilogue (two exponentials and a divide per
+  // element) 128x128 tiles win: 8192x3072x768 + bias + GELU 75.1 us vs
+  // 91.0 us for 256x256 w8, whose 1.5 waves of tiles expose the epilogue.
   const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
-  return (t256 >= 256 && k >= 2048) ? LdsCfg::T256x256x64s2 : LdsCfg::T128x128x64s2;
+  if (t256 >= 256 && k >= 2048 && act != BG_ACT_GELU_TANH) return LdsCfg::T256x256x32s4w8;
+  if (t256 >= 320 && act != BG_ACT_GELU_TANH) return LdsCfg::T256x256x64s2w8;
+  const int64_t t256x128 = ((m + 255) / 256) * ((n + 127) / 128) * batch;
+  if (n <= 1024 && t256x128 >= 128) return LdsCfg::T256x128x64s3w8;
+  return LdsCfg::T128x128x64s2;
 }
 
 }  // namespace
@@ -813,7 +837,7 @@ static bool gelu_in_epilogue(const bg_matmul_desc& d, const Record& a, const Rec
   const int64_t a_span = ((d.m - 1) * d.lda + d.k) * es;
   const int64_t b_span = ((d.n - 1) * d.ldb + d.k) * es;
   if (!vec || a_span >= (int64_t(1) << 31) || b_span >= (int64_t(1) << 31)) return false;
-  const LdsCfg c = choose_lds_cfg(d.m, d.n, d.k, d.batch);
+  const LdsCfg c = choose_lds_cfg(d.m, d.n, d.k, d.batch, d.act);
   return c != LdsCfg::T256x256x64s2 && c != LdsCfg::T256x256x32s4;
 }
 
@@ -912,13 +936,13 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
   const bool lds_ok = vec && a_span < (int64_t(1) << 31) && b_span < (int64_t(1) << 31);
   if (lds_ok) {
     const uint32_t ab = uint32_t(a_span), bb = uint32_t(b_span);
-    const LdsCfg cfg = choose_lds_cfg(d.m, d.n, d.k, d.batch);
+    const LdsCfg cfg = choose_lds_cfg(d.m, d.n, d.k, d.batch, act);
     auto go = [&](auto tag) {
       using T = decltype(tag);
       P.tiles_m = int((d.m + T::BM - 1) / T::BM);
       P.tiles_n = int((d.n + T::BN - 1) / T::BN);
-      if (bf) launch16_lds<T::BM, T::BN, T::BK, T::S, true>(ctx, P, d.batch, ab, bb);
-      else launch16_lds<T::BM, T::BN, T::BK, T::S, false>(ctx, P, d.batch, ab, bb);
+      if (bf) launch16_lds<T::BM, T::BN, T::BK, T::S, true, T::WGM, T::WGN>(ctx, P, d.batch, ab, bb);
+      else launch16_lds<T::BM, T::BN, T::BK, T::S, false, T::WGM, T::WGN>(ctx, P, d.batch, ab, bb);
     };
     switch (cfg) {
       case LdsCfg::T256x256x64s2: go(CfgTag<256, 256, 64, 2>{}); break;
@@ -927,6 +951,9 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
       case LdsCfg::T128x256x64s3: go(CfgTag<128, 256, 64, 3>{}); break;
       case LdsCfg::T128x128x64s4: go(CfgTag<128, 128, 64, 4>{}); break;
       case LdsCfg::T128x128x32s4: go(CfgTag<128, 128, 32, 4>{}); break;
+      case LdsCfg::T256x256x64s2w8: go(CfgTag<256, 256, 64, 2, 2, 4>{}); break;
+      case LdsCfg::T256x256x32s4w8: go(CfgTag<256, 256, 32, 4, 2, 4>{}); break;
+      case LdsCfg::T256x128x64s3w8: go(CfgTag<256, 128, 64, 3, 4, 2>{}); break;
       default: go(CfgTag<128, 128, 64, 2>{}); break;
     }
     return;

@@ -67,17 +67,24 @@ def log(msg: str) -> None:
 
 def timed(br, step, steps: int, warmup: int, label: str):
     """Run `warmup` untimed steps, then `steps` timed ones bracketed by a
-    stream synchronize on both sides.  Returns (wall ms/step, mean per-launch
-    ms of kernels whose profile label is `label`, launches counted)."""
+    stream synchronize on both sides, with per-dispatch profiling off (no
+    timing events in the stream, as a caller that does not profile runs).
+    Then `steps` more with profiling on, for the per-launch kernel time.
+    Returns (wall ms/step, mean per-launch ms of kernels whose profile label
+    is `label`, launches counted)."""
+    br.set_profiling(False)
     for _ in range(warmup):
         step()
     br.synchronize()
-    n0 = len(br.flushProfiles()["passProfiles"])
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     br.synchronize()
     t1 = time.perf_counter()
+    br.set_profiling(True)
+    n0 = len(br.flushProfiles()["passProfiles"])
+    for _ in range(steps):
+        step()
     profs = br.flushProfiles()["passProfiles"][n0:]
     ks = [p["gpuMs"] for p in profs if p["label"] == label]
     kmean = float(np.mean(ks)) if ks else float("nan")
@@ -281,15 +288,19 @@ def bench_c5(br, steps, warmup):
     def step():
         br.release(walk(g, s.buffers, gbt, materialize=False))
 
+    br.set_profiling(False)
     for _ in range(warmup):
         step()
     br.synchronize()
-    n0 = len(br.flushProfiles()["passProfiles"])
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     br.synchronize()
     t1 = time.perf_counter()
+    br.set_profiling(True)
+    n0 = len(br.flushProfiles()["passProfiles"])
+    for _ in range(steps):
+        step()
     profs = br.flushProfiles()["passProfiles"][n0:]
     by_label = {}
     for p in profs:

@@ -128,6 +128,7 @@ SIGNATURES = {
     "bg_alive_handles": (C.c_int, [ctx_p, P64]),
     "bg_resource_snapshot": (C.c_int, [ctx_p, C.POINTER(Snapshot)]),
     "bg_flush_profiles": (C.c_int, [ctx_p, C.POINTER(PassProfile), C.c_int, C.POINTER(C.c_int)]),
+    "bg_set_profiling": (C.c_int, [ctx_p, C.c_int]),
     "bg_matmul": (C.c_int, [ctx_p, handle_t, handle_t, C.c_int64, C.c_int64, C.c_int64, C.c_int, PH]),
     "bg_fused_elementwise": (C.c_int, [ctx_p, PH, C.c_int, C.POINTER(FusedOp), C.c_int, P64, C.c_int, C.c_int, PH]),
     "bg_cast": (C.c_int, [ctx_p, handle_t, C.c_int, C.c_int, P64, C.c_int, PH]),

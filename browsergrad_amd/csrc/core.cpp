@@ -449,6 +449,12 @@ int bg_flush_profiles(bg_ctx* ctx, bg_pass_profile* out, int cap, int* n_out) {
   BG_API_END
 }
 
+int bg_set_profiling(bg_ctx* ctx, int on) {
+  BG_API_BEGIN
+  ctx->profiling = on != 0;
+  BG_API_END
+}
+
 int bg_device_ptr(bg_ctx* ctx, bg_handle h, void** ptr) {
   BG_API_BEGIN
   Record& r = get(ctx, h, "device_ptr");

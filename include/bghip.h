@@ -248,6 +248,10 @@ int bg_resource_snapshot(bg_ctx* ctx, bg_snapshot* out);
 /* flushProfiles: realizer.ts:1678-1681.  Waits for the stream, resolves all
  * pending event pairs, and copies up to `cap` profiles (oldest first). */
 int bg_flush_profiles(bg_ctx* ctx, bg_pass_profile* out, int cap, int* n_out);
+/* extension: switch per-dispatch profiling on or off between calls.  The
+ * reference fixes it at creation (options.profiling, realizer.ts:899, 914);
+ * profiles already recorded stay pending until bg_flush_profiles. */
+int bg_set_profiling(bg_ctx* ctx, int on);
 
 /* ---- compute ------------------------------------------------------------ */
 /* matmul: realizer.ts:1043-1060.  A[M,K] @ B[K,N] row-major; dtype is

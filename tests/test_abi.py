@@ -77,3 +77,44 @@ def test_fused_codegen_compiles_every_opcode(lib):
     buf = C.create_string_buffer(4096)
     failures = lib.bg_fused_codegen_selftest(buf, 4096)
     assert failures == 0, buf.value.decode()
+
+
+def test_fused_ex_descriptor_cache_passes_each_calls_handles():
+    """HipRealizerBridge.fused_ex reuses one ctypes descriptor per program
+    structure; every call must still pass its own input handles, and a change
+    of structure (ops, shape, immediates, reduction) must get its own
+    descriptor.  Checked on the CPU against a stand-in for the library that
+    records what bg_fused_ex receives (no GPU call)."""
+    import numpy as np  # noqa: F401
+
+    from browsergrad_amd.bridge import HipRealizerBridge
+
+    seen = []
+
+    class RecordingLib:
+        def bg_fused_ex(self, ctx, dptr, out):
+            d = C.cast(dptr, C.POINTER(N.FusedDesc)).contents
+            seen.append({
+                "inputs": [int(d.inputs[i]) for i in range(d.n_inputs)],
+                "ops": [(d.ops[i].code, d.ops[i].a, d.ops[i].b) for i in range(d.n_ops)],
+                "shape": [int(d.shape[i]) for i in range(d.rank)],
+                "imms": [float(d.imms[i]) for i in range(d.n_imms)],
+                "reduce": int(d.reduce_op),
+            })
+            C.cast(out, C.POINTER(N.handle_t)).contents.value = 100 + len(seen)
+            return N.BG_OK
+
+    br = HipRealizerBridge.__new__(HipRealizerBridge)
+    br._lib = RecordingLib()
+    br._ctx = None
+    br._fused_descs = {}
+    ops = [("MUL", -1, -2, 0), ("ADD", 0, -3, 0)]
+    assert br.fused_ex([1, 2, 3], ops, (4, 8), "float32") == 101
+    assert br.fused_ex([7, 8, 9], ops, (4, 8), "float32") == 102
+    assert br.fused_ex([7, 8, 9], ops, (4, 8), "float32", imms=[2.5], reduce=1) == 103
+    assert br.fused_ex([4, 5], [("ADD", -1, -2, 0)], (16,), "float32") == 104
+    assert [s["inputs"] for s in seen] == [[1, 2, 3], [7, 8, 9], [7, 8, 9], [4, 5]]
+    assert seen[0]["ops"] == seen[1]["ops"] == [(N.OPS["MUL"], -1, -2), (N.OPS["ADD"], 0, -3)]
+    assert seen[2]["imms"] == [2.5] and seen[2]["reduce"] == 1 and seen[1]["reduce"] == 0
+    assert seen[3]["shape"] == [16] and seen[3]["ops"] == [(N.OPS["ADD"], -1, -2)]
+    assert len(br._fused_descs) == 3

@@ -292,6 +292,22 @@ def test_attention_rectangular_noncausal(bridge, rng):
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
 
 
+@pytest.mark.parametrize("sq,sk", [(300, 100), (100, 300), (600, 130), (257, 257), (64, 2048)])
+def test_attention_rectangular_causal(bridge, rng, sq, sk):
+    """Causal with Sq != Sk: the reference mask triu(ones(Sq, Sk), k=1) is
+    top-left aligned (key j visible to query i iff j <= i), so queries past Sk
+    see every key.  (600, 130) puts whole query blocks past the last key."""
+    b, h, d = 1, 2, 64
+    q = rng.standard_normal((b, h, sq, d)).astype(np.float16)
+    k = rng.standard_normal((b, h, sk, d)).astype(np.float16)
+    v = rng.standard_normal((b, h, sk, d)).astype(np.float16)
+    ho = bridge.attention_ex(up(bridge, q), up(bridge, k), up(bridge, v), batch=b, heads=h, sq=sq, sk=sk, d=d,
+                             scale=0.125, causal=True, in_dtype="float16", round_scores=True)
+    y = bridge.to_numpy(ho).astype(np.float32)
+    ref = O.sdpa_amp(q, k, v, 0.125, True).astype(np.float32)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
 def test_attention_strided_fused_qkv_views(bridge, rng):
     """Q/K/V as views into one fused QKV projection [B, S, 3, H, D] (the GPT-2
     block layout): head-split without a copy, output [B, S, H, D]."""

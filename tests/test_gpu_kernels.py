@@ -308,6 +308,38 @@ def test_attention_rectangular_causal(bridge, rng, sq, sk):
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_attention_late_dominant_key(bridge, rng, causal, dtype):
+    """Head 0 holds a key (index 100) whose score beats every key of the first
+    32 by far more than 16 (log2 units): a reference max taken from the first
+    keys must move, or P overflows the 16-bit range.  Head 1 is ordinary
+    random data in the same launch, so blocks that need no recompute must be
+    left as they are."""
+    b, h, s, d = 1, 2, 300, 64
+    q = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    k = (0.25 * rng.standard_normal((b, h, s, d))).astype(np.float32)
+    v = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    u = np.ones(d, np.float32) / 2.0
+    q[0, 0] += 4.0 * u   # every query of head 0 leans towards u
+    k[0, 0, 100] = 4.0 * u  # q.k ~ 256 for key 100: 46 log2 units above the rest
+    scale = 0.125
+    if dtype == "float16":
+        q16, k16, v16 = (t.astype(np.float16) for t in (q, k, v))
+        hq, hk, hv = up(bridge, q16), up(bridge, k16), up(bridge, v16)
+        ref = O.sdpa_amp(q16, k16, v16, scale, causal).astype(np.float32)
+    else:
+        q16, k16, v16 = (O.f32_to_bf16_bits(t) for t in (q, k, v))
+        hq, hk, hv = (up(bridge, t, "bfloat16") for t in (q16, k16, v16))
+        ref = O.bf16_bits_to_f32(O.sdpa_bf16(q16, k16, v16, scale, causal))
+    ho = bridge.attention_ex(hq, hk, hv, batch=b, heads=h, sq=s, sk=s, d=d, scale=scale, causal=causal,
+                             in_dtype=dtype, round_scores=True)
+    y = bridge.to_numpy(ho)
+    y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
+    assert np.isfinite(y).all()
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
 def test_attention_strided_fused_qkv_views(bridge, rng):
     """Q/K/V as views into one fused QKV projection [B, S, 3, H, D] (the GPT-2
     block layout): head-split without a copy, output [B, S, H, D]."""

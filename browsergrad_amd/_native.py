@@ -104,6 +104,19 @@ class Snapshot(C.Structure):
     ]
 
 
+class OptimArgs(C.Structure):
+    """bg_optim_args: the scalar arguments of one optimizer update."""
+    _fields_ = [("lr", C.c_double), ("beta1", C.c_double), ("beta2", C.c_double), ("eps", C.c_double),
+                ("weight_decay", C.c_double), ("step", C.c_int64)]
+
+
+# bg_optimizer_update kinds (BG_OPT_*), keyed by the reference's plan op names.
+OPTIM_KINDS = {
+    "SGD_UPDATE": 0, "ADAMW_UPDATE_M": 1, "ADAMW_UPDATE_V": 2, "ADAMW_UPDATE_PARAM": 3,
+    "ADAM_UPDATE_M": 4, "ADAM_UPDATE_V": 5, "ADAM_UPDATE_PARAM": 6,
+}
+
+
 class PassProfile(C.Structure):
     _fields_ = [("label", C.c_char * 48), ("gpu_ms", C.c_double), ("bytes", C.c_int64), ("flops", C.c_int64)]
 
@@ -138,6 +151,12 @@ SIGNATURES = {
     "bg_fused_ex": (C.c_int, [ctx_p, C.POINTER(FusedDesc), PH]),
     "bg_attention_ex": (C.c_int, [ctx_p, C.POINTER(AttentionDesc), PH]),
     "bg_layer_norm": (C.c_int, [ctx_p, handle_t, handle_t, handle_t, C.c_int64, C.c_int64, C.c_float, C.c_int, PH]),
+    "bg_layer_norm_backward_input": (C.c_int, [ctx_p, handle_t, handle_t, handle_t, C.c_int64, C.c_int64,
+                                               C.c_float, PH]),
+    "bg_layer_norm_backward_weight": (C.c_int, [ctx_p, handle_t, handle_t, C.c_int64, C.c_int64, C.c_float, PH]),
+    "bg_layer_norm_backward_bias": (C.c_int, [ctx_p, handle_t, C.c_int64, C.c_int64, PH]),
+    "bg_optimizer_update": (C.c_int, [ctx_p, C.c_int, C.POINTER(handle_t), C.c_int, C.POINTER(OptimArgs),
+                                      C.c_int64, PH]),
     "bg_copy_strided": (C.c_int, [ctx_p, handle_t, C.c_int64, P64, P64, C.c_int, PH]),
     "bg_reshape": (C.c_int, [ctx_p, handle_t, P64, C.c_int, PH]),
     "bg_reduce_last": (C.c_int, [ctx_p, handle_t, C.c_int64, C.c_int64, C.c_int, C.c_int, PH]),

@@ -298,6 +298,46 @@ class HipRealizerBridge:
                                             float(eps), _dtype_code(out_dtype, "layer_norm"), C.byref(out)))
         return int(out.value)
 
+    def layer_norm_backward_input(self, dy: int, x: int, weight: int, rows: int, cols: int,
+                                  eps: float = 1e-5) -> int:
+        """dX of LayerNorm (the plan op LAYER_NORM_BACKWARD_INPUT,
+        tensor_plan.ts:2209-2255), f32 [rows, cols]."""
+        out = N.handle_t()
+        self._check(self._lib.bg_layer_norm_backward_input(self._ctx, int(dy), int(x), int(weight), int(rows),
+                                                           int(cols), float(eps), C.byref(out)))
+        return int(out.value)
+
+    def layer_norm_backward_weight(self, dy: int, x: int, rows: int, cols: int, eps: float = 1e-5) -> int:
+        """dW of LayerNorm (LAYER_NORM_BACKWARD_WEIGHT, tensor_plan.ts:2257-2295), f32 [cols]."""
+        out = N.handle_t()
+        self._check(self._lib.bg_layer_norm_backward_weight(self._ctx, int(dy), int(x), int(rows), int(cols),
+                                                            float(eps), C.byref(out)))
+        return int(out.value)
+
+    def layer_norm_backward_bias(self, dy: int, rows: int, cols: int) -> int:
+        """dB of LayerNorm (LAYER_NORM_BACKWARD_BIAS, tensor_plan.ts:2297-2321), f32 [cols]."""
+        out = N.handle_t()
+        self._check(self._lib.bg_layer_norm_backward_bias(self._ctx, int(dy), int(rows), int(cols),
+                                                          C.byref(out)))
+        return int(out.value)
+
+    def optimizer_update(self, op: str, inputs: Sequence[int], n: int, *, lr: float = 0.0,
+                         beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8,
+                         weight_decay: float = 0.0, step: int = 1) -> int:
+        """One optimizer step over n f32 elements; `op` is the reference's plan
+        op name (SGD_UPDATE, ADAMW_UPDATE_{M,V,PARAM}, ADAM_UPDATE_{M,V,PARAM};
+        tensor_plan.ts:2000-2168) and `inputs` its input handles in the
+        plan's order."""
+        kind = N.OPTIM_KINDS.get(op)
+        if kind is None:
+            raise ValueError(f"optimizer_update: unknown op {op!r}")
+        hs = (N.handle_t * max(len(inputs), 1))(*[int(h) for h in inputs])
+        args = N.OptimArgs(float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(step))
+        out = N.handle_t()
+        self._check(self._lib.bg_optimizer_update(self._ctx, kind, hs, len(inputs), C.byref(args), int(n),
+                                                  C.byref(out)))
+        return int(out.value)
+
     def copy_strided(self, src: int, offset: int, shape: Sequence[int], strides: Sequence[int]) -> int:
         shp = _shape(shape)
         out = N.handle_t()

@@ -8,6 +8,7 @@
 #include "core.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <sstream>
@@ -653,6 +654,109 @@ int bg_layer_norm(bg_ctx* ctx, bg_handle x, bg_handle weight, bg_handle bias,
     launch_layer_norm(ctx, rx2.ptr(), rx2.dtype, reinterpret_cast<float*>(rw2.ptr()),
                       reinterpret_cast<float*>(rb2.ptr()), ro.ptr(), out_dtype, rows,
                       cols, eps);
+  }
+  *out = o;
+  BG_API_END
+}
+
+// Shared checks of the LayerNorm backward entry points: an f32 handle of
+// exactly `want` elements.
+static Record& ln_bwd_operand(bg_ctx* ctx, bg_handle h, int64_t want, const char* what) {
+  Record& r = get(ctx, h, what);
+  if (r.dtype != BG_F32) fail(BG_E_DTYPE, std::string(what) + " must be float32");
+  if (r.numel() != want) fail(BG_E_SHAPE, std::string(what) + " does not hold rows*cols (or cols) elements");
+  return r;
+}
+
+static void ln_bwd_dims(int64_t rows, int64_t cols, float eps, const char* op) {
+  if (rows <= 0 || cols <= 0) fail(BG_E_INVALID, std::string(op) + ": rows and cols must be positive");
+  if (!(eps > 0.f) || !std::isfinite(eps)) fail(BG_E_INVALID, std::string(op) + ": eps must be finite and > 0");
+}
+
+int bg_layer_norm_backward_input(bg_ctx* ctx, bg_handle dy, bg_handle x, bg_handle weight, int64_t rows,
+                                 int64_t cols, float eps, bg_handle* out) {
+  BG_API_BEGIN
+  ln_bwd_dims(rows, cols, eps, "layer_norm_backward_input");
+  ln_bwd_operand(ctx, dy, rows * cols, "layer_norm_backward_input[dy]");
+  const std::vector<int64_t> shape = ln_bwd_operand(ctx, x, rows * cols, "layer_norm_backward_input[x]").shape;
+  ln_bwd_operand(ctx, weight, cols, "layer_norm_backward_input[weight]");
+  bg_handle o = mint(ctx, size_t(rows * cols * 4), shape, BG_F32);
+  const float* pdy = reinterpret_cast<const float*>(ctx->handles[dy].ptr());
+  const float* px = reinterpret_cast<const float*>(ctx->handles[x].ptr());
+  const float* pw = reinterpret_cast<const float*>(ctx->handles[weight].ptr());
+  float* po = reinterpret_cast<float*>(ctx->handles[o].ptr());
+  {
+    Profile prof(ctx, "layer_norm_backward_input", rows * cols * 12 + cols * 4, 0);
+    launch_ln_backward_input(ctx, pdy, px, pw, po, rows, cols, eps);
+  }
+  *out = o;
+  BG_API_END
+}
+
+int bg_layer_norm_backward_weight(bg_ctx* ctx, bg_handle dy, bg_handle x, int64_t rows, int64_t cols, float eps,
+                                  bg_handle* out) {
+  BG_API_BEGIN
+  ln_bwd_dims(rows, cols, eps, "layer_norm_backward_weight");
+  ln_bwd_operand(ctx, dy, rows * cols, "layer_norm_backward_weight[dy]");
+  ln_bwd_operand(ctx, x, rows * cols, "layer_norm_backward_weight[x]");
+  bg_handle o = mint(ctx, size_t(cols * 4), {cols}, BG_F32);
+  const float* pdy = reinterpret_cast<const float*>(ctx->handles[dy].ptr());
+  const float* px = reinterpret_cast<const float*>(ctx->handles[x].ptr());
+  float* po = reinterpret_cast<float*>(ctx->handles[o].ptr());
+  {
+    Profile prof(ctx, "layer_norm_backward_weight", rows * cols * 8 + cols * 4, 0);
+    launch_ln_backward_cols(ctx, pdy, px, po, rows, cols, eps, true);
+  }
+  *out = o;
+  BG_API_END
+}
+
+int bg_layer_norm_backward_bias(bg_ctx* ctx, bg_handle dy, int64_t rows, int64_t cols, bg_handle* out) {
+  BG_API_BEGIN
+  ln_bwd_dims(rows, cols, 1.f, "layer_norm_backward_bias");
+  ln_bwd_operand(ctx, dy, rows * cols, "layer_norm_backward_bias[dy]");
+  bg_handle o = mint(ctx, size_t(cols * 4), {cols}, BG_F32);
+  const float* pdy = reinterpret_cast<const float*>(ctx->handles[dy].ptr());
+  float* po = reinterpret_cast<float*>(ctx->handles[o].ptr());
+  {
+    Profile prof(ctx, "layer_norm_backward_bias", rows * cols * 4 + cols * 4, 0);
+    launch_ln_backward_cols(ctx, pdy, nullptr, po, rows, cols, 0.f, false);
+  }
+  *out = o;
+  BG_API_END
+}
+
+int bg_optimizer_update(bg_ctx* ctx, int kind, const bg_handle* inputs, int n_inputs, const bg_optim_args* args,
+                        int64_t n, bg_handle* out) {
+  BG_API_BEGIN
+  static const int arity[] = {2, 2, 2, 4, 3, 3, 3};
+  static const char* names[] = {"sgd_update",    "adamw_update_m", "adamw_update_v", "adamw_update_param",
+                                "adam_update_m", "adam_update_v",  "adam_update_param"};
+  if (kind < BG_OPT_SGD || kind > BG_OPT_ADAM_PARAM) fail(BG_E_INVALID, "optimizer_update: unknown kind");
+  const std::string op = names[kind];
+  if (!args || !out) fail(BG_E_INVALID, op + ": args and out must be non-NULL");
+  if (n_inputs != arity[kind] || !inputs)
+    fail(BG_E_INVALID, op + ": expects " + std::to_string(arity[kind]) + " inputs");
+  if (n < 0) fail(BG_E_INVALID, op + ": n must be >= 0");
+  const bg_optim_args& a = *args;
+  for (double v : {a.lr, a.beta1, a.beta2, a.eps, a.weight_decay})
+    if (!std::isfinite(v)) fail(BG_E_INVALID, op + ": arguments must be finite");
+  if (a.lr < 0) fail(BG_E_INVALID, op + ": lr must be >= 0");
+  if (kind != BG_OPT_SGD && a.step < 1) fail(BG_E_INVALID, op + ": step must be >= 1");
+  std::vector<int64_t> shape;
+  for (int i = 0; i < n_inputs; ++i) {
+    Record& r = get(ctx, inputs[i], op.c_str());
+    if (r.dtype != BG_F32) fail(BG_E_DTYPE, op + ": inputs must be float32");
+    if (r.numel() != n) fail(BG_E_SHAPE, op + ": input " + std::to_string(i) + " does not hold n elements");
+    if (i == 0) shape = r.shape;
+  }
+  bg_handle o = mint(ctx, size_t(n * 4), shape, BG_F32);
+  const float* in[4] = {nullptr, nullptr, nullptr, nullptr};
+  for (int i = 0; i < n_inputs; ++i) in[i] = reinterpret_cast<const float*>(ctx->handles[inputs[i]].ptr());
+  float* po = reinterpret_cast<float*>(ctx->handles[o].ptr());
+  {
+    Profile prof(ctx, names[kind], n * 4 * (n_inputs + 1), 0);
+    launch_optimizer(ctx, kind, a, in, po, n);
   }
   *out = o;
   BG_API_END

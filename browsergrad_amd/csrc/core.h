@@ -160,6 +160,14 @@ void launch_copy_strided(bg_ctx* ctx, const void* src, int64_t elem_size,
 void launch_layer_norm(bg_ctx* ctx, const void* x, int x_dtype,
                        const float* w, const float* b, void* y, int y_dtype,
                        int64_t rows, int64_t cols, float eps);
+void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, const float* w, float* dx,
+                              int64_t rows, int64_t cols, float eps);
+// Column sums over rows of dy * x_hat (weight) or dy (bias, x unused).
+void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float* out, int64_t rows, int64_t cols,
+                             float eps, bool weight);
+// in[] holds the kind's inputs in bg_optimizer_update order (unused slots NULL).
+void launch_optimizer(bg_ctx* ctx, int kind, const bg_optim_args& a, const float* const (&in)[4], float* out,
+                      int64_t n);
 void launch_reduce_last(bg_ctx* ctx, const void* x, int dtype, void* y,
                         int64_t rows, int64_t cols, int op);
 void launch_softmax_last(bg_ctx* ctx, const void* x, int x_dtype, void* y, int y_dtype,

@@ -28,12 +28,15 @@
 //   ADD/MUL/DIV with broadcastable (not only equal-numel) inputs
 //   MATMUL rank > 2  -> batched GEMM (bg_matmul_ex), numpy batch broadcasting
 //   CAST between f32 / f16 / bf16 / bool
-// CONV*, LAYER_NORM_BACKWARD_* and the optimizer updates are refused with
+// LAYER_NORM_BACKWARD_{INPUT,WEIGHT,BIAS}, SGD_UPDATE, ADAMW_UPDATE_{M,V,PARAM}
+// and ADAM_UPDATE_{M,V,PARAM} lower onto bg_layer_norm_backward_* and
+// bg_optimizer_update (f32 only, as in the reference).  CONV* is refused with
 // BG_E_UNSUPPORTED naming the op.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <set>
 #include <string>
 #include <unordered_map>
@@ -480,6 +483,114 @@ std::unordered_map<int64_t, std::vector<int64_t>> bind_requests(const Plan& p, c
   return axes;
 }
 
+// ---- argument rules of the LayerNorm and optimizer steps ----------------------
+
+// expectShape (tensor_plan.ts:3215-3226).
+void expect_shape(const std::vector<int64_t>& actual, const std::vector<int64_t>& expected,
+                  const std::string& name) {
+  auto str = [](const std::vector<int64_t>& v) {
+    std::string r = "[";
+    for (size_t i = 0; i < v.size(); ++i) r += (i ? "," : "") + std::to_string(v[i]);
+    return r + "]";
+  };
+  if (actual.size() != expected.size())
+    fail(BG_E_SHAPE, name + " expected rank " + std::to_string(expected.size()) + ", got " + str(actual));
+  for (size_t i = 0; i < expected.size(); ++i)
+    if (actual[i] != expected[i])
+      fail(BG_E_SHAPE, name + " shape mismatch at dim " + std::to_string(i) + ": expected " +
+                           std::to_string(expected[i]) + ", got " + std::to_string(actual[i]));
+}
+
+// The first of `keys` present and not null, else nullptr (JavaScript's `??`
+// chain over snake_case then camelCase spellings).
+const JVal* first_of(const JVal& arg, std::initializer_list<const char*> keys) {
+  for (const char* k : keys)
+    if (const JVal* v = arg.get(k); v && v->kind != JVal::Null) return v;
+  return nullptr;
+}
+
+// expectFiniteNumber with a default for an absent field (tensor_plan.ts:3948-3953).
+double finite_or(const JVal* v, double dflt, bool required, const std::string& name) {
+  if (!v) {
+    if (required) fail(BG_E_INVALID, name + " must be a finite number");
+    return dflt;
+  }
+  if (v->kind != JVal::Num || !std::isfinite(v->num)) fail(BG_E_INVALID, name + " must be a finite number");
+  return v->num;
+}
+
+const JVal& arg_object(const JVal* arg, const std::string& op) {
+  if (!arg || arg->kind != JVal::Obj) plan_fail(op + ".arg must be an object");
+  return *arg;
+}
+
+struct LnArg {
+  std::vector<int64_t> normalized_shape;
+  int64_t rows = 0, cols = 0;
+  float eps = 1e-5f;
+};
+
+// expectLayerNormArg (tensor_plan.ts:3829-3852).
+LnArg ln_arg(const Step& s) {
+  const JVal& arg = arg_object(s.arg, s.op);
+  LnArg a;
+  const JVal* ns = first_of(arg, {"normalized_shape", "normalizedShape"});
+  if (!ns || ns->kind != JVal::Arr) fail(BG_E_INVALID, s.op + ".normalized_shape must be an array");
+  for (size_t i = 0; i < ns->arr.size(); ++i)
+    a.normalized_shape.push_back(expect_int(&ns->arr[i], s.op + ".normalized_shape[" + std::to_string(i) + "]"));
+  a.rows = expect_int(arg.get("rows"), s.op + ".rows");
+  a.cols = expect_int(arg.get("cols"), s.op + ".cols");
+  const double eps = finite_or(first_of(arg, {"eps"}), 1e-5, false, s.op + ".eps");
+  if (a.normalized_shape.empty()) plan_fail(s.op + ".normalized_shape must be non-empty");
+  if (a.rows <= 0 || a.cols <= 0) plan_fail(s.op + ".rows and cols must be positive");
+  if (numel(a.normalized_shape) != a.cols) plan_fail(s.op + ".cols must equal normalized_shape numel");
+  if (eps <= 0) plan_fail(s.op + ".eps must be > 0");
+  a.eps = float(eps);
+  return a;
+}
+
+int optim_kind(const std::string& op) {
+  static const char* names[7] = {"SGD_UPDATE",    "ADAMW_UPDATE_M", "ADAMW_UPDATE_V", "ADAMW_UPDATE_PARAM",
+                                 "ADAM_UPDATE_M", "ADAM_UPDATE_V",  "ADAM_UPDATE_PARAM"};
+  for (int k = 0; k < 7; ++k)
+    if (op == names[k]) return k;
+  return -1;
+}
+
+// expectSgdUpdateArg / expectAdamwUpdateArg / expectAdamUpdateArg
+// (tensor_plan.ts:3776-3827): SGD needs lr; AdamW needs beta1, beta2 and
+// step (lr 0.001, eps 1e-8 by default); Adam defaults every field (lr 0.001,
+// betas 0.9 / 0.999, eps 1e-8, step 1); weight_decay defaults to 0.
+bg_optim_args optim_arg(const Step& s, int kind) {
+  const JVal& arg = arg_object(s.arg, s.op);
+  const std::string& op = s.op;
+  bg_optim_args a{};
+  const double wd = finite_or(first_of(arg, {"weight_decay", "weightDecay"}), 0.0, false, op + ".weight_decay");
+  if (kind == BG_OPT_SGD) {
+    a.lr = finite_or(first_of(arg, {"lr"}), 0, true, "SGD_UPDATE.lr");
+    a.weight_decay = wd;
+    if (a.lr < 0) plan_fail("SGD_UPDATE.lr must be >= 0");
+    a.beta1 = a.beta2 = a.eps = 0;
+    a.step = 1;
+    return a;
+  }
+  const bool adamw = kind <= BG_OPT_ADAMW_PARAM;
+  a.lr = finite_or(first_of(arg, {"lr"}), 0.001, false, op + ".lr");
+  a.beta1 = finite_or(first_of(arg, {"beta1"}), 0.9, adamw, op + ".beta1");
+  a.beta2 = finite_or(first_of(arg, {"beta2"}), 0.999, adamw, op + ".beta2");
+  a.eps = finite_or(first_of(arg, {"eps"}), 1e-8, false, op + ".eps");
+  a.weight_decay = wd;
+  const JVal* st = first_of(arg, {"step"});
+  if (!st && !adamw) {
+    a.step = 1;
+  } else {
+    a.step = expect_int(st, op + ".step");
+  }
+  if (a.lr < 0) plan_fail(op + ".lr must be >= 0");
+  if (a.step <= 0) plan_fail(op + ".step must be >= 1");
+  return a;
+}
+
 // ---- execution -------------------------------------------------------------
 
 struct Runner {
@@ -722,18 +833,54 @@ struct Runner {
       return own(out);
     }
     if (op == "LAYER_NORM") {
-      if (!s.arg || s.arg->kind != JVal::Obj) plan_fail("LAYER_NORM.arg must be an object");
-      const int64_t rows = expect_int(s.arg->get("rows"), "LAYER_NORM.rows");
-      const int64_t cols = expect_int(s.arg->get("cols"), "LAYER_NORM.cols");
-      double eps = 1e-5;
-      if (const JVal* e = s.arg->get("eps"); e && e->kind != JVal::Null) {
-        if (e->kind != JVal::Num || !std::isfinite(e->num)) plan_fail("LAYER_NORM.eps must be finite");
-        eps = e->num;
-      }
-      if (rows <= 0 || cols <= 0) plan_fail("LAYER_NORM.rows and cols must be positive");
-      if (eps <= 0) plan_fail("LAYER_NORM.eps must be > 0");
+      const LnArg a = ln_arg(s);
+      expect_shape(rec(need(s, 0)).shape, s.shape, op + ".input");
+      expect_shape(rec(need(s, 1)).shape, a.normalized_shape, op + ".weight");
+      expect_shape(rec(need(s, 2)).shape, a.normalized_shape, op + ".bias");
       bg_handle out = 0;
-      call(bg_layer_norm(ctx, need(s, 0), need(s, 1), need(s, 2), rows, cols, float(eps), dt, &out));
+      call(bg_layer_norm(ctx, need(s, 0), need(s, 1), need(s, 2), a.rows, a.cols, a.eps, dt, &out));
+      ctx->handles[out].shape = s.shape;
+      return own(out);
+    }
+    if (op == "LAYER_NORM_BACKWARD_INPUT" || op == "LAYER_NORM_BACKWARD_WEIGHT" ||
+        op == "LAYER_NORM_BACKWARD_BIAS") {
+      // tensor_plan.ts:648-662 (lowering), :2855-2929 (shape rules)
+      const LnArg a = ln_arg(s);
+      if (dt != BG_F32) fail(BG_E_DTYPE, "tensor plan " + op + " supports float32 only");
+      bg_handle out = 0;
+      if (op == "LAYER_NORM_BACKWARD_INPUT") {
+        expect_shape(rec(need(s, 0)).shape, s.shape, op + ".dy");
+        expect_shape(rec(need(s, 1)).shape, s.shape, op + ".input");
+        expect_shape(rec(need(s, 2)).shape, a.normalized_shape, op + ".weight");
+        call(bg_layer_norm_backward_input(ctx, need(s, 0), need(s, 1), need(s, 2), a.rows, a.cols, a.eps, &out));
+      } else if (op == "LAYER_NORM_BACKWARD_WEIGHT") {
+        expect_shape(rec(need(s, 0)).shape, rec(need(s, 1)).shape, op + ".dy");
+        expect_shape(s.shape, a.normalized_shape, op + ".output");
+        call(bg_layer_norm_backward_weight(ctx, need(s, 0), need(s, 1), a.rows, a.cols, a.eps, &out));
+      } else {
+        expect_shape(s.shape, a.normalized_shape, op + ".output");
+        call(bg_layer_norm_backward_bias(ctx, need(s, 0), a.rows, a.cols, &out));
+      }
+      ctx->handles[out].shape = s.shape;
+      return own(out);
+    }
+    if (const int kind = optim_kind(op); kind >= 0) {
+      // tensor_plan.ts:663-702 (lowering), :2926-3113 (shape rules),
+      // :3776-3827 (arguments)
+      static const char* roles[7][4] = {{"param", "grad"},          {"m", "grad"},
+                                        {"v", "grad"},              {"param", "grad", "m", "v"},
+                                        {"param", "grad", "m"},     {"param", "grad", "v"},
+                                        {"param", "m", "v"}};
+      static const int arity[7] = {2, 2, 2, 4, 3, 3, 3};
+      const bg_optim_args a = optim_arg(s, kind);
+      if (dt != BG_F32) fail(BG_E_DTYPE, "tensor plan " + op + " supports float32 only");
+      bg_handle in[4] = {0, 0, 0, 0};
+      for (int i = 0; i < arity[kind]; ++i) {
+        in[i] = need(s, size_t(i));
+        expect_shape(rec(in[i]).shape, s.shape, op + "." + roles[kind][i]);
+      }
+      bg_handle out = 0;
+      call(bg_optimizer_update(ctx, kind, in, arity[kind], &a, numel(s.shape), &out));
       ctx->handles[out].shape = s.shape;
       return own(out);
     }

@@ -283,6 +283,52 @@ int bg_attention_ex(bg_ctx* ctx, const bg_attention_desc* desc, bg_handle* out);
 int bg_layer_norm(bg_ctx* ctx, bg_handle x, bg_handle weight, bg_handle bias,
                   int64_t rows, int64_t cols, float eps, int out_dtype,
                   bg_handle* out);
+/* LayerNorm backward, f32 throughout (the tensor-plan ops
+ * LAYER_NORM_BACKWARD_INPUT / _WEIGHT / _BIAS, tensor_plan.ts:2209-2321;
+ * oracle _realize.py:1036-1072).  dy, x: [rows, cols]; weight: [cols].
+ * input -> [rows, cols]; weight and bias -> [cols] (sums over rows). */
+int bg_layer_norm_backward_input(bg_ctx* ctx, bg_handle dy, bg_handle x,
+                                 bg_handle weight, int64_t rows, int64_t cols,
+                                 float eps, bg_handle* out);
+int bg_layer_norm_backward_weight(bg_ctx* ctx, bg_handle dy, bg_handle x,
+                                  int64_t rows, int64_t cols, float eps,
+                                  bg_handle* out);
+int bg_layer_norm_backward_bias(bg_ctx* ctx, bg_handle dy, int64_t rows,
+                                int64_t cols, bg_handle* out);
+/* Optimizer updates, f32 elementwise over n elements (the tensor-plan ops
+ * SGD_UPDATE, ADAMW_UPDATE_{M,V,PARAM}, ADAM_UPDATE_{M,V,PARAM},
+ * tensor_plan.ts:2000-2168 with argument rules :648-702; oracle
+ * _realize.py:1637-1721).  Inputs, in the reference's order:
+ *   SGD          param, grad             param - lr*(grad + wd*param)
+ *   ADAMW_M      m, grad                 b1*m + (1-b1)*grad
+ *   ADAMW_V      v, grad                 b2*v + (1-b2)*grad^2
+ *   ADAMW_PARAM  param, grad, m', v'     param - lr*mh/(sqrt(vh)+eps) - lr*wd*param
+ *   ADAM_M       param, grad, m          b1*m + (1-b1)*(grad + wd*param)
+ *   ADAM_V       param, grad, v          b2*v + (1-b2)*(grad + wd*param)^2
+ *   ADAM_PARAM   param, m', v'           param - lr*mh/(sqrt(vh)+eps)
+ * with mh = m'/(1-b1^step), vh = v'/(1-b2^step).  The output is a new
+ * handle of n f32 elements.  (extension: the reference exposes these only
+ * as plan steps; bg_run_tensor_plan lowers them onto this entry point.) */
+enum {
+  BG_OPT_SGD = 0,
+  BG_OPT_ADAMW_M = 1,
+  BG_OPT_ADAMW_V = 2,
+  BG_OPT_ADAMW_PARAM = 3,
+  BG_OPT_ADAM_M = 4,
+  BG_OPT_ADAM_V = 5,
+  BG_OPT_ADAM_PARAM = 6
+};
+typedef struct bg_optim_args {
+  double lr;
+  double beta1;
+  double beta2;
+  double eps;
+  double weight_decay;
+  int64_t step; /* >= 1 for the PARAM kinds */
+} bg_optim_args;
+int bg_optimizer_update(bg_ctx* ctx, int kind, const bg_handle* inputs,
+                        int n_inputs, const bg_optim_args* args, int64_t n,
+                        bg_handle* out);
 /* Strided copy (PERMUTE / SLICE / BROADCAST materialisation,
  * tensor_plan.ts:824-997): out[i0..i{r-1}] = src[offset + sum(i_j*strides[j])]
  * in the dtype of src, shape `shape`. */

@@ -170,6 +170,109 @@ def layer_norm(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float = 1e-5) -
     return out.reshape(x.shape).astype(x.dtype, copy=False)
 
 
+def _ln_rows(x: np.ndarray, cols: int, eps: float):
+    """Row statistics shared by the LayerNorm handlers (_realize.py:1008-1023):
+    f32 mean, centered values, biased variance, 1/sqrt(var + eps), x_hat."""
+    x2 = np.asarray(x, dtype=F32).reshape(-1, cols)
+    mean = x2.mean(axis=1, keepdims=True)
+    centered = x2 - mean
+    var = (centered * centered).mean(axis=1, keepdims=True)
+    inv_std = F32(1.0) / np.sqrt(var + F32(eps))
+    return inv_std, centered * inv_std
+
+
+def layer_norm_backward_input(dy: np.ndarray, x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """LAYER_NORM_BACKWARD_INPUT handler (_realize.py:1036-1050):
+    g = dy*w, dx = (inv_std/n) * ((n*g - sum(g)) - x_hat*sum(g*x_hat)), f32."""
+    cols = x.shape[-1]
+    inv_std, x_hat = _ln_rows(x, cols, eps)
+    g = np.asarray(dy, dtype=F32).reshape(-1, cols) * np.asarray(w, dtype=F32).reshape(1, cols)
+    s_g = g.sum(axis=1, keepdims=True)
+    s_gx = (g * x_hat).sum(axis=1, keepdims=True)
+    n = F32(cols)
+    dx = (inv_std / n) * ((n * g - s_g) - x_hat * s_gx)
+    return dx.reshape(x.shape)
+
+
+def layer_norm_backward_weight(dy: np.ndarray, x: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """LAYER_NORM_BACKWARD_WEIGHT handler (_realize.py:1053-1063): column sums
+    of dy * x_hat, f32 [cols]."""
+    cols = x.shape[-1]
+    _, x_hat = _ln_rows(x, cols, eps)
+    return (np.asarray(dy, dtype=F32).reshape(-1, cols) * x_hat).sum(axis=0)
+
+
+def layer_norm_backward_bias(dy: np.ndarray) -> np.ndarray:
+    """LAYER_NORM_BACKWARD_BIAS handler (_realize.py:1066-1072): column sums of dy."""
+    d = np.asarray(dy, dtype=F32)
+    return d.reshape(-1, d.shape[-1]).sum(axis=0)
+
+
+# ---------------------------------------------------------------------------
+# Optimizer updates (_realize.py:1637-1721).  Each handler mixes Python floats
+# with float32 arrays; NumPy 2 casts a Python float operand to float32 at the
+# operation (NEP 50), while float-with-float subexpressions such as
+# 1 - beta1, lr * weight_decay and 1 - beta1**step are taken in double first.
+# The F32(...) casts below make each of those roundings explicit.
+# ---------------------------------------------------------------------------
+
+
+def sgd_update(param, grad, lr: float, weight_decay: float = 0.0) -> np.ndarray:
+    """SGD_UPDATE (_realize.py:1637-1643): param - lr*(grad + wd*param); the
+    decay term is skipped when wd == 0."""
+    p, g = np.asarray(param, F32), np.asarray(grad, F32)
+    u = g + F32(weight_decay) * p if weight_decay != 0.0 else g
+    return p - F32(lr) * u
+
+
+def adamw_update_m(m, grad, beta1: float) -> np.ndarray:
+    """ADAMW_UPDATE_M (_realize.py:1646-1650): beta1*m + (1-beta1)*grad."""
+    return F32(beta1) * np.asarray(m, F32) + F32(1.0 - beta1) * np.asarray(grad, F32)
+
+
+def adamw_update_v(v, grad, beta2: float) -> np.ndarray:
+    """ADAMW_UPDATE_V (_realize.py:1653-1657): beta2*v + (1-beta2)*grad^2."""
+    g = np.asarray(grad, F32)
+    return F32(beta2) * np.asarray(v, F32) + F32(1.0 - beta2) * (g * g)
+
+
+def adamw_update_param(param, m_new, v_new, lr: float, beta1: float, beta2: float, eps: float,
+                       step: int, weight_decay: float = 0.0) -> np.ndarray:
+    """ADAMW_UPDATE_PARAM (_realize.py:1660-1677): decoupled decay,
+    (param - lr*m_hat/(sqrt(v_hat)+eps)) - (lr*wd)*param with
+    m_hat = m/(1-beta1^step), v_hat = v/(1-beta2^step)."""
+    p = np.asarray(param, F32)
+    m_hat = np.asarray(m_new, F32) / F32(1.0 - beta1 ** int(step))
+    v_hat = np.asarray(v_new, F32) / F32(1.0 - beta2 ** int(step))
+    upd = m_hat / (np.sqrt(v_hat) + F32(eps))
+    return (p - F32(lr) * upd) - F32(lr * weight_decay) * p
+
+
+def _adam_grad(param, grad, weight_decay: float) -> np.ndarray:
+    g = np.asarray(grad, F32)
+    return g + F32(weight_decay) * np.asarray(param, F32) if weight_decay != 0.0 else g
+
+
+def adam_update_m(param, grad, m, beta1: float, weight_decay: float = 0.0) -> np.ndarray:
+    """ADAM_UPDATE_M (_realize.py:1680-1690): L2 decay folded into the
+    gradient, beta1*m + (1-beta1)*(grad + wd*param)."""
+    return F32(beta1) * np.asarray(m, F32) + F32(1.0 - beta1) * _adam_grad(param, grad, weight_decay)
+
+
+def adam_update_v(param, grad, v, beta2: float, weight_decay: float = 0.0) -> np.ndarray:
+    """ADAM_UPDATE_V (_realize.py:1693-1703): beta2*v + (1-beta2)*(grad + wd*param)^2."""
+    ge = _adam_grad(param, grad, weight_decay)
+    return F32(beta2) * np.asarray(v, F32) + F32(1.0 - beta2) * (ge * ge)
+
+
+def adam_update_param(param, m_new, v_new, lr: float, beta1: float, beta2: float, eps: float,
+                      step: int) -> np.ndarray:
+    """ADAM_UPDATE_PARAM (_realize.py:1706-1721): param - lr*(m_hat/(sqrt(v_hat)+eps))."""
+    m_hat = np.asarray(m_new, F32) / F32(1.0 - beta1 ** int(step))
+    v_hat = np.asarray(v_new, F32) / F32(1.0 - beta2 ** int(step))
+    return np.asarray(param, F32) - F32(lr) * (m_hat / (np.sqrt(v_hat) + F32(eps)))
+
+
 GELU_C = F32((2.0 / np.pi) ** 0.5)
 
 

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the HIP realizer on 1 MI355X (the BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,c4,c5 | copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,c4,c5,train | copy]
 
 Prints ONE JSON line.  ``value`` is configs[1] of BASELINE.json -- the fused
 elementwise + row-reduction chain ``relu(a*b+c)*exp(-a*a) -> sum(axis=1)`` on
@@ -11,8 +11,10 @@ kernel launch) over inputs already resident in HBM.  Three input sets are
 rotated so the 256 MB Infinity Cache cannot hold the working set.
 
 ``extra`` carries the other configs of the metric (GEMM and attention
-TFLOP/s with their fraction of the MFMA peak, the MLP latency), each with
-the per-launch kernel time measured by HIP events on the library's stream.
+TFLOP/s with their fraction of the MFMA peak, the MLP latency) and the
+training primitives of the plan route (AdamW update, LayerNorm backward,
+GB/s with their fraction of HBM peak), each with the per-launch kernel time
+measured by HIP events on the library's stream.
 
 ``roofline`` is for the dominant kernel of ``value`` (the fused kernel),
 ``cpu_baseline`` is the NumPy restatement of the reference CPU realizer
@@ -320,6 +322,79 @@ def bench_c5(br, steps, warmup):
             "parity": O.report(out, ref, 2e-2)}
 
 
+# --------------------------------------------------------------------------- training primitives
+
+GPT2_PARAMS = 124_439_808  # GPT-2 small, tied embeddings
+LN_ROWS, LN_COLS = 8192, 768  # the C5 block's LayerNorm (B8 x S1024, E768)
+
+
+def bench_train(br, steps, warmup):
+    """One AdamW step over a GPT-2-small-sized f32 parameter vector (the plan
+    ops ADAMW_UPDATE_M, _V, _PARAM, one launch each) and the three LayerNorm
+    backward ops at the C5 block's shape.  All HBM-bound: algorithmic bytes
+    are 12 B/element for M and V (read state + grad, write state), 20 B for
+    PARAM (read param, grad, m', v', write param), 12 / 8 / 4 B per element
+    of dy for the LayerNorm input / weight / bias gradients."""
+    n = GPT2_PARAMS
+    rng = np.random.default_rng(6)
+    host = {k: rng.standard_normal(n, dtype=np.float32) for k in ("p", "g", "m")}
+    host["v"] = np.abs(rng.standard_normal(n, dtype=np.float32)) * np.float32(1e-2)
+    h = {k: br.upload(a, a.shape, "float32") for k, a in host.items()}
+    kw = dict(lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=10)
+    ops = {
+        "adamw_update_m": ("ADAMW_UPDATE_M", ["m", "g"], 12),
+        "adamw_update_v": ("ADAMW_UPDATE_V", ["v", "g"], 12),
+        "adamw_update_param": ("ADAMW_UPDATE_PARAM", ["p", "g", "m", "v"], 20),
+    }
+    out = {"elements": n}
+    for label, (op, names, bpe) in ops.items():
+        hs = [h[k] for k in names]
+
+        def step():
+            br.release(br.optimizer_update(op, hs, n, **kw))
+
+        wall_ms, k_ms, _ = timed(br, step, steps, warmup, label)
+        gbs = bpe * n / (k_ms * 1e-3) / 1e9
+        out[label] = {"kernel_us": round(k_ms * 1e3, 2), "wall_us": round(wall_ms * 1e3, 2),
+                      "gbs_kernel": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    from oracle import ops as O  # checker only: the first 2^20 elements, bit-exact
+    s = 1 << 20
+    y = br.to_numpy(r := br.optimizer_update("ADAMW_UPDATE_PARAM", [h["p"], h["g"], h["m"], h["v"]], n, **kw))[:s]
+    br.release(r)
+    ref = O.adamw_update_param(host["p"][:s], host["m"][:s], host["v"][:s], kw["lr"], kw["beta1"], kw["beta2"],
+                               kw["eps"], kw["step"], kw["weight_decay"])
+    out["adamw_param_bit_exact"] = bool(np.array_equal(y, ref))
+    for hh in h.values():
+        br.release(hh)
+    del host
+
+    rows, cols = LN_ROWS, LN_COLS
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    dy = rng.standard_normal((rows, cols), dtype=np.float32)
+    w = rng.standard_normal(cols, dtype=np.float32)
+    hx, hdy, hw = (br.upload(a, a.shape, "float32") for a in (x, dy, w))
+    ln = {
+        "layer_norm_backward_input": (lambda: br.layer_norm_backward_input(hdy, hx, hw, rows, cols, 1e-5), 12),
+        "layer_norm_backward_weight": (lambda: br.layer_norm_backward_weight(hdy, hx, rows, cols, 1e-5), 8),
+        "layer_norm_backward_bias": (lambda: br.layer_norm_backward_bias(hdy, rows, cols), 4),
+    }
+    for label, (fn, bpe) in ln.items():
+        def step(fn=fn):
+            br.release(fn())
+
+        wall_ms, k_ms, nk = timed(br, step, steps, warmup, label)
+        gbs = bpe * rows * cols / (k_ms * 1e-3) / 1e9
+        out[label] = {"kernel_us": round(k_ms * 1e3, 2), "wall_us": round(wall_ms * 1e3, 2),
+                      "gbs_kernel": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    r = br.layer_norm_backward_input(hdy, hx, hw, rows, cols, 1e-5)
+    y = br.to_numpy(r)[:256]
+    br.release(r)
+    out["ln_input_parity"] = O.report(y, O.layer_norm_backward_input(dy[:256], x[:256], w, 1e-5), 1e-4)
+    for hh in (hx, hdy, hw):
+        br.release(hh)
+    return out
+
+
 def copy_probe(br, reps=5):
     """A plain copy kernel of known size (256 MiB read + 256 MiB written per
     launch): the calibration point for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -339,7 +414,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--only", default="c1,c2,c3,c4,c5,train")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -373,6 +448,10 @@ def main() -> int:
         log("c5 gpt-2 block B8 S1024 E768 H12 autocast f16 (walker)")
         extra["c5_gpt2_block_fp16"] = bench_c5(br, max(10, a.steps // 5), max(3, a.warmup // 2))
         log(f"  {extra['c5_gpt2_block_fp16']}")
+    if "train" in only:
+        log("training primitives: AdamW over 124M f32 params, LayerNorm backward 8192x768")
+        extra["train_adamw_layernorm_bwd"] = bench_train(br, max(10, a.steps // 5), max(3, a.warmup // 2))
+        log(f"  {extra['train_adamw_layernorm_bwd']}")
     if "c1" in only:
         log("c1 mlp 784-128-10 batch 64 f32")
         extra["c1_mlp_fp32"] = bench_c1(br, a.steps, a.warmup)

@@ -7,13 +7,16 @@
 // All are HBM-bound.  Arithmetic follows the oracle's NumPy order with every
 // operation rounded to f32 (no contraction in this build); the scalar
 // constants arrive already rounded the way NumPy rounds a Python float that
-// meets a float32 array (see bg_optimizer_update).
+// meets a float32 array (launch_optimizer).
 //
-// The reference's WGSL recomputes each row's mean and variance once per
-// column for the weight gradient (O(rows * cols^2)); here the row statistics
-// are computed once (a wavefront per row), the column sums run as coalesced
-// per-column partial sums over row chunks, and a last pass adds the partials
-// in a fixed order, so results do not depend on scheduling.
+// The reference's WGSL for the weight gradient runs one thread per column
+// and recomputes every row's mean and variance in each of them
+// (O(rows * cols^2) loads).  Here, for rows of up to 1024 columns, a block
+// reads 16 whole rows once (a wavefront per row, statistics by shuffles),
+// accumulates each column's sum in registers and writes one partial row;
+// wider rows take a statistics pass and one thread per column over chunks of
+// 16 rows.  A last kernel adds the partial rows with 16 lanes per column and
+// a fixed-order combine, so results do not depend on scheduling.
 #include <algorithm>
 #include <cmath>
 
@@ -179,14 +182,101 @@ __global__ void __launch_bounds__(256) ln_col_partial_kernel(const float* __rest
   part[int64_t(blockIdx.y) * cols + c] = acc;
 }
 
-// out[c] = sum over chunks (in order) of part[chunk][c].
+// Column sums for rows held in registers (cols <= 64 * PER): a block owns
+// 4 * RPW consecutive rows and wavefront w takes RPW of them, w, w+4, ...,
+// issuing the loads of all its rows before any arithmetic (rows past the end
+// are clamped to the last row and not accumulated).  For the weight
+// gradient each wavefront computes its rows' mean and inv_std with shuffles
+// (no separate statistics pass, x read once) and accumulates dy * x_hat per
+// column in registers.  The four wavefronts' sums are added in a fixed order
+// through LDS into part[block][c].
+template <int PER, int RPW, bool WEIGHT>
+__global__ void __launch_bounds__(256) ln_col_rows_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+                                                          float* __restrict__ part, int64_t rows, int64_t cols,
+                                                          float eps) {
+  __shared__ float sm[4][64 * PER];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const float n = float(cols);
+  const int64_t r0 = int64_t(blockIdx.x) * (4 * RPW) + w;
+  float d[RPW][PER];
+  float v[WEIGHT ? RPW : 1][PER];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int64_t base = min(r0 + 4 * i, rows - 1) * cols;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int64_t c = int64_t(j) * 64 + lane;
+      d[i][j] = c < cols ? dy[base + c] : 0.f;
+      if constexpr (WEIGHT) v[i][j] = c < cols ? x[base + c] : 0.f;
+    }
+  }
+  float acc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    if (r0 + 4 * i >= rows) break;  // wave-uniform
+    if constexpr (WEIGHT) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) s += v[i][j];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+      const float mean = s / n;
+      float q = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int64_t c = int64_t(j) * 64 + lane;
+        v[i][j] = v[i][j] - mean;
+        if (c < cols) q += v[i][j] * v[i][j];
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+      const float inv = 1.0f / sqrtf(q / n + eps);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) acc[j] += d[i][j] * (v[i][j] * inv);
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER; ++j) acc[j] += d[i][j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) sm[w][j * 64 + lane] = acc[j];
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < cols; c += 256)
+    part[int64_t(blockIdx.x) * cols + c] = ((sm[0][c] + sm[1][c]) + sm[2][c]) + sm[3][c];
+}
+
+// out[c] = sum over k < chunks of part[k][c], for 16 columns per block: the
+// 16 lanes of a column each sum every 16th partial row, then lane 0 adds
+// the 16 sums in order (deterministic, and parallel along the reduced axis).
 __global__ void __launch_bounds__(256) ln_col_final_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            int64_t chunks, int64_t cols) {
-  const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
+  __shared__ float sm[16][17];
+  const int cl = threadIdx.x & 15;
+  const int kl = threadIdx.x >> 4;
+  const int64_t c = int64_t(blockIdx.x) * 16 + cl;
   float acc = 0.f;
-  for (int64_t k = 0; k < chunks; ++k) acc += part[k * cols + c];
-  out[c] = acc;
+  if (c < cols) {
+    int64_t k = kl;
+    for (; k + 112 < chunks; k += 128) {  // eight independent loads per round
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = part[(k + 16 * u) * cols + c];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += t[u];
+    }
+    for (; k < chunks; k += 16) acc += part[k * cols + c];
+  }
+  sm[kl][cl] = acc;
+  __syncthreads();
+  if (kl == 0 && c < cols) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += sm[i][cl];
+    out[c] = t;
+  }
 }
 
 // ---- optimizer updates -------------------------------------------------------------
@@ -205,64 +295,97 @@ struct OptimConsts {
   int has_wd;    // weight_decay != 0 (the oracle skips the term otherwise)
 };
 
-// One element of each update, in the oracle's operation order.
+constexpr int optim_arity(int kind) {
+  return kind == BG_OPT_ADAMW_PARAM ? 4 : (kind >= BG_OPT_ADAM_M ? 3 : 2);
+}
+
+// One element of each update, in the oracle's operation order; v holds the
+// element of each input in bg_optimizer_update order.
 template <int KIND>
-__device__ __forceinline__ float optim_elem(const OptimConsts& k, const float* const (&in)[4], int64_t i) {
-  if constexpr (KIND == BG_OPT_SGD) {  // in: param, grad
-    const float p = in[0][i];
-    float u = in[1][i];
-    if (k.has_wd) u = u + k.wd * p;
-    return p - k.lr * u;
-  } else if constexpr (KIND == BG_OPT_ADAMW_M) {  // in: m, grad
-    return k.b1 * in[0][i] + k.omb1 * in[1][i];
-  } else if constexpr (KIND == BG_OPT_ADAMW_V) {  // in: v, grad
-    const float gv = in[1][i];
-    return k.b2 * in[0][i] + k.omb2 * (gv * gv);
-  } else if constexpr (KIND == BG_OPT_ADAMW_PARAM) {  // in: param, grad, m_new, v_new
-    const float p = in[0][i];
-    const float mh = in[2][i] / k.c1;
-    const float vh = in[3][i] / k.c2;
+__device__ __forceinline__ float optim_val(const OptimConsts& k, const float (&v)[4]) {
+  if constexpr (KIND == BG_OPT_SGD) {  // param, grad
+    float u = v[1];
+    if (k.has_wd) u = u + k.wd * v[0];
+    return v[0] - k.lr * u;
+  } else if constexpr (KIND == BG_OPT_ADAMW_M) {  // m, grad
+    return k.b1 * v[0] + k.omb1 * v[1];
+  } else if constexpr (KIND == BG_OPT_ADAMW_V) {  // v, grad
+    return k.b2 * v[0] + k.omb2 * (v[1] * v[1]);
+  } else if constexpr (KIND == BG_OPT_ADAMW_PARAM) {  // param, grad, m_new, v_new
+    const float mh = v[2] / k.c1;
+    const float vh = v[3] / k.c2;
     const float u = mh / (sqrtf(vh) + k.eps);
-    return (p - k.lr * u) - k.lr_wd * p;
-  } else if constexpr (KIND == BG_OPT_ADAM_M) {  // in: param, grad, m
-    float gv = in[1][i];
-    if (k.has_wd) gv = gv + k.wd * in[0][i];
-    return k.b1 * in[2][i] + k.omb1 * gv;
-  } else if constexpr (KIND == BG_OPT_ADAM_V) {  // in: param, grad, v
-    float gv = in[1][i];
-    if (k.has_wd) gv = gv + k.wd * in[0][i];
-    return k.b2 * in[2][i] + k.omb2 * (gv * gv);
-  } else {  // BG_OPT_ADAM_PARAM, in: param, m_new, v_new
-    const float mh = in[1][i] / k.c1;
-    const float vh = in[2][i] / k.c2;
-    return in[0][i] - k.lr * (mh / (sqrtf(vh) + k.eps));
+    return (v[0] - k.lr * u) - k.lr_wd * v[0];
+  } else if constexpr (KIND == BG_OPT_ADAM_M) {  // param, grad, m
+    float g = v[1];
+    if (k.has_wd) g = g + k.wd * v[0];
+    return k.b1 * v[2] + k.omb1 * g;
+  } else if constexpr (KIND == BG_OPT_ADAM_V) {  // param, grad, v
+    float g = v[1];
+    if (k.has_wd) g = g + k.wd * v[0];
+    return k.b2 * v[2] + k.omb2 * (g * g);
+  } else {  // BG_OPT_ADAM_PARAM: param, m_new, v_new
+    const float mh = v[1] / k.c1;
+    const float vh = v[2] / k.c2;
+    return v[0] - k.lr * (mh / (sqrtf(vh) + k.eps));
   }
 }
 
-// Grid-stride over n elements; each thread handles 4 consecutive elements per
-// iteration (16-byte accesses when every buffer is 16-byte aligned, which
-// the caller checks through VEC).
-template <int KIND, bool VEC>
-__global__ void __launch_bounds__(256) optim_kernel(OptimConsts k, const float* a, const float* b, const float* c,
-                                                    const float* d, float* __restrict__ out, int64_t n) {
-  const float* const in[4] = {a, b, c, d};
-  const int64_t stride = int64_t(gridDim.x) * blockDim.x * 4;
-  for (int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4; i < n; i += stride) {
-    if (VEC && i + 3 < n) {
-      float r[4];
+template <int KIND>
+__device__ __forceinline__ float4 optim_vec(const OptimConsts& k, const float4 (&x)[4]) {
+  constexpr int NIN = optim_arity(KIND);
+  float r[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = optim_elem<KIND>(k, in, i + j);
-      *reinterpret_cast<float4*>(out + i) = make_float4(r[0], r[1], r[2], r[3]);
-    } else {
-      for (int64_t j = i; j < min(n, i + 4); ++j) out[j] = optim_elem<KIND>(k, in, j);
+  for (int e = 0; e < 4; ++e) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NIN; ++q) v[q] = e == 0 ? x[q].x : e == 1 ? x[q].y : e == 2 ? x[q].z : x[q].w;
+    r[e] = optim_val<KIND>(k, v);
+  }
+  return make_float4(r[0], r[1], r[2], r[3]);
+}
+
+// Grid-stride update of n elements.  VEC (every buffer 16-byte aligned):
+// each thread takes two float4 groups per iteration, issuing all their loads
+// before any arithmetic; the n % 4 tail goes one element per thread.
+template <int KIND, bool VEC>
+__global__ void __launch_bounds__(256) optim_kernel(OptimConsts k, const float* __restrict__ a,
+                                                    const float* __restrict__ b, const float* __restrict__ c,
+                                                    const float* __restrict__ d, float* __restrict__ out,
+                                                    int64_t n) {
+  constexpr int NIN = optim_arity(KIND);
+  const float* in[4] = {a, b, c, d};
+  const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t T = int64_t(gridDim.x) * blockDim.x;
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const int64_t nv = n >> 2;
+    for (int64_t v0 = tid; v0 < nv; v0 += 2 * T) {
+      const int64_t v1 = v0 + T;
+      const bool two = v1 < nv;
+      float4 x0[4], x1[4];
+#pragma unroll
+      for (int q = 0; q < NIN; ++q) {
+        x0[q] = reinterpret_cast<const float4*>(in[q])[v0];
+        if (two) x1[q] = reinterpret_cast<const float4*>(in[q])[v1];
+      }
+      reinterpret_cast<float4*>(out)[v0] = optim_vec<KIND>(k, x0);
+      if (two) reinterpret_cast<float4*>(out)[v1] = optim_vec<KIND>(k, x1);
     }
+    done = nv << 2;
+  }
+  for (int64_t i = done + tid; i < n; i += T) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NIN; ++q) v[q] = in[q][i];
+    out[i] = optim_val<KIND>(k, v);
   }
 }
 
 template <int KIND>
 void launch_optim_kind(bg_ctx* ctx, const OptimConsts& k, const float* const (&in)[4], float* out, int64_t n,
                        bool vec) {
-  const int64_t blocks = std::min<int64_t>((n + 1023) / 1024, 8192);
+  const int64_t blocks = std::min<int64_t>((n + 2047) / 2048, 8192);
   const dim3 grid(unsigned(std::max<int64_t>(blocks, 1)));
   if (vec)
     bg::dispatch(ctx, optim_kernel<KIND, true>, grid, dim3(256), 0, k, in[0], in[1], in[2], in[3], out, n);
@@ -280,6 +403,10 @@ void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, cons
   const dim3 grid(unsigned((rows + 3) / 4));
   if (cols <= 256)
     bg::dispatch(ctx, ln_bwd_input_kernel<4>, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
+  else if (cols <= 512)
+    bg::dispatch(ctx, ln_bwd_input_kernel<8>, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
+  else if (cols <= 768)
+    bg::dispatch(ctx, ln_bwd_input_kernel<12>, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
   else if (cols <= 1024)
     bg::dispatch(ctx, ln_bwd_input_kernel<16>, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
   else
@@ -287,28 +414,55 @@ void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, cons
   hip_check(hipGetLastError(), "layer_norm_backward_input launch");
 }
 
+template <int PER>
+void launch_ln_col_rows(bg_ctx* ctx, const float* dy, const float* x, float* part, int64_t rows, int64_t cols,
+                        int64_t blocks, float eps, bool weight) {
+  if (weight)
+    bg::dispatch(ctx, ln_col_rows_kernel<PER, 4, true>, dim3(unsigned(blocks)), dim3(256), 0, dy, x, part, rows,
+                 cols, eps);
+  else
+    bg::dispatch(ctx, ln_col_rows_kernel<PER, 4, false>, dim3(unsigned(blocks)), dim3(256), 0, dy, x, part, rows,
+                 cols, eps);
+}
+
 void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float* out, int64_t rows, int64_t cols,
                              float eps, bool weight) {
-  // Enough row chunks for ~4 workgroups per CU; each thread sums at least
-  // 16 rows of its column.
-  const int64_t col_blocks = (cols + 255) / 256;
-  int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((rows + 15) / 16, 1024 / std::max<int64_t>(col_blocks, 1)));
-  const int64_t rpc = (rows + chunks - 1) / chunks;
-  chunks = (rows + rpc - 1) / rpc;
-  float* stats = nullptr;
-  size_t ws = size_t(chunks * cols) * sizeof(float);
-  if (weight) ws += size_t(rows) * 2 * sizeof(float);
-  float* part = static_cast<float*>(bg::scratch(ctx, ws, 0));
-  if (weight) {
-    stats = part + chunks * cols;
-    bg::dispatch(ctx, ln_row_stats_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, x, stats, rows, cols, eps);
-    bg::dispatch(ctx, ln_col_partial_kernel<true>, dim3(unsigned(col_blocks), unsigned(chunks)), dim3(256), 0, dy,
-                 x, stats, part, rows, cols, rpc);
+  float* part;
+  int64_t chunks;
+  if (cols <= 1024) {
+    // Rows held in registers, 16 rows per block (4 per wavefront).
+    const int64_t rpb = 16;  // 4 * RPW
+    chunks = (rows + rpb - 1) / rpb;
+    part = static_cast<float*>(bg::scratch(ctx, size_t(chunks * cols) * sizeof(float), 0));
+    if (cols <= 256)
+      launch_ln_col_rows<4>(ctx, dy, x, part, rows, cols, chunks, eps, weight);
+    else if (cols <= 512)
+      launch_ln_col_rows<8>(ctx, dy, x, part, rows, cols, chunks, eps, weight);
+    else if (cols <= 768)
+      launch_ln_col_rows<12>(ctx, dy, x, part, rows, cols, chunks, eps, weight);
+    else
+      launch_ln_col_rows<16>(ctx, dy, x, part, rows, cols, chunks, eps, weight);
   } else {
-    bg::dispatch(ctx, ln_col_partial_kernel<false>, dim3(unsigned(col_blocks), unsigned(chunks)), dim3(256), 0, dy,
-                 x, stats, part, rows, cols, rpc);
+    // Wide rows: row statistics first, then one thread per column over
+    // chunks of 16 rows, for ~2 blocks of 256 columns per chunk and CU.
+    const int64_t col_blocks = (cols + 255) / 256;
+    const int64_t rpc = std::max<int64_t>(16, (rows + 65534) / 65535);  // grid y <= 65535
+    chunks = (rows + rpc - 1) / rpc;
+    size_t ws = size_t(chunks * cols) * sizeof(float);
+    if (weight) ws += size_t(rows) * 2 * sizeof(float);
+    part = static_cast<float*>(bg::scratch(ctx, ws, 0));
+    float* stats = weight ? part + chunks * cols : nullptr;
+    if (weight)
+      bg::dispatch(ctx, ln_row_stats_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, x, stats, rows, cols,
+                   eps);
+    if (weight)
+      bg::dispatch(ctx, ln_col_partial_kernel<true>, dim3(unsigned(col_blocks), unsigned(chunks)), dim3(256), 0, dy,
+                   x, stats, part, rows, cols, rpc);
+    else
+      bg::dispatch(ctx, ln_col_partial_kernel<false>, dim3(unsigned(col_blocks), unsigned(chunks)), dim3(256), 0,
+                   dy, x, stats, part, rows, cols, rpc);
   }
-  bg::dispatch(ctx, ln_col_final_kernel, dim3(unsigned(col_blocks)), dim3(256), 0, part, out, chunks, cols);
+  bg::dispatch(ctx, ln_col_final_kernel, dim3(unsigned((cols + 15) / 16)), dim3(256), 0, part, out, chunks, cols);
   hip_check(hipGetLastError(), "layer_norm_backward column launch");
 }
 

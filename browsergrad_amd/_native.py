@@ -110,6 +110,18 @@ class OptimArgs(C.Structure):
                 ("weight_decay", C.c_double), ("step", C.c_int64)]
 
 
+class ConvDesc(C.Structure):
+    """bg_conv_desc: one convolution of the plan route (any rank, transposed or not)."""
+    _fields_ = [("op", C.c_int32), ("transposed", C.c_int32), ("spatial", C.c_int32), ("pad0", C.c_int32),
+                ("n", C.c_int64), ("c_in", C.c_int64), ("c_out", C.c_int64), ("groups", C.c_int64),
+                ("in_", C.c_int64 * 3), ("out", C.c_int64 * 3), ("k", C.c_int64 * 3), ("stride", C.c_int64 * 3),
+                ("pad", C.c_int64 * 3), ("dilation", C.c_int64 * 3), ("output_pad", C.c_int64 * 3),
+                ("a", handle_t), ("b", handle_t), ("bias", handle_t)]
+
+
+CONV_OPS = {"forward": 0, "backward_input": 1, "backward_weight": 2, "backward_bias": 3}
+
+
 # bg_optimizer_update kinds (BG_OPT_*), keyed by the reference's plan op names.
 OPTIM_KINDS = {
     "SGD_UPDATE": 0, "ADAMW_UPDATE_M": 1, "ADAMW_UPDATE_V": 2, "ADAMW_UPDATE_PARAM": 3,
@@ -157,6 +169,15 @@ SIGNATURES = {
     "bg_layer_norm_backward_bias": (C.c_int, [ctx_p, handle_t, C.c_int64, C.c_int64, PH]),
     "bg_optimizer_update": (C.c_int, [ctx_p, C.c_int, C.POINTER(handle_t), C.c_int, C.POINTER(OptimArgs),
                                       C.c_int64, PH]),
+    "bg_conv1d": (C.c_int, [ctx_p, handle_t, handle_t, handle_t] + [C.c_int64] * 10 + [C.c_int, PH]),
+    "bg_conv1d_backward_input": (C.c_int, [ctx_p, handle_t, handle_t] + [C.c_int64] * 10 + [C.c_int, PH]),
+    "bg_conv1d_backward_weight": (C.c_int, [ctx_p, handle_t, handle_t] + [C.c_int64] * 10 + [C.c_int, PH]),
+    "bg_conv1d_backward_bias": (C.c_int, [ctx_p, handle_t] + [C.c_int64] * 3 + [C.c_int, PH]),
+    "bg_conv2d": (C.c_int, [ctx_p, handle_t, handle_t, handle_t] + [C.c_int64] * 16 + [C.c_int, PH]),
+    "bg_conv2d_backward_input": (C.c_int, [ctx_p, handle_t, handle_t] + [C.c_int64] * 16 + [C.c_int, PH]),
+    "bg_conv2d_backward_weight": (C.c_int, [ctx_p, handle_t, handle_t] + [C.c_int64] * 16 + [C.c_int, PH]),
+    "bg_conv2d_backward_bias": (C.c_int, [ctx_p, handle_t] + [C.c_int64] * 4 + [C.c_int, PH]),
+    "bg_conv_ex": (C.c_int, [ctx_p, C.POINTER(ConvDesc), PH]),
     "bg_copy_strided": (C.c_int, [ctx_p, handle_t, C.c_int64, P64, P64, C.c_int, PH]),
     "bg_reshape": (C.c_int, [ctx_p, handle_t, P64, C.c_int, PH]),
     "bg_reduce_last": (C.c_int, [ctx_p, handle_t, C.c_int64, C.c_int64, C.c_int, C.c_int, PH]),

@@ -338,6 +338,101 @@ class HipRealizerBridge:
                                                   C.byref(out)))
         return int(out.value)
 
+    # -- convolutions (realizer.ts:114-238, 1153-1521) ------------------------------------
+    def conv1d(self, input: int, weight: int, bias: Optional[int], n: int, cIn: int, lIn: int,  # noqa: N803
+               cOut: int, k: int, stride: int, padding: int, dilation: int, groups: int, lOut: int,  # noqa: N803
+               dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_conv1d(self._ctx, int(input), int(weight), int(bias or 0), n, cIn, lIn, cOut, k,
+                                        stride, padding, dilation, groups, lOut, _dtype_code(dtype, "conv1d"),
+                                        C.byref(out)))
+        return int(out.value)
+
+    def conv1d_backward_input(self, dy: int, weight: int, n: int, cIn: int, lIn: int, cOut: int,  # noqa: N803
+                              k: int, stride: int, padding: int, dilation: int, groups: int, lOut: int,  # noqa: N803
+                              dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_conv1d_backward_input(
+            self._ctx, int(dy), int(weight), n, cIn, lIn, cOut, k, stride, padding, dilation, groups, lOut,
+            _dtype_code(dtype, "conv1d_backward_input"), C.byref(out)))
+        return int(out.value)
+
+    def conv1d_backward_weight(self, dy: int, input: int, n: int, cIn: int, lIn: int, cOut: int,  # noqa: N803
+                               k: int, stride: int, padding: int, dilation: int, groups: int, lOut: int,  # noqa: N803
+                               dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_conv1d_backward_weight(
+            self._ctx, int(dy), int(input), n, cIn, lIn, cOut, k, stride, padding, dilation, groups, lOut,
+            _dtype_code(dtype, "conv1d_backward_weight"), C.byref(out)))
+        return int(out.value)
+
+    def conv1d_backward_bias(self, dy: int, n: int, cOut: int, lOut: int, dtype: str = "float32") -> int:  # noqa: N803
+        out = N.handle_t()
+        self._check(self._lib.bg_conv1d_backward_bias(self._ctx, int(dy), n, cOut, lOut,
+                                                      _dtype_code(dtype, "conv1d_backward_bias"), C.byref(out)))
+        return int(out.value)
+
+    def conv2d(self, input: int, weight: int, bias: Optional[int], n: int, cIn: int, h: int, w: int,  # noqa: N803
+               cOut: int, kh: int, kw: int, strideH: int, strideW: int, padH: int, padW: int,  # noqa: N803
+               dilationH: int, dilationW: int, groups: int, outH: int, outW: int,  # noqa: N803
+               dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_conv2d(self._ctx, int(input), int(weight), int(bias or 0), n, cIn, h, w, cOut, kh,
+                                        kw, strideH, strideW, padH, padW, dilationH, dilationW, groups, outH, outW,
+                                        _dtype_code(dtype, "conv2d"), C.byref(out)))
+        return int(out.value)
+
+    def conv2d_backward_input(self, dy: int, weight: int, n: int, cIn: int, h: int, w: int, cOut: int,  # noqa: N803
+                              kh: int, kw: int, strideH: int, strideW: int, padH: int, padW: int,  # noqa: N803
+                              dilationH: int, dilationW: int, groups: int, outH: int, outW: int,  # noqa: N803
+                              dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_conv2d_backward_input(
+            self._ctx, int(dy), int(weight), n, cIn, h, w, cOut, kh, kw, strideH, strideW, padH, padW, dilationH,
+            dilationW, groups, outH, outW, _dtype_code(dtype, "conv2d_backward_input"), C.byref(out)))
+        return int(out.value)
+
+    def conv2d_backward_weight(self, dy: int, input: int, n: int, cIn: int, h: int, w: int, cOut: int,  # noqa: N803
+                               kh: int, kw: int, strideH: int, strideW: int, padH: int, padW: int,  # noqa: N803
+                               dilationH: int, dilationW: int, groups: int, outH: int, outW: int,  # noqa: N803
+                               dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_conv2d_backward_weight(
+            self._ctx, int(dy), int(input), n, cIn, h, w, cOut, kh, kw, strideH, strideW, padH, padW, dilationH,
+            dilationW, groups, outH, outW, _dtype_code(dtype, "conv2d_backward_weight"), C.byref(out)))
+        return int(out.value)
+
+    def conv2d_backward_bias(self, dy: int, n: int, cOut: int, outH: int, outW: int,  # noqa: N803
+                             dtype: str = "float32") -> int:
+        out = N.handle_t()
+        self._check(self._lib.bg_conv2d_backward_bias(self._ctx, int(dy), n, cOut, outH, outW,
+                                                      _dtype_code(dtype, "conv2d_backward_bias"), C.byref(out)))
+        return int(out.value)
+
+    def conv_ex(self, op: str, a: int, b: int = 0, bias: int = 0, *, n: int, c_in: int, c_out: int,
+                in_size: Sequence[int], out_size: Sequence[int], k: Sequence[int], stride: Sequence[int],
+                pad: Sequence[int], dilation: Sequence[int], groups: int = 1, transposed: bool = False,
+                output_pad: Optional[Sequence[int]] = None) -> int:
+        """bg_conv_ex: `op` is forward / backward_input / backward_weight /
+        backward_bias; spatial arrays have one entry per spatial dim."""
+        r = len(in_size)
+        d = N.ConvDesc()
+        d.op = N.CONV_OPS[op]
+        d.transposed = 1 if transposed else 0
+        d.spatial = r
+        d.n, d.c_in, d.c_out, d.groups = int(n), int(c_in), int(c_out), int(groups)
+        for name, vals in (("in_", in_size), ("out", out_size), ("k", k), ("stride", stride), ("pad", pad),
+                           ("dilation", dilation), ("output_pad", output_pad or [0] * r)):
+            if len(vals) != r:
+                raise ValueError(f"conv_ex: {name.strip('_')} needs {r} entries")
+            arr = getattr(d, name)
+            for i, v in enumerate(vals):
+                arr[i] = int(v)
+        d.a, d.b, d.bias = int(a), int(b or 0), int(bias or 0)
+        out = N.handle_t()
+        self._check(self._lib.bg_conv_ex(self._ctx, C.byref(d), C.byref(out)))
+        return int(out.value)
+
     def copy_strided(self, src: int, offset: int, shape: Sequence[int], strides: Sequence[int]) -> int:
         shp = _shape(shape)
         out = N.handle_t()
@@ -549,34 +644,5 @@ class HipRealizerBridge:
         self.profiling = bool(on)
 
     # -- reference protocol methods outside this build's scope ---------------------------
-    def _out_of_scope(self, name: str) -> None:
-        raise JitNotImplementedError(
-            f"HIP bridge: {name} is not part of the HIP realizer's hot path "
-            f"(convolution and user WGSL kernels are out of scope)")
-
-    def conv1d(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv1d")
-
-    def conv1d_backward_input(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv1d_backward_input")
-
-    def conv1d_backward_weight(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv1d_backward_weight")
-
-    def conv1d_backward_bias(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv1d_backward_bias")
-
-    def conv2d(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv2d")
-
-    def conv2d_backward_input(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv2d_backward_input")
-
-    def conv2d_backward_weight(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv2d_backward_weight")
-
-    def conv2d_backward_bias(self, *a: Any, **k: Any) -> Any:
-        self._out_of_scope("conv2d_backward_bias")
-
     def run_user_kernel(self, *a: Any, **k: Any) -> Any:
         raise JitNotImplementedError("HIP bridge: run_user_kernel takes WGSL, which has no HIP meaning")

@@ -257,21 +257,6 @@ static void resolve_profiles(bg_ctx* ctx) {
 
 using namespace bg;
 
-#define BG_API_BEGIN \
-  if (!ctx) return BG_E_INVALID; \
-  try {
-#define BG_API_END                          \
-  }                                         \
-  catch (const bg::Error& e) {              \
-    ctx->err = e.what();                    \
-    return e.code;                          \
-  }                                         \
-  catch (const std::exception& e) {         \
-    ctx->err = std::string("HIP bridge: ") + e.what(); \
-    return BG_E_INVALID;                    \
-  }                                         \
-  return BG_OK;
-
 extern "C" {
 
 const char* bg_version(void) { return "bghip 0.1 gfx950"; }

@@ -160,6 +160,18 @@ void launch_copy_strided(bg_ctx* ctx, const void* src, int64_t elem_size,
 void launch_layer_norm(bg_ctx* ctx, const void* x, int x_dtype,
                        const float* w, const float* b, void* y, int y_dtype,
                        int64_t rows, int64_t cols, float eps);
+// A convolution in the "conv picture": x [n][c][in...] -> y [n][o][out...],
+// weight [o][c/groups][k...]; spatial arrays are (D, H, W), unit-padded for
+// 1-D and 2-D problems.
+struct ConvProblem {
+  int64_t n, c, o, groups;
+  int64_t in[3], out[3], k[3], stride[3], pad[3], dil[3];
+};
+// mode 0: y = conv(a = x, b = w) (+ bias[o]); 1: dx = a = dy against b = w
+// (+ bias[c]); 2: dw from a = dy, b = x.
+void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, const float* b, const float* bias,
+                 float* out);
+void launch_conv_bias_grad(bg_ctx* ctx, const float* dy, float* out, int64_t n, int64_t o, int64_t spatial);
 void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, const float* w, float* dx,
                               int64_t rows, int64_t cols, float eps);
 // Column sums over rows of dy * x_hat (weight) or dy (bias, x unused).
@@ -193,3 +205,21 @@ bg_handle run_plan(bg_ctx* ctx, const char* json, const char* requests_json, con
                    const bg_handle* handles, int n, int dtype, bool resident);
 
 }  // namespace bg
+
+// Body of every C entry point: bg::Error -> its status and message in
+// ctx->err; any other exception -> BG_E_INVALID.
+#define BG_API_BEGIN \
+  if (!ctx) return BG_E_INVALID; \
+  try {
+#define BG_API_END                          \
+  }                                         \
+  catch (const bg::Error& e) {              \
+    ctx->err = e.what();                    \
+    return e.code;                          \
+  }                                         \
+  catch (const std::exception& e) {         \
+    ctx->err = std::string("HIP bridge: ") + e.what(); \
+    return BG_E_INVALID;                    \
+  }                                         \
+  return BG_OK;
+

@@ -30,8 +30,8 @@
 //   CAST between f32 / f16 / bf16 / bool
 // LAYER_NORM_BACKWARD_{INPUT,WEIGHT,BIAS}, SGD_UPDATE, ADAMW_UPDATE_{M,V,PARAM}
 // and ADAM_UPDATE_{M,V,PARAM} lower onto bg_layer_norm_backward_* and
-// bg_optimizer_update (f32 only, as in the reference).  CONV* is refused with
-// BG_E_UNSUPPORTED naming the op.
+// bg_optimizer_update; CONV1D*, CONV2D*, CONV3D* and CONV_TRANSPOSE2D* onto
+// bg_conv_ex (all f32 only, as in the reference).
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -591,6 +591,108 @@ bg_optim_args optim_arg(const Step& s, int kind) {
   return a;
 }
 
+// ---- convolution steps (tensor_plan.ts:554-641, 2321-2830, 3228-3775) --------
+
+struct ConvStep {
+  int spatial = 0;
+  bool transposed = false;
+  int op = 0;  // BG_CONV_*
+};
+
+// CONV1D*, CONV2D*, CONV3D*, CONV_TRANSPOSE2D* -> (rank, transposed, op);
+// spatial 0 for any other op.
+ConvStep conv_step(const std::string& op) {
+  ConvStep c;
+  std::string base = op;
+  static const std::pair<const char*, int> suffixes[] = {
+      {"_BACKWARD_INPUT", BG_CONV_BACKWARD_INPUT},
+      {"_BACKWARD_WEIGHT", BG_CONV_BACKWARD_WEIGHT},
+      {"_BACKWARD_BIAS", BG_CONV_BACKWARD_BIAS}};
+  for (const auto& sf : suffixes) {
+    const std::string suf = sf.first;
+    if (base.size() > suf.size() && base.compare(base.size() - suf.size(), suf.size(), suf) == 0) {
+      base = base.substr(0, base.size() - suf.size());
+      c.op = sf.second;
+      break;
+    }
+  }
+  if (base == "CONV1D") c.spatial = 1;
+  else if (base == "CONV2D") c.spatial = 2;
+  else if (base == "CONV3D") c.spatial = 3;
+  else if (base == "CONV_TRANSPOSE2D") {
+    c.spatial = 2;
+    c.transposed = true;
+  }
+  return c;
+}
+
+struct ConvArg {
+  std::unordered_map<std::string, int64_t> v;
+  int64_t operator[](const char* k) const { return v.at(k); }
+};
+
+// expectConv1dArg / expectConv2dArg / expectConvTranspose2dArg /
+// expectConv3dArg followed by the matching validate*Shape: every field an
+// integer (in the interface's order), sizes positive, padding non-negative,
+// the channel rule of the family.
+ConvArg conv_arg(const Step& s, const ConvStep& c) {
+  const JVal& arg = arg_object(s.arg, s.op);
+  const std::string& op = s.op;
+  static const std::vector<std::string> k1 = {"n", "c_in", "l_in", "c_out", "k", "stride", "padding", "dilation",
+                                              "groups", "l_out"};
+  static const std::vector<std::string> k2 = {"n", "c_in", "h", "w", "c_out", "kh", "kw", "stride_h", "stride_w",
+                                              "pad_h", "pad_w", "dilation_h", "dilation_w", "groups", "out_h",
+                                              "out_w"};
+  static const std::vector<std::string> kt = {"n", "c_in", "h", "w", "c_out", "c_out_per_group", "kh", "kw",
+                                              "stride_h", "stride_w", "pad_h", "pad_w", "output_pad_h",
+                                              "output_pad_w", "dilation_h", "dilation_w", "groups", "out_h",
+                                              "out_w"};
+  static const std::vector<std::string> k3 = {"n", "c_in", "d", "h", "w", "c_out", "kd", "kh", "kw", "stride_d",
+                                              "stride_h", "stride_w", "pad_d", "pad_h", "pad_w", "dilation_d",
+                                              "dilation_h", "dilation_w", "groups", "out_d", "out_h", "out_w"};
+  const std::vector<std::string>& keys = c.transposed ? kt : c.spatial == 1 ? k1 : c.spatial == 2 ? k2 : k3;
+  ConvArg a;
+  for (const std::string& k : keys) a.v[k] = expect_int(arg.get(k.c_str()), op + "." + k);
+  // validate*Shape: positive sizes under their camelCase names.
+  static const std::vector<std::pair<const char*, const char*>> p1 = {
+      {"n", "n"}, {"c_in", "cIn"}, {"l_in", "lIn"}, {"c_out", "cOut"}, {"k", "k"}, {"stride", "stride"},
+      {"dilation", "dilation"}, {"groups", "groups"}, {"l_out", "lOut"}};
+  static const std::vector<std::pair<const char*, const char*>> p2 = {
+      {"n", "n"}, {"c_in", "cIn"}, {"h", "h"}, {"w", "w"}, {"c_out", "cOut"}, {"kh", "kh"}, {"kw", "kw"},
+      {"stride_h", "strideH"}, {"stride_w", "strideW"}, {"dilation_h", "dilationH"},
+      {"dilation_w", "dilationW"}, {"groups", "groups"}, {"out_h", "outH"}, {"out_w", "outW"}};
+  static const std::vector<std::pair<const char*, const char*>> pt = {
+      {"n", "n"}, {"c_in", "cIn"}, {"h", "h"}, {"w", "w"}, {"c_out", "cOut"},
+      {"c_out_per_group", "cOutPerGroup"}, {"kh", "kh"}, {"kw", "kw"}, {"stride_h", "strideH"},
+      {"stride_w", "strideW"}, {"dilation_h", "dilationH"}, {"dilation_w", "dilationW"}, {"groups", "groups"},
+      {"out_h", "outH"}, {"out_w", "outW"}};
+  static const std::vector<std::pair<const char*, const char*>> p3 = {
+      {"n", "n"}, {"c_in", "cIn"}, {"d", "d"}, {"h", "h"}, {"w", "w"}, {"c_out", "cOut"}, {"kd", "kd"},
+      {"kh", "kh"}, {"kw", "kw"}, {"stride_d", "strideD"}, {"stride_h", "strideH"}, {"stride_w", "strideW"},
+      {"dilation_d", "dilationD"}, {"dilation_h", "dilationH"}, {"dilation_w", "dilationW"},
+      {"groups", "groups"}, {"out_d", "outD"}, {"out_h", "outH"}, {"out_w", "outW"}};
+  const auto& pos = c.transposed ? pt : c.spatial == 1 ? p1 : c.spatial == 2 ? p2 : p3;
+  for (const auto& kv : pos)
+    if (a[kv.first] <= 0) plan_fail(op + "." + kv.second + " must be a positive integer");
+  if (c.spatial == 1) {
+    if (a["padding"] < 0) plan_fail(op + ".padding must be a non-negative integer");
+  } else {
+    for (const char* k : {"pad_d", "pad_h", "pad_w"})
+      if (a.v.count(k) && a[k] < 0) plan_fail(op + " padding must be non-negative integers");
+  }
+  if (c.transposed) {
+    if (a["output_pad_h"] < 0 || a["output_pad_w"] < 0)
+      plan_fail(op + " output_padding must be non-negative integers");
+    if (a["c_in"] % a["groups"] != 0 || a["c_out"] != a["c_out_per_group"] * a["groups"])
+      plan_fail(op + " channels must match groups");
+    if (a["output_pad_h"] >= a["stride_h"] || a["output_pad_w"] >= a["stride_w"])
+      plan_fail(op + " output_padding must be smaller than stride");
+  } else if (a["c_in"] % a["groups"] != 0 || a["c_out"] % a["groups"] != 0) {
+    plan_fail(op + " channels must be divisible by groups");
+  }
+  return a;
+}
+
 // ---- execution -------------------------------------------------------------
 
 struct Runner {
@@ -861,6 +963,78 @@ struct Runner {
         expect_shape(s.shape, a.normalized_shape, op + ".output");
         call(bg_layer_norm_backward_bias(ctx, need(s, 0), a.rows, a.cols, &out));
       }
+      ctx->handles[out].shape = s.shape;
+      return own(out);
+    }
+    if (const ConvStep cs = conv_step(op); cs.spatial) {
+      const ConvArg a = conv_arg(s, cs);
+      if (dt != BG_F32) fail(BG_E_DTYPE, "tensor plan " + op + " supports float32 only");
+      const int r = cs.spatial;
+      static const char* ax3[3] = {"d", "h", "w"};
+      bg_conv_desc d{};
+      d.op = cs.op;
+      d.transposed = cs.transposed ? 1 : 0;
+      d.spatial = r;
+      d.n = a["n"];
+      d.c_in = a["c_in"];
+      d.c_out = a["c_out"];
+      d.groups = a["groups"];
+      for (int i = 0; i < r; ++i) {
+        const std::string x = ax3[3 - r + i];
+        if (r == 1) {
+          d.in[0] = a["l_in"];
+          d.out[0] = a["l_out"];
+          d.k[0] = a["k"];
+          d.stride[0] = a["stride"];
+          d.pad[0] = a["padding"];
+          d.dilation[0] = a["dilation"];
+        } else {
+          d.in[i] = a.v.at(x);
+          d.out[i] = a.v.at("out_" + x);
+          d.k[i] = a.v.at("k" + x);
+          d.stride[i] = a.v.at("stride_" + x);
+          d.pad[i] = a.v.at("pad_" + x);
+          d.dilation[i] = a.v.at("dilation_" + x);
+          if (cs.transposed) d.output_pad[i] = a.v.at("output_pad_" + x);
+        }
+      }
+      std::vector<int64_t> xs{d.n, d.c_in}, ys{d.n, d.c_out}, ws;
+      ws = cs.transposed ? std::vector<int64_t>{d.c_in, a["c_out_per_group"]}
+                         : std::vector<int64_t>{d.c_out, d.c_in / d.groups};
+      for (int i = 0; i < r; ++i) {
+        xs.push_back(d.in[i]);
+        ys.push_back(d.out[i]);
+        ws.push_back(d.k[i]);
+      }
+      if (cs.op == BG_CONV_FORWARD) {
+        d.a = need(s, 0);
+        d.b = need(s, 1);
+        expect_shape(rec(d.a).shape, xs, op + ".input");
+        expect_shape(rec(d.b).shape, ws, op + ".weight");
+        expect_shape(s.shape, ys, op + ".output");
+        if (s.inputs.size() > 2) {
+          d.bias = need(s, 2);
+          expect_shape(rec(d.bias).shape, {d.c_out}, op + ".bias");
+        }
+      } else if (cs.op == BG_CONV_BACKWARD_INPUT) {
+        d.a = need(s, 0);
+        d.b = need(s, 1);
+        expect_shape(rec(d.a).shape, ys, op + ".dy");
+        expect_shape(rec(d.b).shape, ws, op + ".weight");
+        expect_shape(s.shape, xs, op + ".output");
+      } else if (cs.op == BG_CONV_BACKWARD_WEIGHT) {
+        d.a = need(s, 0);
+        d.b = need(s, 1);
+        expect_shape(rec(d.a).shape, ys, op + ".dy");
+        expect_shape(rec(d.b).shape, xs, op + ".input");
+        expect_shape(s.shape, ws, op + ".output");
+      } else {
+        d.a = need(s, 0);
+        expect_shape(rec(d.a).shape, ys, op + ".dy");
+        expect_shape(s.shape, {d.c_out}, op + ".output");
+      }
+      bg_handle out = 0;
+      call(bg_conv_ex(ctx, &d, &out));
       ctx->handles[out].shape = s.shape;
       return own(out);
     }

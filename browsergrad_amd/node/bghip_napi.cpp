@@ -295,6 +295,38 @@ napi_value Cast(napi_env env, napi_callback_info info) {  // (ctx, h, src, dst, 
   return number(env, double(out));
 }
 
+// (ctx, op, transposed, a, b|null, bias|null, n, cIn, cOut, groups, in[], out[],
+//  k[], stride[], pad[], dilation[], outputPad[]) -> bg_conv_ex
+napi_value Conv(napi_env env, napi_callback_info info) {
+  Args a(env, info, 17);
+  bg_ctx* ctx = a.ctx();
+  bg_conv_desc d{};
+  d.op = int32_t(a.i64(1));
+  d.transposed = int32_t(a.i64(2));
+  d.a = a.handle(3);
+  d.b = a.is_nullish(4) ? 0 : a.handle(4);
+  d.bias = a.is_nullish(5) ? 0 : a.handle(5);
+  d.n = a.i64(6);
+  d.c_in = a.i64(7);
+  d.c_out = a.i64(8);
+  d.groups = a.i64(9);
+  int64_t* arrays[7] = {d.in, d.out, d.k, d.stride, d.pad, d.dilation, d.output_pad};
+  for (int j = 0; j < 7 && a.ok; ++j) {
+    const std::vector<double> v = a.nums(size_t(10 + j));
+    if (!a.ok) break;
+    if (j == 0) d.spatial = int32_t(v.size());
+    if (v.size() != size_t(d.spatial) || v.size() < 1 || v.size() > 3) {
+      throw_kernel_error(env, "HIP bridge: conv spatial arrays must hold 1 to 3 equal-length entries");
+      return nullptr;
+    }
+    for (size_t i = 0; i < v.size(); ++i) arrays[j][i] = int64_t(v[i]);
+  }
+  if (!a.ok) return nullptr;
+  bg_handle out = 0;
+  if (!check(env, ctx, bg_conv_ex(ctx, &d, &out))) return nullptr;
+  return number(env, double(out));
+}
+
 // (ctx, q, k, v, mask|null, b, h, sq, sk, d, scale, dtype)
 napi_value FlashAttention(napi_env env, napi_callback_info info) {
   Args a(env, info, 12);
@@ -412,6 +444,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"release", Release},           {"handleInfo", HandleInfo},
       {"matmul", Matmul},             {"fusedElementwise", FusedElementwise},
       {"cast", Cast},                 {"flashAttention", FlashAttention},
+      {"conv", Conv},
       {"runTensorPlan", RunTensorPlan}, {"aliveHandles", AliveHandles},
       {"resourceSnapshot", ResourceSnapshot}, {"flushProfiles", FlushProfiles},
       {"version", Version},

@@ -20,6 +20,28 @@ export interface HipRealizerBridge {
   cast(h: Handle, srcDtype: string, dstDtype: string, shape: readonly number[]): Handle;
   flash_attention(q: Handle, k: Handle, v: Handle, mask: Handle | null, b: number, h: number, sq: number,
                   sk: number, d: number, scale: number, dtype: string): Promise<Handle>;
+  conv1d(input: Handle, weight: Handle, bias: Handle | null, n: number, cIn: number, lIn: number, cOut: number,
+         k: number, stride: number, padding: number, dilation: number, groups: number, lOut: number,
+         dtype: string): Handle;
+  conv1d_backward_input(dy: Handle, weight: Handle, n: number, cIn: number, lIn: number, cOut: number, k: number,
+                        stride: number, padding: number, dilation: number, groups: number, lOut: number,
+                        dtype: string): Handle;
+  conv1d_backward_weight(dy: Handle, input: Handle, n: number, cIn: number, lIn: number, cOut: number, k: number,
+                         stride: number, padding: number, dilation: number, groups: number, lOut: number,
+                         dtype: string): Handle;
+  conv1d_backward_bias(dy: Handle, n: number, cOut: number, lOut: number, dtype: string): Handle;
+  conv2d(input: Handle, weight: Handle, bias: Handle | null, n: number, cIn: number, h: number, w: number,
+         cOut: number, kh: number, kw: number, strideH: number, strideW: number, padH: number, padW: number,
+         dilationH: number, dilationW: number, groups: number, outH: number, outW: number, dtype: string): Handle;
+  conv2d_backward_input(dy: Handle, weight: Handle, n: number, cIn: number, h: number, w: number, cOut: number,
+                        kh: number, kw: number, strideH: number, strideW: number, padH: number, padW: number,
+                        dilationH: number, dilationW: number, groups: number, outH: number, outW: number,
+                        dtype: string): Handle;
+  conv2d_backward_weight(dy: Handle, input: Handle, n: number, cIn: number, h: number, w: number, cOut: number,
+                         kh: number, kw: number, strideH: number, strideW: number, padH: number, padW: number,
+                         dilationH: number, dilationW: number, groups: number, outH: number, outW: number,
+                         dtype: string): Handle;
+  conv2d_backward_bias(dy: Handle, n: number, cOut: number, outH: number, outW: number, dtype: string): Handle;
   run_tensor_plan(plan: unknown, inputs: readonly TensorPlanInput[], dtype: string): Promise<Uint8Array>;
   run_tensor_plan_semantic(plan: unknown, requests: unknown, inputs: readonly TensorPlanInput[],
                            dtype: string): Promise<Uint8Array>;

@@ -141,13 +141,58 @@ function createHipRealizerBridge(options = {}) {
     flushProfiles: async () => wrap(() => ({ ...n.resourceSnapshot(ctx), passProfiles: n.flushProfiles(ctx) })),
     close: () => n.ctxDestroy(ctx),
   };
-  const outOfScope = (name) => () => {
-    throw new KernelError(`HIP bridge: ${name} is not part of the HIP realizer's hot path`);
+  // conv1d / conv2d and their backward kernels (realizer.ts:114-238), on the
+  // descriptor entry point bg_conv_ex: op 0 forward, 1 input, 2 weight, 3 bias.
+  const f32 = (dtype, name) => {
+    if (dtype !== 'float32') throw new KernelError(`HIP bridge: ${name} supports float32 only, got ${dtype}`);
   };
-  for (const name of ['conv1d', 'conv1d_backward_input', 'conv1d_backward_weight', 'conv1d_backward_bias',
-    'conv2d', 'conv2d_backward_input', 'conv2d_backward_weight', 'conv2d_backward_bias', 'run_user_kernel']) {
-    bridge[name] = outOfScope(name);
-  }
+  const conv = (op, a, b, bias, nn, cIn, cOut, groups, sp) => wrap(() => n.conv(
+    ctx, op, 0, a, b, bias, nn, cIn, cOut, groups, sp.in, sp.out, sp.k, sp.stride, sp.pad, sp.dil,
+    sp.in.map(() => 0)));
+  const sp1 = (lIn, lOut, k, stride, padding, dilation) =>
+    ({ in: [lIn], out: [lOut], k: [k], stride: [stride], pad: [padding], dil: [dilation] });
+  const sp2 = (h, w, outH, outW, kh, kw, sh, sw, ph, pw, dh, dw) =>
+    ({ in: [h, w], out: [outH, outW], k: [kh, kw], stride: [sh, sw], pad: [ph, pw], dil: [dh, dw] });
+  Object.assign(bridge, {
+    conv1d: (input, weight, bias, nn, cIn, lIn, cOut, k, stride, padding, dilation, groups, lOut, dtype) => {
+      f32(dtype, 'conv1d');
+      return conv(0, input, weight, bias, nn, cIn, cOut, groups, sp1(lIn, lOut, k, stride, padding, dilation));
+    },
+    conv1d_backward_input: (dy, weight, nn, cIn, lIn, cOut, k, stride, padding, dilation, groups, lOut, dtype) => {
+      f32(dtype, 'conv1d_backward_input');
+      return conv(1, dy, weight, null, nn, cIn, cOut, groups, sp1(lIn, lOut, k, stride, padding, dilation));
+    },
+    conv1d_backward_weight: (dy, input, nn, cIn, lIn, cOut, k, stride, padding, dilation, groups, lOut, dtype) => {
+      f32(dtype, 'conv1d_backward_weight');
+      return conv(2, dy, input, null, nn, cIn, cOut, groups, sp1(lIn, lOut, k, stride, padding, dilation));
+    },
+    conv1d_backward_bias: (dy, nn, cOut, lOut, dtype) => {
+      f32(dtype, 'conv1d_backward_bias');
+      return conv(3, dy, null, null, nn, cOut, cOut, 1, sp1(lOut, lOut, 1, 1, 0, 1));
+    },
+    conv2d: (input, weight, bias, nn, cIn, h, w, cOut, kh, kw, sh, sw, ph, pw, dh, dw, groups, outH, outW,
+      dtype) => {
+      f32(dtype, 'conv2d');
+      return conv(0, input, weight, bias, nn, cIn, cOut, groups, sp2(h, w, outH, outW, kh, kw, sh, sw, ph, pw, dh, dw));
+    },
+    conv2d_backward_input: (dy, weight, nn, cIn, h, w, cOut, kh, kw, sh, sw, ph, pw, dh, dw, groups, outH, outW,
+      dtype) => {
+      f32(dtype, 'conv2d_backward_input');
+      return conv(1, dy, weight, null, nn, cIn, cOut, groups, sp2(h, w, outH, outW, kh, kw, sh, sw, ph, pw, dh, dw));
+    },
+    conv2d_backward_weight: (dy, input, nn, cIn, h, w, cOut, kh, kw, sh, sw, ph, pw, dh, dw, groups, outH, outW,
+      dtype) => {
+      f32(dtype, 'conv2d_backward_weight');
+      return conv(2, dy, input, null, nn, cIn, cOut, groups, sp2(h, w, outH, outW, kh, kw, sh, sw, ph, pw, dh, dw));
+    },
+    conv2d_backward_bias: (dy, nn, cOut, outH, outW, dtype) => {
+      f32(dtype, 'conv2d_backward_bias');
+      return conv(3, dy, null, null, nn, cOut, cOut, 1, sp2(outH, outW, outH, outW, 1, 1, 1, 1, 0, 0, 1, 1));
+    },
+    run_user_kernel: () => {
+      throw new KernelError("HIP bridge: run_user_kernel takes WGSL, which has no HIP meaning");
+    },
+  });
   return bridge;
 }
 

@@ -274,6 +274,59 @@ int bg_flash_attention(bg_ctx* ctx, bg_handle q, bg_handle k, bg_handle v,
                        int64_t sk, int64_t d, float scale, int dtype,
                        bg_handle* out);
 
+/* conv1d / conv2d and their backward kernels: realizer.ts:114-238
+ * (interface), 1153-1521 (implementation).  f32 only (dtype must be BG_F32,
+ * the reference's assertF32).  Layouts: input [n, c_in, l_in] or
+ * [n, c_in, h, w]; weight [c_out, c_in/groups, k] or [c_out, c_in/groups,
+ * kh, kw]; bias [c_out] or 0 for none; dy [n, c_out, l_out] or
+ * [n, c_out, out_h, out_w].  The output sizes are taken as given (the
+ * reference does not derive them): positions whose window lies outside the
+ * padded input read zeros.  backward_input returns dx in the input's
+ * layout, backward_weight dw in the weight's, backward_bias db [c_out]. */
+int bg_conv1d(bg_ctx* ctx, bg_handle input, bg_handle weight, bg_handle bias,
+              int64_t n, int64_t c_in, int64_t l_in, int64_t c_out, int64_t k,
+              int64_t stride, int64_t padding, int64_t dilation,
+              int64_t groups, int64_t l_out, int dtype, bg_handle* out);
+int bg_conv1d_backward_input(bg_ctx* ctx, bg_handle dy, bg_handle weight,
+                             int64_t n, int64_t c_in, int64_t l_in,
+                             int64_t c_out, int64_t k, int64_t stride,
+                             int64_t padding, int64_t dilation, int64_t groups,
+                             int64_t l_out, int dtype, bg_handle* out);
+int bg_conv1d_backward_weight(bg_ctx* ctx, bg_handle dy, bg_handle input,
+                              int64_t n, int64_t c_in, int64_t l_in,
+                              int64_t c_out, int64_t k, int64_t stride,
+                              int64_t padding, int64_t dilation,
+                              int64_t groups, int64_t l_out, int dtype,
+                              bg_handle* out);
+int bg_conv1d_backward_bias(bg_ctx* ctx, bg_handle dy, int64_t n,
+                            int64_t c_out, int64_t l_out, int dtype,
+                            bg_handle* out);
+int bg_conv2d(bg_ctx* ctx, bg_handle input, bg_handle weight, bg_handle bias,
+              int64_t n, int64_t c_in, int64_t h, int64_t w, int64_t c_out,
+              int64_t kh, int64_t kw, int64_t stride_h, int64_t stride_w,
+              int64_t pad_h, int64_t pad_w, int64_t dilation_h,
+              int64_t dilation_w, int64_t groups, int64_t out_h,
+              int64_t out_w, int dtype, bg_handle* out);
+int bg_conv2d_backward_input(bg_ctx* ctx, bg_handle dy, bg_handle weight,
+                             int64_t n, int64_t c_in, int64_t h, int64_t w,
+                             int64_t c_out, int64_t kh, int64_t kw,
+                             int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                             int64_t pad_w, int64_t dilation_h,
+                             int64_t dilation_w, int64_t groups,
+                             int64_t out_h, int64_t out_w, int dtype,
+                             bg_handle* out);
+int bg_conv2d_backward_weight(bg_ctx* ctx, bg_handle dy, bg_handle input,
+                              int64_t n, int64_t c_in, int64_t h, int64_t w,
+                              int64_t c_out, int64_t kh, int64_t kw,
+                              int64_t stride_h, int64_t stride_w,
+                              int64_t pad_h, int64_t pad_w,
+                              int64_t dilation_h, int64_t dilation_w,
+                              int64_t groups, int64_t out_h, int64_t out_w,
+                              int dtype, bg_handle* out);
+int bg_conv2d_backward_bias(bg_ctx* ctx, bg_handle dy, int64_t n,
+                            int64_t c_out, int64_t out_h, int64_t out_w,
+                            int dtype, bg_handle* out);
+
 /* ---- extensions --------------------------------------------------------- */
 int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out);
 int bg_fused_ex(bg_ctx* ctx, const bg_fused_desc* desc, bg_handle* out);
@@ -329,6 +382,36 @@ typedef struct bg_optim_args {
 int bg_optimizer_update(bg_ctx* ctx, int kind, const bg_handle* inputs,
                         int n_inputs, const bg_optim_args* args, int64_t n,
                         bg_handle* out);
+/* Any convolution of the tensor-plan route (CONV1D*, CONV2D*, CONV3D*,
+ * CONV_TRANSPOSE2D*, tensor_plan.ts:554-641; argument rules :3228-3775;
+ * oracle _realize.py:413-1005) through one descriptor.  The first `spatial`
+ * entries of each array are used, in (D,) H, W order.  Inputs by op:
+ *   FORWARD          a = x [n, c_in, in...], b = weight, bias (0 = none)
+ *   BACKWARD_INPUT   a = dy [n, c_out, out...], b = weight   -> [n, c_in, in...]
+ *   BACKWARD_WEIGHT  a = dy, b = x                           -> weight layout
+ *   BACKWARD_BIAS    a = dy                                  -> [c_out]
+ * weight is [c_out, c_in/groups, k...], or [c_in, c_out/groups, k...] when
+ * `transposed` (ConvTranspose: y[n, co, q] = sum x[n, ci, p] w[ci, co', kv]
+ * over q = p*stride - pad + kv*dilation; output_pad only sizes the output,
+ * which is given).  (extension) */
+enum {
+  BG_CONV_FORWARD = 0,
+  BG_CONV_BACKWARD_INPUT = 1,
+  BG_CONV_BACKWARD_WEIGHT = 2,
+  BG_CONV_BACKWARD_BIAS = 3
+};
+typedef struct bg_conv_desc {
+  int32_t op;
+  int32_t transposed;
+  int32_t spatial; /* 1, 2 or 3 */
+  int32_t pad0;
+  int64_t n, c_in, c_out, groups;
+  int64_t in[3];  /* input spatial size */
+  int64_t out[3]; /* output spatial size */
+  int64_t k[3], stride[3], pad[3], dilation[3], output_pad[3];
+  bg_handle a, b, bias;
+} bg_conv_desc;
+int bg_conv_ex(bg_ctx* ctx, const bg_conv_desc* desc, bg_handle* out);
 /* Strided copy (PERMUTE / SLICE / BROADCAST materialisation,
  * tensor_plan.ts:824-997): out[i0..i{r-1}] = src[offset + sum(i_j*strides[j])]
  * in the dtype of src, shape `shape`. */

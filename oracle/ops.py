@@ -273,6 +273,137 @@ def adam_update_param(param, m_new, v_new, lr: float, beta1: float, beta2: float
     return np.asarray(param, F32) - F32(lr) * (m_hat / (np.sqrt(v_hat) + F32(eps)))
 
 
+# ---------------------------------------------------------------------------
+# Convolutions (_realize.py:413-1005): N-d restatements of the per-rank
+# handlers.  x [n, c, *in], weight [o, c/groups, *k]; every tap whose input
+# index falls outside [0, in) contributes nothing (the handlers pad with zeros
+# by `pad` and the transposed handler bounds-checks each output index), and
+# the output sizes are taken as given.  Products and sums are float32; the
+# reduction order is NumPy's (einsum), not the handlers' loop order.
+# ---------------------------------------------------------------------------
+
+
+def _tap_slices(offset, out_len, stride):
+    return slice(offset, offset + (out_len - 1) * stride + 1, stride)
+
+
+def _padded(x, pad, need):
+    """x zero-padded by pad[i] in front of spatial dim i and far enough
+    behind that index need[i] - 1 exists."""
+    widths = [(0, 0), (0, 0)]
+    for i, p in enumerate(pad):
+        hi = max(p, need[i] - x.shape[2 + i] - p)
+        widths.append((p, hi))
+    return np.pad(np.asarray(x, F32), widths)
+
+
+def _kernel_taps(k):
+    return list(np.ndindex(*k))
+
+
+def _conv_columns(x, k, stride, pad, dil, out):
+    """cols[n, c, tap, *out] = x[n, c, out*stride + tap*dil - pad] (0 outside)."""
+    need = [(out[i] - 1) * stride[i] + (k[i] - 1) * dil[i] + 1 for i in range(len(k))]
+    xp = _padded(x, pad, need)
+    taps = []
+    for t in _kernel_taps(k):
+        sl = tuple(_tap_slices(t[i] * dil[i], out[i], stride[i]) for i in range(len(k)))
+        taps.append(xp[(slice(None), slice(None)) + sl])
+    return np.stack(taps, axis=2)
+
+
+def conv_forward(x, w, bias, stride, pad, dil, groups, out):
+    """CONV1D / CONV2D / CONV3D (_realize.py:413-450, 532-583, 815-878):
+    y[n, g*opg + o, p] = sum_{c, tap} x[n, g*cpg + c, p*s + tap*d - pad] * w[g*opg + o, c, tap] (+ bias)."""
+    x = np.asarray(x, F32)
+    w = np.asarray(w, F32)
+    n, c = x.shape[:2]
+    o = w.shape[0]
+    k = w.shape[2:]
+    cols = _conv_columns(x, k, stride, pad, dil, out)  # [n, c, taps, *out]
+    cpg, opg = c // groups, o // groups
+    ys = []
+    for g in range(groups):
+        cg = cols[:, g * cpg:(g + 1) * cpg].reshape(n, cpg * len(_kernel_taps(k)), -1)
+        wg = w[g * opg:(g + 1) * opg].reshape(opg, -1)
+        ys.append(np.einsum("ok,nkp->nop", wg, cg))
+    y = np.concatenate(ys, axis=1).reshape((n, o) + tuple(out)).astype(F32)
+    if bias is not None:
+        y = y + np.asarray(bias, F32).reshape((1, o) + (1,) * len(k))
+    return y
+
+
+def conv_backward_input(dy, w, stride, pad, dil, groups, in_size):
+    """CONV*_BACKWARD_INPUT (_realize.py:452-488, 585-636, 880-941): every
+    dy[n, g*opg + o, p] * w[g*opg + o, c, tap] is added into
+    dx[n, g*cpg + c, p*s + tap*d - pad]; taps outside [0, in) are dropped."""
+    dy = np.asarray(dy, F32)
+    w = np.asarray(w, F32)
+    n, o = dy.shape[:2]
+    out = dy.shape[2:]
+    cpg = w.shape[1]
+    k = w.shape[2:]
+    opg = o // groups
+    r = len(k)
+    full = [max(in_size[i] + 2 * pad[i], (out[i] - 1) * stride[i] + (k[i] - 1) * dil[i] + 1) for i in range(r)]
+    dxp = np.zeros((n, cpg * groups) + tuple(full), F32)
+    for ti, t in enumerate(_kernel_taps(k)):
+        sl = tuple(_tap_slices(t[i] * dil[i], out[i], stride[i]) for i in range(r))
+        for g in range(groups):
+            wt = w[g * opg:(g + 1) * opg][(slice(None), slice(None)) + tuple(t)]  # [opg, cpg]
+            contrib = np.einsum("oc,no...->nc...", wt, dy[:, g * opg:(g + 1) * opg])
+            dxp[(slice(None), slice(g * cpg, (g + 1) * cpg)) + sl] += contrib
+    crop = tuple(slice(pad[i], pad[i] + in_size[i]) for i in range(r))
+    return dxp[(slice(None), slice(None)) + crop].copy()
+
+
+def conv_backward_weight(dy, x, k, stride, pad, dil, groups):
+    """CONV*_BACKWARD_WEIGHT (_realize.py:490-525, 638-681, 943-1001):
+    dw[g*opg + o, c, tap] = sum_{n, p} dy[n, g*opg + o, p] * x[n, g*cpg + c, p*s + tap*d - pad]."""
+    dy = np.asarray(dy, F32)
+    x = np.asarray(x, F32)
+    n, o = dy.shape[:2]
+    out = dy.shape[2:]
+    c = x.shape[1]
+    cols = _conv_columns(x, k, stride, pad, dil, out)
+    cpg, opg = c // groups, o // groups
+    ntap = len(_kernel_taps(k))
+    ws = []
+    for g in range(groups):
+        cg = cols[:, g * cpg:(g + 1) * cpg].reshape(n, cpg * ntap, -1)
+        dg = dy[:, g * opg:(g + 1) * opg].reshape(n, opg, -1)
+        ws.append(np.einsum("nop,nkp->ok", dg, cg))
+    return np.concatenate(ws, axis=0).reshape((o, cpg) + tuple(k)).astype(F32)
+
+
+def conv_backward_bias(dy):
+    """CONV*_BACKWARD_BIAS (_realize.py:527-529, 683-685, 1003-1005): sum over n and space."""
+    dy = np.asarray(dy, F32)
+    return dy.sum(axis=(0,) + tuple(range(2, dy.ndim)))
+
+
+def conv_transpose_forward(x, w, bias, stride, pad, dil, groups, out):
+    """CONV_TRANSPOSE2D (_realize.py:712-744): x [n, ci, *in], w [ci, co/groups, *k];
+    x[n, ci, p] * w[ci, co', tap] lands on y[n, g*co_pg + co', p*s - pad + tap*d]
+    (output indices outside [0, out) dropped), then + bias."""
+    y = conv_backward_input(x, w, stride, pad, dil, groups, out)
+    if bias is not None:
+        y = y + np.asarray(bias, F32).reshape((1, -1) + (1,) * (y.ndim - 2))
+    return y
+
+
+def conv_transpose_backward_input(dy, w, stride, pad, dil, groups, in_size):
+    """CONV_TRANSPOSE2D_BACKWARD_INPUT (_realize.py:747-776): the forward
+    convolution of dy with the same weight."""
+    return conv_forward(dy, w, None, stride, pad, dil, groups, in_size)
+
+
+def conv_transpose_backward_weight(dy, x, k, stride, pad, dil, groups):
+    """CONV_TRANSPOSE2D_BACKWARD_WEIGHT (_realize.py:779-807):
+    dw[ci, co', tap] = sum_{n, p} x[n, ci, p] * dy[n, g*co_pg + co', p*s - pad + tap*d]."""
+    return conv_backward_weight(x, dy, k, stride, pad, dil, groups)
+
+
 GELU_C = F32((2.0 / np.pi) ** 0.5)
 
 

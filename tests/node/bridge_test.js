@@ -4,6 +4,7 @@
 //   matmul [[1,2],[3,4]]·[[5,6],[7,8]] = [19,22,43,50]   webgpu_real.test.ts:1558-1589
 //   fused exp(a+b)/a (closed form per element)           webgpu_real.test.ts:1431-1472
 //   attention CS336 non-causal rows                      flash_attention_oracle.test.ts:16-52
+//   conv1d / conv2d and conv1d backward known answers    webgpu_real.test.ts:943-1203
 //   residency: upload/release/alive bookkeeping          realizer.ts:906-943
 const assert = require('assert');
 const path = require('path');
@@ -73,12 +74,33 @@ async function main() {
   close(fromBytes(await br.materialize(root, [3, 2], 'float32')), want, 1e-6, 'resident plan');
   assert.strictEqual((await br.semanticTensorPlanExecutionTrace(root)).preparation.requests[0].valueId, 2);
 
+  console.log('[node] conv1d / conv2d known answers');
+  // webgpu_real.test.ts:943-1203
+  const cx = br.upload(f32([1, 2, 3, 4]), [1, 1, 4], 'float32');
+  const cw = br.upload(f32([2, -1]), [1, 1, 2], 'float32');
+  const cb = br.upload(f32([0.5]), [1], 'float32');
+  const cy = br.conv1d(cx, cw, cb, 1, 1, 4, 1, 2, 1, 0, 1, 1, 3, 'float32');
+  close(fromBytes(await br.materialize(cy, [1, 1, 3], 'float32')), [0.5, 1.5, 2.5], 0, 'conv1d');
+  const cdy = br.upload(f32([10, 20, 30]), [1, 1, 3], 'float32');
+  const cdx = br.conv1d_backward_input(cdy, cw, 1, 1, 4, 1, 2, 1, 0, 1, 1, 3, 'float32');
+  close(fromBytes(await br.materialize(cdx, [1, 1, 4], 'float32')), [20, 30, 40, -30], 0, 'conv1d dx');
+  const cdw = br.conv1d_backward_weight(cdy, cx, 1, 1, 4, 1, 2, 1, 0, 1, 1, 3, 'float32');
+  close(fromBytes(await br.materialize(cdw, [1, 1, 2], 'float32')), [140, 200], 0, 'conv1d dw');
+  const cdb = br.conv1d_backward_bias(cdy, 1, 1, 3, 'float32');
+  close(fromBytes(await br.materialize(cdb, [1], 'float32')), [60], 0, 'conv1d db');
+  const x2 = br.upload(f32([1, 2, 3, 4, 5, 6, 7, 8, 9]), [1, 1, 3, 3], 'float32');
+  const w2 = br.upload(f32([1, 0, 0, -1]), [1, 1, 2, 2], 'float32');
+  const y2 = br.conv2d(x2, w2, cb, 1, 1, 3, 3, 1, 2, 2, 1, 1, 0, 0, 1, 1, 1, 2, 2, 'float32');
+  close(fromBytes(await br.materialize(y2, [1, 1, 2, 2], 'float32')), [-3.5, -3.5, -3.5, -3.5], 0, 'conv2d');
+  for (const h of [cx, cw, cb, cy, cdy, cdx, cdw, cdb, x2, w2, y2]) br.release(h);
+
   console.log('[node] errors are KernelError');
   assert.throws(() => br.matmul(a, 999999, 2, 2, 2, 'float32'), (e) => e.name === 'KernelError');
   await assert.rejects(br.run_tensor_plan_semantic(plan, { ...requests, requests: [] },
                                                    [{ valueId: 0, data: f32(x) }], 'float32'),
                        (e) => e instanceof KernelError && /expected exactly 1 request/.test(e.message));
   assert.throws(() => br.conv2d(), (e) => e.name === 'KernelError');
+  assert.throws(() => br.run_user_kernel(), (e) => e.name === 'KernelError');
 
   console.log('[node] residency bookkeeping');
   for (const h of [a, b, c, ha, hb, hf, q, k, v, o, h16, back, root]) br.release(h);

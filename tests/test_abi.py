@@ -69,6 +69,8 @@ def test_struct_layouts_match_header():
     assert C.sizeof(N.FusedOp) == 16
     assert C.sizeof(N.MatmulDesc) == 3 * 8 + 12 * 8 + 6 * 4
     assert C.sizeof(N.PassProfile) == 48 + 8 + 8 + 8
+    assert C.sizeof(N.OptimArgs) == 6 * 8
+    assert C.sizeof(N.ConvDesc) == 4 * 4 + 4 * 8 + 7 * 3 * 8 + 3 * 8
 
 
 def test_fused_codegen_compiles_every_opcode(lib):

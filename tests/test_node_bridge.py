@@ -32,7 +32,7 @@ def test_addon_loads_and_exports():
     assert r.returncode == 0, r.stderr
     out = r.stdout.strip()
     for name in ("createHipRealizerBridge", "KernelError", "ctxCreate", "upload", "materialize", "matmul",
-                 "fusedElementwise", "cast", "flashAttention", "runTensorPlan", "aliveHandles",
+                 "fusedElementwise", "cast", "flashAttention", "conv", "runTensorPlan", "aliveHandles",
                  "resourceSnapshot", "flushProfiles"):
         assert name in out
     assert "bghip" in out

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the HIP realizer on 1 MI355X (the BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,c4,c5,train | copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,c4,c5,train,conv | copy]
 
 Prints ONE JSON line.  ``value`` is configs[1] of BASELINE.json -- the fused
 elementwise + row-reduction chain ``relu(a*b+c)*exp(-a*a) -> sum(axis=1)`` on
@@ -13,8 +13,9 @@ rotated so the 256 MB Infinity Cache cannot hold the working set.
 ``extra`` carries the other configs of the metric (GEMM and attention
 TFLOP/s with their fraction of the MFMA peak, the MLP latency) and the
 training primitives of the plan route (AdamW update, LayerNorm backward,
-GB/s with their fraction of HBM peak), each with the per-launch kernel time
-measured by HIP events on the library's stream.
+GB/s with their fraction of HBM peak) and a conv2d layer's forward and
+backward kernels (TFLOP/s against the f32 MFMA peak), each with the
+per-launch kernel time measured by HIP events on the library's stream.
 
 ``roofline`` is for the dominant kernel of ``value`` (the fused kernel),
 ``cpu_baseline`` is the NumPy restatement of the reference CPU realizer
@@ -395,6 +396,66 @@ def bench_train(br, steps, warmup):
     return out
 
 
+# --------------------------------------------------------------------------- convolutions
+
+CONV = dict(n=32, c=128, hw=28, o=128, k=3)  # a ResNet-50 stage-2 3x3 layer, stride 1, pad 1
+
+
+def bench_conv(br, steps, warmup):
+    """conv2d forward, input gradient, weight gradient and bias gradient of
+    one 3x3 layer (f32, implicit-GEMM MFMA): TFLOP/s against 2 * N*O*H*W * C*9
+    per op and the f32 MFMA peak; the bias gradient in GB/s."""
+    n, c, hw, o, k = CONV["n"], CONV["c"], CONV["hw"], CONV["o"], CONV["k"]
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((n, c, hw, hw), dtype=np.float32)
+    w = (rng.standard_normal((o, c, k, k), dtype=np.float32) / np.float32(np.sqrt(c * k * k)))
+    b = rng.standard_normal(o, dtype=np.float32)
+    dy = rng.standard_normal((n, o, hw, hw), dtype=np.float32)
+    hx, hw_, hb, hdy = (br.upload(t, t.shape, "float32") for t in (x, w, b, dy))
+    geo = dict(n=n, c_in=c, c_out=o, in_size=(hw, hw), out_size=(hw, hw), k=(k, k), stride=(1, 1), pad=(1, 1),
+               dilation=(1, 1))
+    flops = 2.0 * n * o * hw * hw * c * k * k
+    ops = {
+        "conv2d": ("forward", hx, hw_, hb),
+        "conv2d_backward_input": ("backward_input", hdy, hw_, 0),
+        "conv2d_backward_weight": ("backward_weight", hdy, hx, 0),
+    }
+    out = {"layer": f"N{n} C{c} {hw}x{hw} O{o} k{k} s1 p1", "flops_per_op": flops}
+    for label, (op, a_, b_, bias) in ops.items():
+        def step(op=op, a_=a_, b_=b_, bias=bias):
+            br.release(br.conv_ex(op, a_, b_, bias, **geo))
+
+        wall_ms, k_ms, _ = timed(br, step, steps, warmup, label)
+        tf = flops / (k_ms * 1e-3) / 1e12
+        out[label] = {"kernel_us": round(k_ms * 1e3, 2), "wall_us": round(wall_ms * 1e3, 2),
+                      "tflops_kernel": round(tf, 2), "frac_fp32_peak": round(tf / FP32_PEAK_TFLOPS, 4)}
+
+    def bias_step():
+        br.release(br.conv_ex("backward_bias", hdy, **geo))
+
+    wall_ms, k_ms, _ = timed(br, bias_step, steps, warmup, "conv2d_backward_bias")
+    gbs = dy.nbytes / (k_ms * 1e-3) / 1e9
+    out["conv2d_backward_bias"] = {"kernel_us": round(k_ms * 1e3, 2), "gbs_kernel": round(gbs, 1),
+                                   "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    # Parity: the first two images of the forward output against float64
+    # (bound 8 sqrt(K) 2^-24 * sum|x||w|, K = C*9).
+    import torch
+    import torch.nn.functional as F
+    h = br.conv_ex("forward", hx, hw_, hb, **geo)
+    y = br.to_numpy(h)[:2]
+    br.release(h)
+    x64 = torch.tensor(x[:2], dtype=torch.float64)
+    w64 = torch.tensor(w, dtype=torch.float64)
+    truth = F.conv2d(x64, w64, torch.tensor(b, dtype=torch.float64), padding=1).numpy()
+    mass = F.conv2d(x64.abs(), w64.abs(), torch.tensor(np.abs(b), dtype=torch.float64), padding=1).numpy()
+    bound = 8 * np.sqrt(c * k * k) * 2.0 ** -24 * mass + 1e-6
+    out["forward_parity"] = {"pass": bool(np.all(np.abs(y - truth) <= bound)),
+                             "max_err_over_bound": float(np.max(np.abs(y - truth) / bound))}
+    for hh in (hx, hw_, hb, hdy):
+        br.release(hh)
+    return out
+
+
 def copy_probe(br, reps=5):
     """A plain copy kernel of known size (256 MiB read + 256 MiB written per
     launch): the calibration point for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -414,7 +475,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c1,c2,c3,c4,c5,train")
+    ap.add_argument("--only", default="c1,c2,c3,c4,c5,train,conv")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -452,6 +513,10 @@ def main() -> int:
         log("training primitives: AdamW over 124M f32 params, LayerNorm backward 8192x768")
         extra["train_adamw_layernorm_bwd"] = bench_train(br, max(10, a.steps // 5), max(3, a.warmup // 2))
         log(f"  {extra['train_adamw_layernorm_bwd']}")
+    if "conv" in only:
+        log("conv2d 3x3 N32 C128 28x28 O128 f32: forward, input / weight / bias gradients")
+        extra["conv2d_3x3_fp32"] = bench_conv(br, max(10, a.steps // 5), max(3, a.warmup // 2))
+        log(f"  {extra['conv2d_3x3_fp32']}")
     if "c1" in only:
         log("c1 mlp 784-128-10 batch 64 f32")
         extra["c1_mlp_fp32"] = bench_c1(br, a.steps, a.warmup)

@@ -17,8 +17,9 @@
 // Operands are gathered straight from the NCDHW tensors into LDS (no im2col
 // buffer in HBM); out-of-range taps load 0, exactly as the reference's
 // bounds-checked loops skip them.  The product runs on v_mfma_f32_32x32x2f32
-// (full f32) in 64 x 64 workgroup tiles, four wavefronts of 32 x 32.
+// (full f32) in 64- or 128-wide workgroup tiles of four wavefronts.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.cuh"
 #include "core.h"
@@ -66,39 +67,52 @@ struct ConvK {
   FDiv f_oS, f_oHW, f_oW, f_S, f_HW, f_W, f_KV, f_KHW, f_KW, f_sd, f_sh, f_sw;
 };
 
-constexpr int CBM = 64, CBN = 64, CBK = 16, CLD = CBM + 1;
+constexpr int CBK = 16;
 
-template <int MODE>
+// Workgroup tile BM x BN (64 or 128 each), four wavefronts in a 2 x 2 grid,
+// each holding (BM/2) x (BN/2) as TM x TN MFMA 32 x 32 accumulators.
+// Operand tiles are staged k-major in LDS (rows padded by one float).
+//
+// Two load mappings: "row-mapped" (FWD / DGRAD A) gives thread t the fixed
+// row t % BM and the k offsets t / BM + (256 / BM) * i, which are uniform
+// over a wavefront, so the k decomposition runs on the scalar unit;
+// "k-mapped" (the other operands) gives the fixed k offset t % 16 and the
+// rows t / 16 + 16 * i.
+template <int MODE, int BM, int BN>
 __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
-  __shared__ float As[2][CBK * CLD];
-  __shared__ float Bs[2][CBK * CLD];
+  constexpr int LDA = BM + 1, LDB = BN + 1;
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int NA = BM * CBK / 256, NB = BN * CBK / 256;
+  constexpr int RSTEP = 256 / BM;  // row-mapped k stride
+  __shared__ float As[2][CBK * LDA];
+  __shared__ float Bs[2][CBK * LDB];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int tm = int(blockIdx.x) % P.tiles_m, tn = int(blockIdx.x) / P.tiles_m;
   const int g = MODE == MODE_WGRAD ? int(blockIdx.y) / P.ksplit : int(blockIdx.y);
   const int split = MODE == MODE_WGRAD ? int(blockIdx.y) % P.ksplit : 0;
-  const int m0 = tm * CBM, n0 = tn * CBN;
+  const int m0 = tm * BM, n0 = tn * BN;
   const int kbeg = split * P.k_chunk;
   const int kend = min(P.K, kbeg + P.k_chunk);
   const int HW = P.H * P.W, oHW = P.oH * P.oW, KHW = P.KH * P.KW;
 
-  // Per-thread fixed coordinates.  "Row-mapped" operands give lane l row
-  // m0 + l and the k offsets wave + 4 i; "k-mapped" ones give every thread
-  // the k offset tid & 15 and the rows (tid >> 4) + 16 i.
-  const int kk_k = tid & 15;
-  const int r_k = tid >> 4;
-  // FWD / DGRAD A (row-mapped): output (FWD) or input (DGRAD) position.
+  const int r_row = tid % BM;                                   // row-mapped row
+  const int k_row0 = __builtin_amdgcn_readfirstlane(tid / BM);  // row-mapped first k offset
+  const int kk_k = tid & 15;                                    // k-mapped k offset
+  const int r_k = tid >> 4;                                     // k-mapped first row
+
+  // FWD / DGRAD A: this thread's output (FWD) or input (DGRAD) position.
   int64_t a_base = 0;
   int a_p0 = 0, a_p1 = 0, a_p2 = 0;
   bool a_row_ok = false;
-  // WGRAD B rows (k-mapped): (c, kd, kh, kw) of the four columns j.
-  int64_t wb_chan[4] = {0, 0, 0, 0};
-  int wb_d[4] = {0, 0, 0, 0}, wb_h[4] = {0, 0, 0, 0}, wb_w[4] = {0, 0, 0, 0};
-  bool wb_ok[4] = {false, false, false, false};
+  // WGRAD B: (c, kd, kh, kw) of this thread's NB columns.
+  int64_t wb_chan[NB];
+  int wb_d[NB], wb_h[NB], wb_w[NB];
+  bool wb_ok[NB];
   if constexpr (MODE == MODE_FWD || MODE == MODE_DGRAD) {
-    const int m = m0 + lane;
+    const int m = m0 + r_row;
     a_row_ok = m < P.M;
     const uint32_t mm = a_row_ok ? uint32_t(m) : 0u;
     if constexpr (MODE == MODE_FWD) {
@@ -121,7 +135,7 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
   }
   if constexpr (MODE == MODE_WGRAD) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int j = n0 + r_k + 16 * i;
       wb_ok[i] = j < P.NC;
       const uint32_t jj = wb_ok[i] ? uint32_t(j) : 0u;
@@ -135,40 +149,40 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
     }
   }
 
-  float ra[4], rb[4];
+  float ra[NA], rb[NB];
   auto fetch = [&](int k0) {
     if constexpr (MODE == MODE_FWD) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {  // A: x gathered at (m, k)
-        const int k = k0 + wave + 4 * i;
+      for (int i = 0; i < NA; ++i) {  // A: x at (m, k = (c, kv)); k uniform over the wavefront
+        const int k = k0 + k_row0 + RSTEP * i;
         float v = 0.f;
-        if (a_row_ok && k < kend) {
+        if (k < kend) {
           const uint32_t c = fdiv(uint32_t(k), P.f_KV), kv = uint32_t(k) - c * uint32_t(P.KV);
           const uint32_t kd = fdiv(kv, P.f_KHW), r = kv - kd * uint32_t(KHW);
           const uint32_t kh = fdiv(r, P.f_KW), kw = r - kh * uint32_t(P.KW);
           const int id = a_p0 + int(kd) * P.dd, ih = a_p1 + int(kh) * P.dh, iw = a_p2 + int(kw) * P.dw;
-          if (unsigned(id) < unsigned(P.D) && unsigned(ih) < unsigned(P.H) && unsigned(iw) < unsigned(P.W))
+          if (a_row_ok && unsigned(id) < unsigned(P.D) && unsigned(ih) < unsigned(P.H) && unsigned(iw) < unsigned(P.W))
             v = P.a[a_base + int64_t(c) * P.S + (int64_t(id) * P.H + ih) * P.W + iw];
         }
         ra[i] = v;
       }
       const int k = k0 + kk_k;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {  // B: w[g*Opg + o][k], contiguous along k
+      for (int i = 0; i < NB; ++i) {  // B: w[g*Opg + o][k], contiguous along k
         const int o = n0 + r_k + 16 * i;
         rb[i] = (o < P.NC && k < kend) ? P.b[(int64_t(g) * P.Opg + o) * P.K + k] : 0.f;
       }
     } else if constexpr (MODE == MODE_DGRAD) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {  // A: dy gathered at (m, k = (o, kv))
-        const int k = k0 + wave + 4 * i;
+      for (int i = 0; i < NA; ++i) {  // A: dy at (m, k = (o, kv)); k uniform over the wavefront
+        const int k = k0 + k_row0 + RSTEP * i;
         float v = 0.f;
-        if (a_row_ok && k < kend) {
+        if (k < kend) {
           const uint32_t o = fdiv(uint32_t(k), P.f_KV), kv = uint32_t(k) - o * uint32_t(P.KV);
           const uint32_t kd = fdiv(kv, P.f_KHW), r = kv - kd * uint32_t(KHW);
           const uint32_t kh = fdiv(r, P.f_KW), kw = r - kh * uint32_t(P.KW);
           const int td = a_p0 - int(kd) * P.dd, th = a_p1 - int(kh) * P.dh, tw = a_p2 - int(kw) * P.dw;
-          if (td >= 0 && th >= 0 && tw >= 0) {
+          if (a_row_ok && td >= 0 && th >= 0 && tw >= 0) {
             const uint32_t od = fdiv(uint32_t(td), P.f_sd), oh = fdiv(uint32_t(th), P.f_sh),
                            ow = fdiv(uint32_t(tw), P.f_sw);
             if (od * uint32_t(P.sd) == uint32_t(td) && oh * uint32_t(P.sh) == uint32_t(th) &&
@@ -184,7 +198,7 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
       const uint32_t kc = k_ok ? uint32_t(k) : 0u;
       const uint32_t o = fdiv(kc, P.f_KV), kv = kc - o * uint32_t(P.KV);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {  // B: w[g*Opg + o][c][kv]
+      for (int i = 0; i < NB; ++i) {  // B: w[g*Opg + o][c][kv]
         const int c = n0 + r_k + 16 * i;
         rb[i] = (c < P.NC && k_ok) ? P.b[((int64_t(g) * P.Opg + o) * P.Cpg + c) * P.KV + kv] : 0.f;
       }
@@ -194,7 +208,7 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
       const uint32_t kc = k_ok ? uint32_t(k) : 0u;
       const uint32_t n = fdiv(kc, P.f_oS), sp = kc - n * uint32_t(P.oS);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {  // A: dy[n][g*Opg + o][sp]
+      for (int i = 0; i < NA; ++i) {  // A: dy[n][g*Opg + o][sp]
         const int o = m0 + r_k + 16 * i;
         ra[i] = (o < P.M && k_ok) ? P.a[(int64_t(n) * P.O + int64_t(g) * P.Opg + o) * P.oS + sp] : 0.f;
       }
@@ -202,7 +216,7 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
       const uint32_t oh = fdiv(r, P.f_oW), ow = r - oh * uint32_t(P.oW);
       const int64_t xn = int64_t(n) * P.C * P.S;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {  // B: x gathered at (k = (n, p), j = (c, kv))
+      for (int i = 0; i < NB; ++i) {  // B: x at (k = (n, p), j = (c, kv))
         const int id = int(od) * P.sd + wb_d[i], ih = int(oh) * P.sh + wb_h[i], iw = int(ow) * P.sw + wb_w[i];
         const bool ok = wb_ok[i] && k_ok && unsigned(id) < unsigned(P.D) && unsigned(ih) < unsigned(P.H) &&
                         unsigned(iw) < unsigned(P.W);
@@ -213,18 +227,22 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
   auto commit = [&](int buf) {
     if constexpr (MODE == MODE_WGRAD) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) As[buf][kk_k * CLD + r_k + 16 * i] = ra[i];
+      for (int i = 0; i < NA; ++i) As[buf][kk_k * LDA + r_k + 16 * i] = ra[i];
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) As[buf][(wave + 4 * i) * CLD + lane] = ra[i];
+      for (int i = 0; i < NA; ++i) As[buf][(k_row0 + RSTEP * i) * LDA + r_row] = ra[i];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) Bs[buf][kk_k * CLD + r_k + 16 * i] = rb[i];
+    for (int i = 0; i < NB; ++i) Bs[buf][kk_k * LDB + r_k + 16 * i] = rb[i];
   };
 
-  float16v acc;
+  float16v acc[TM][TN];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = kend > kbeg ? (kend - kbeg + CBK - 1) / CBK : 0;
   if (nk > 0) {
     fetch(kbeg);
@@ -237,37 +255,70 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
 #pragma unroll
     for (int s = 0; s < CBK / 2; ++s) {
       const int k = 2 * s + (lane >> 5);
-      const float af = As[buf][k * CLD + wm * 32 + (lane & 31)];
-      const float bf = Bs[buf][k * CLD + wn * 32 + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af, bf, acc, 0, 0, 0);
+      float af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = As[buf][k * LDA + wm * (BM / 2) + i * 32 + (lane & 31)];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = Bs[buf][k * LDB + wn * (BN / 2) + j * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < nk) commit(buf ^ 1);
     __syncthreads();
   }
 
-  // Lane l holds rows 8*(e/4) + (e%4) + 4*(l/32) and column l%32 of its
-  // wavefront's 32 x 32 tile.
-  const int col = n0 + wn * 32 + (lane & 31);
-  if (col >= P.NC) return;
-  float bz = 0.f;
-  if constexpr (MODE == MODE_FWD) {
-    if (P.bias) bz = P.bias[int64_t(g) * P.Opg + col];
-  } else if constexpr (MODE == MODE_DGRAD) {
-    if (P.bias) bz = P.bias[int64_t(g) * P.Cpg + col];
-  }
+  // Lane l holds rows 8*(e/4) + (e%4) + 4*(l/32) and column l%32 of each
+  // 32 x 32 tile: groups of four consecutive rows, stored as one float4 when
+  // they are contiguous and aligned in the output (spatial size % 4 == 0).
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int row = m0 + wm * 32 + 8 * (e >> 2) + (e & 3) + 4 * (lane >> 5);
-    if (row >= P.M) continue;
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+    if (col >= P.NC) continue;
+    float bz = 0.f;
     if constexpr (MODE == MODE_FWD) {
-      const uint32_t n = fdiv(uint32_t(row), P.f_oS), sp = uint32_t(row) - n * uint32_t(P.oS);
-      P.out[(int64_t(n) * P.O + int64_t(g) * P.Opg + col) * P.oS + sp] = acc[e] + bz;
+      if (P.bias) bz = P.bias[int64_t(g) * P.Opg + col];
     } else if constexpr (MODE == MODE_DGRAD) {
-      const uint32_t n = fdiv(uint32_t(row), P.f_S), sp = uint32_t(row) - n * uint32_t(P.S);
-      P.out[(int64_t(n) * P.C + int64_t(g) * P.Cpg + col) * P.S + sp] = acc[e] + bz;
-    } else {
-      P.out[int64_t(split) * P.part_stride + (int64_t(g) * P.Opg + row) * P.NC + col] = acc[e];
+      if (P.bias) bz = P.bias[int64_t(g) * P.Cpg + col];
     }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = m0 + wm * (BM / 2) + i * 32 + 8 * q + 4 * (lane >> 5);
+        if (row >= P.M) continue;
+        if constexpr (MODE == MODE_WGRAD) {
+          float* dst = P.out + int64_t(split) * P.part_stride + (int64_t(g) * P.Opg + row) * P.NC + col;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (row + e < P.M) dst[int64_t(e) * P.NC] = acc[i][j][4 * q + e];
+        } else {
+          const int spatial = MODE == MODE_FWD ? P.oS : P.S;
+          const int chans = MODE == MODE_FWD ? P.O : P.C;
+          const int cpg = MODE == MODE_FWD ? P.Opg : P.Cpg;
+          const uint32_t n = fdiv(uint32_t(row), MODE == MODE_FWD ? P.f_oS : P.f_S);
+          const uint32_t sp = uint32_t(row) - n * uint32_t(spatial);
+          float* dst = P.out + (int64_t(n) * chans + int64_t(g) * cpg + col) * spatial + sp;
+          const float4 v = make_float4(acc[i][j][4 * q] + bz, acc[i][j][4 * q + 1] + bz,
+                                       acc[i][j][4 * q + 2] + bz, acc[i][j][4 * q + 3] + bz);
+          if ((spatial & 3) == 0 && row + 3 < P.M) {
+            *reinterpret_cast<float4*>(dst) = v;
+          } else {
+            // Rows may cross into the next image: place each one on its own.
+            const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int re = row + e;
+              if (re >= P.M) break;
+              const uint32_t ne = fdiv(uint32_t(re), MODE == MODE_FWD ? P.f_oS : P.f_S);
+              const uint32_t se = uint32_t(re) - ne * uint32_t(spatial);
+              P.out[(int64_t(ne) * chans + int64_t(g) * cpg + col) * spatial + se] = vals[e];
+            }
+          }
+        }
+      }
   }
 }
 
@@ -278,28 +329,56 @@ __global__ void __launch_bounds__(256) conv_split_reduce_kernel(const float* __r
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= total) return;
   float acc = 0.f;
-  for (int s = 0; s < splits; ++s) acc += part[int64_t(s) * total + i];
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = part[int64_t(s + u) * total + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += t[u];
+  }
+  for (; s < splits; ++s) acc += part[int64_t(s) * total + i];
   out[i] = acc;
 }
 
-// db[o] = sum over n and the spatial positions of dy[n][o][.]: one
-// workgroup per channel, a fixed-order LDS tree at the end.
-__global__ void __launch_bounds__(256) conv_bias_grad_kernel(const float* __restrict__ dy, float* __restrict__ db,
-                                                             int64_t n, int64_t o_count, int64_t spatial) {
-  __shared__ float sm[256];
-  const int64_t o = blockIdx.x;
+// part[r] = sum of dy row r (r = n * O + o, `spatial` floats): one
+// wavefront per row, four independent loads in flight per lane.
+__global__ void __launch_bounds__(256) conv_row_sum_kernel(const float* __restrict__ dy, float* __restrict__ part,
+                                                           int64_t rows, int64_t spatial) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* row = dy + r * spatial;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int64_t p = lane;
+  for (; p + 192 < spatial; p += 256) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += row[p + 64 * u];
+  }
+  for (; p < spatial; p += 64) acc[0] += row[p];
+  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (lane == 0) part[r] = s;
+}
+
+// db[o] = sum over n (in order) of part[n * O + o]; eight loads are issued
+// before they are added.
+__global__ void __launch_bounds__(256) conv_bias_final_kernel(const float* __restrict__ part, float* __restrict__ db,
+                                                              int64_t n, int64_t o_count) {
+  const int64_t o = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (o >= o_count) return;
   float acc = 0.f;
-  for (int64_t b = 0; b < n; ++b) {
-    const float* row = dy + (b * o_count + o) * spatial;
-    for (int64_t p = threadIdx.x; p < spatial; p += 256) acc += row[p];
+  int64_t b = 0;
+  for (; b + 8 <= n; b += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = part[(b + u) * o_count + o];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += t[u];
   }
-  sm[threadIdx.x] = acc;
-  __syncthreads();
-  for (int w = 128; w >= 1; w >>= 1) {
-    if (int(threadIdx.x) < w) sm[threadIdx.x] += sm[threadIdx.x + w];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) db[o] = sm[0];
+  for (; b < n; ++b) acc += part[b * o_count + o];
+  db[o] = acc;
 }
 
 }  // namespace
@@ -363,14 +442,19 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   k.f_sd = make_fdiv(uint32_t(k.sd));
   k.f_sh = make_fdiv(uint32_t(k.sh));
   k.f_sw = make_fdiv(uint32_t(k.sw));
-  k.tiles_m = int((k.M + CBM - 1) / CBM);
-  const int64_t tiles_n = (k.NC + CBN - 1) / CBN;
+  // 128-wide tiles where the GEMM is large enough along that side.
+  const int bm = k.M >= 128 ? 128 : 64;
+  const int bn = k.NC >= 128 ? 128 : 64;
+  k.tiles_m = int((k.M + bm - 1) / bm);
+  const int64_t tiles_n = (k.NC + bn - 1) / bn;
   const int64_t tiles = int64_t(k.tiles_m) * tiles_n;
   if (mode == 2) {
-    // Split the (n, p) reduction so that about 2048 workgroups run, each
-    // over at least 8 k-steps; slices are summed in order afterwards.
+    // Split the (n, p) reduction so that about 1024 workgroups run (the
+    // kernel is latency-bound per workgroup), each over at least 8 k-steps,
+    // and at most 64 slices, whose partial sums a second kernel adds in order.
     const int64_t steps = (int64_t(k.K) + CBK - 1) / CBK;
-    int64_t splits = std::max<int64_t>(1, std::min<int64_t>(2048 / std::max<int64_t>(tiles * G, 1), steps / 8));
+    int64_t splits = std::max<int64_t>(1, std::min<int64_t>(1024 / std::max<int64_t>(tiles * G, 1), steps / 8));
+    splits = std::min<int64_t>(splits, 64);
     splits = std::min<int64_t>(splits, 65535 / G);
     const int64_t chunk_steps = (steps + splits - 1) / std::max<int64_t>(splits, 1);
     k.k_chunk = int(std::max<int64_t>(chunk_steps, 1) * CBK);
@@ -385,12 +469,17 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   }
   if (k.M == 0 || k.NC == 0) return;
   const dim3 grid(unsigned(tiles), unsigned(G * k.ksplit));
-  if (mode == 0)
-    dispatch(ctx, conv_gemm_kernel<MODE_FWD>, grid, dim3(256), 0, k);
-  else if (mode == 1)
-    dispatch(ctx, conv_gemm_kernel<MODE_DGRAD>, grid, dim3(256), 0, k);
-  else
-    dispatch(ctx, conv_gemm_kernel<MODE_WGRAD>, grid, dim3(256), 0, k);
+  auto go = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k); };
+  auto pick = [&](auto mode_tag) {
+    constexpr int MD = decltype(mode_tag)::value;
+    if (bm == 128 && bn == 128) go(conv_gemm_kernel<MD, 128, 128>);
+    else if (bm == 128) go(conv_gemm_kernel<MD, 128, 64>);
+    else if (bn == 128) go(conv_gemm_kernel<MD, 64, 128>);
+    else go(conv_gemm_kernel<MD, 64, 64>);
+  };
+  if (mode == 0) pick(std::integral_constant<int, MODE_FWD>{});
+  else if (mode == 1) pick(std::integral_constant<int, MODE_DGRAD>{});
+  else pick(std::integral_constant<int, MODE_WGRAD>{});
   if (mode == 2 && k.ksplit > 1) {
     const int64_t total = k.part_stride;
     dispatch(ctx, conv_split_reduce_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, k.out, out, total,
@@ -401,7 +490,10 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
 
 void launch_conv_bias_grad(bg_ctx* ctx, const float* dy, float* out, int64_t n, int64_t o, int64_t spatial) {
   if (o == 0) return;
-  dispatch(ctx, conv_bias_grad_kernel, dim3(unsigned(o)), dim3(256), 0, dy, out, n, o, spatial);
+  const int64_t rows = n * o;
+  float* part = static_cast<float*>(scratch(ctx, size_t(rows) * 4, 0));
+  dispatch(ctx, conv_row_sum_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, dy, part, rows, spatial);
+  dispatch(ctx, conv_bias_final_kernel, dim3(unsigned((o + 255) / 256)), dim3(256), 0, part, out, n, o);
   hip_check(hipGetLastError(), "conv bias-gradient launch");
 }
 

@@ -67,7 +67,7 @@ struct ConvK {
   FDiv f_oS, f_oHW, f_oW, f_S, f_HW, f_W, f_KV, f_KHW, f_KW, f_sd, f_sh, f_sw;
 };
 
-constexpr int CBK = 16;
+constexpr int CBK = 16;  // k-step of every tile; WGRAD slices are multiples of it
 
 // Workgroup tile BM x BN (64 or 128 each), four wavefronts in a 2 x 2 grid,
 // each holding (BM/2) x (BN/2) as TM x TN MFMA 32 x 32 accumulators.
@@ -76,14 +76,15 @@ constexpr int CBK = 16;
 // Two load mappings: "row-mapped" (FWD / DGRAD A) gives thread t the fixed
 // row t % BM and the k offsets t / BM + (256 / BM) * i, which are uniform
 // over a wavefront, so the k decomposition runs on the scalar unit;
-// "k-mapped" (the other operands) gives the fixed k offset t % 16 and the
-// rows t / 16 + 16 * i.
+// "k-mapped" (the other operands) gives the fixed k offset t % BK and the
+// rows t / BK + (256 / BK) * i.
 template <int MODE, int BM, int BN>
 __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
   constexpr int LDA = BM + 1, LDB = BN + 1;
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr int NA = BM * CBK / 256, NB = BN * CBK / 256;
-  constexpr int RSTEP = 256 / BM;  // row-mapped k stride
+  constexpr int RSTEP = 256 / BM;   // row-mapped k stride
+  constexpr int KROWS = 256 / CBK;  // k-mapped row stride
   __shared__ float As[2][CBK * LDA];
   __shared__ float Bs[2][CBK * LDB];
   const int tid = threadIdx.x;
@@ -100,8 +101,8 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
 
   const int r_row = tid % BM;                                   // row-mapped row
   const int k_row0 = __builtin_amdgcn_readfirstlane(tid / BM);  // row-mapped first k offset
-  const int kk_k = tid & 15;                                    // k-mapped k offset
-  const int r_k = tid >> 4;                                     // k-mapped first row
+  const int kk_k = tid % CBK;                                   // k-mapped k offset
+  const int r_k = tid / CBK;                                    // k-mapped first row
 
   // FWD / DGRAD A: this thread's output (FWD) or input (DGRAD) position.
   int64_t a_base = 0;
@@ -136,7 +137,7 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
   if constexpr (MODE == MODE_WGRAD) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int j = n0 + r_k + 16 * i;
+      const int j = n0 + r_k + KROWS * i;
       wb_ok[i] = j < P.NC;
       const uint32_t jj = wb_ok[i] ? uint32_t(j) : 0u;
       const uint32_t c = fdiv(jj, P.f_KV), kv = jj - c * uint32_t(P.KV);
@@ -154,44 +155,49 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
     if constexpr (MODE == MODE_FWD) {
 #pragma unroll
       for (int i = 0; i < NA; ++i) {  // A: x at (m, k = (c, kv)); k uniform over the wavefront
+        // Branch-free: every lane loads (out-of-range taps from the group's
+        // first element, always in bounds) and zeroes what lies outside.
         const int k = k0 + k_row0 + RSTEP * i;
-        float v = 0.f;
-        if (k < kend) {
-          const uint32_t c = fdiv(uint32_t(k), P.f_KV), kv = uint32_t(k) - c * uint32_t(P.KV);
-          const uint32_t kd = fdiv(kv, P.f_KHW), r = kv - kd * uint32_t(KHW);
-          const uint32_t kh = fdiv(r, P.f_KW), kw = r - kh * uint32_t(P.KW);
-          const int id = a_p0 + int(kd) * P.dd, ih = a_p1 + int(kh) * P.dh, iw = a_p2 + int(kw) * P.dw;
-          if (a_row_ok && unsigned(id) < unsigned(P.D) && unsigned(ih) < unsigned(P.H) && unsigned(iw) < unsigned(P.W))
-            v = P.a[a_base + int64_t(c) * P.S + (int64_t(id) * P.H + ih) * P.W + iw];
-        }
-        ra[i] = v;
+        const bool k_ok = k < kend;
+        const uint32_t kc = k_ok ? uint32_t(k) : 0u;
+        const uint32_t c = fdiv(kc, P.f_KV), kv = kc - c * uint32_t(P.KV);
+        const uint32_t kd = fdiv(kv, P.f_KHW), r = kv - kd * uint32_t(KHW);
+        const uint32_t kh = fdiv(r, P.f_KW), kw = r - kh * uint32_t(P.KW);
+        const int id = a_p0 + int(kd) * P.dd, ih = a_p1 + int(kh) * P.dh, iw = a_p2 + int(kw) * P.dw;
+        const bool ok = k_ok && a_row_ok && unsigned(id) < unsigned(P.D) && unsigned(ih) < unsigned(P.H) &&
+                        unsigned(iw) < unsigned(P.W);
+        const int64_t off = ok ? int64_t(c) * P.S + (int64_t(id) * P.H + ih) * P.W + iw : 0;
+        const float t = P.a[a_base + off];
+        ra[i] = ok ? t : 0.f;
       }
       const int k = k0 + kk_k;
 #pragma unroll
       for (int i = 0; i < NB; ++i) {  // B: w[g*Opg + o][k], contiguous along k
-        const int o = n0 + r_k + 16 * i;
-        rb[i] = (o < P.NC && k < kend) ? P.b[(int64_t(g) * P.Opg + o) * P.K + k] : 0.f;
+        const int o = n0 + r_k + KROWS * i;
+        const bool ok = o < P.NC && k < kend;
+        const float t = P.b[ok ? (int64_t(g) * P.Opg + o) * P.K + k : 0];
+        rb[i] = ok ? t : 0.f;
       }
     } else if constexpr (MODE == MODE_DGRAD) {
 #pragma unroll
       for (int i = 0; i < NA; ++i) {  // A: dy at (m, k = (o, kv)); k uniform over the wavefront
-        const int k = k0 + k_row0 + RSTEP * i;
-        float v = 0.f;
-        if (k < kend) {
-          const uint32_t o = fdiv(uint32_t(k), P.f_KV), kv = uint32_t(k) - o * uint32_t(P.KV);
-          const uint32_t kd = fdiv(kv, P.f_KHW), r = kv - kd * uint32_t(KHW);
-          const uint32_t kh = fdiv(r, P.f_KW), kw = r - kh * uint32_t(P.KW);
-          const int td = a_p0 - int(kd) * P.dd, th = a_p1 - int(kh) * P.dh, tw = a_p2 - int(kw) * P.dw;
-          if (a_row_ok && td >= 0 && th >= 0 && tw >= 0) {
-            const uint32_t od = fdiv(uint32_t(td), P.f_sd), oh = fdiv(uint32_t(th), P.f_sh),
-                           ow = fdiv(uint32_t(tw), P.f_sw);
-            if (od * uint32_t(P.sd) == uint32_t(td) && oh * uint32_t(P.sh) == uint32_t(th) &&
-                ow * uint32_t(P.sw) == uint32_t(tw) && od < uint32_t(P.oD) && oh < uint32_t(P.oH) &&
-                ow < uint32_t(P.oW))
-              v = P.a[a_base + int64_t(o) * P.oS + (int64_t(od) * P.oH + oh) * P.oW + ow];
-          }
-        }
-        ra[i] = v;
+        const int k = k0 + k_row0 + RSTEP * i;  // branch-free as in FWD
+        const bool k_ok = k < kend;
+        const uint32_t kc = k_ok ? uint32_t(k) : 0u;
+        const uint32_t o = fdiv(kc, P.f_KV), kv = kc - o * uint32_t(P.KV);
+        const uint32_t kd = fdiv(kv, P.f_KHW), r = kv - kd * uint32_t(KHW);
+        const uint32_t kh = fdiv(r, P.f_KW), kw = r - kh * uint32_t(P.KW);
+        const int td = a_p0 - int(kd) * P.dd, th = a_p1 - int(kh) * P.dh, tw = a_p2 - int(kw) * P.dw;
+        const bool nonneg = td >= 0 && th >= 0 && tw >= 0;
+        const uint32_t ud = nonneg ? uint32_t(td) : 0u, uh = nonneg ? uint32_t(th) : 0u,
+                       uw = nonneg ? uint32_t(tw) : 0u;
+        const uint32_t od = fdiv(ud, P.f_sd), oh = fdiv(uh, P.f_sh), ow = fdiv(uw, P.f_sw);
+        const bool ok = k_ok && a_row_ok && nonneg && od * uint32_t(P.sd) == ud && oh * uint32_t(P.sh) == uh &&
+                        ow * uint32_t(P.sw) == uw && od < uint32_t(P.oD) && oh < uint32_t(P.oH) &&
+                        ow < uint32_t(P.oW);
+        const int64_t off = ok ? int64_t(o) * P.oS + (int64_t(od) * P.oH + oh) * P.oW + ow : 0;
+        const float t = P.a[a_base + off];
+        ra[i] = ok ? t : 0.f;
       }
       const int k = k0 + kk_k;
       const bool k_ok = k < kend;
@@ -199,8 +205,10 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
       const uint32_t o = fdiv(kc, P.f_KV), kv = kc - o * uint32_t(P.KV);
 #pragma unroll
       for (int i = 0; i < NB; ++i) {  // B: w[g*Opg + o][c][kv]
-        const int c = n0 + r_k + 16 * i;
-        rb[i] = (c < P.NC && k_ok) ? P.b[((int64_t(g) * P.Opg + o) * P.Cpg + c) * P.KV + kv] : 0.f;
+        const int c = n0 + r_k + KROWS * i;
+        const bool ok = c < P.NC && k_ok;
+        const float t = P.b[ok ? ((int64_t(g) * P.Opg + o) * P.Cpg + c) * P.KV + kv : 0];
+        rb[i] = ok ? t : 0.f;
       }
     } else {
       const int k = k0 + kk_k;
@@ -209,8 +217,10 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
       const uint32_t n = fdiv(kc, P.f_oS), sp = kc - n * uint32_t(P.oS);
 #pragma unroll
       for (int i = 0; i < NA; ++i) {  // A: dy[n][g*Opg + o][sp]
-        const int o = m0 + r_k + 16 * i;
-        ra[i] = (o < P.M && k_ok) ? P.a[(int64_t(n) * P.O + int64_t(g) * P.Opg + o) * P.oS + sp] : 0.f;
+        const int o = m0 + r_k + KROWS * i;
+        const bool ok = o < P.M && k_ok;
+        const float t = P.a[ok ? (int64_t(n) * P.O + int64_t(g) * P.Opg + o) * P.oS + sp : 0];
+        ra[i] = ok ? t : 0.f;
       }
       const uint32_t od = fdiv(sp, P.f_oHW), r = sp - od * uint32_t(oHW);
       const uint32_t oh = fdiv(r, P.f_oW), ow = r - oh * uint32_t(P.oW);
@@ -220,20 +230,21 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
         const int id = int(od) * P.sd + wb_d[i], ih = int(oh) * P.sh + wb_h[i], iw = int(ow) * P.sw + wb_w[i];
         const bool ok = wb_ok[i] && k_ok && unsigned(id) < unsigned(P.D) && unsigned(ih) < unsigned(P.H) &&
                         unsigned(iw) < unsigned(P.W);
-        rb[i] = ok ? P.b[xn + wb_chan[i] + (int64_t(id) * P.H + ih) * P.W + iw] : 0.f;
+        const float t = P.b[ok ? xn + wb_chan[i] + (int64_t(id) * P.H + ih) * P.W + iw : 0];
+        rb[i] = ok ? t : 0.f;
       }
     }
   };
   auto commit = [&](int buf) {
     if constexpr (MODE == MODE_WGRAD) {
 #pragma unroll
-      for (int i = 0; i < NA; ++i) As[buf][kk_k * LDA + r_k + 16 * i] = ra[i];
+      for (int i = 0; i < NA; ++i) As[buf][kk_k * LDA + r_k + KROWS * i] = ra[i];
     } else {
 #pragma unroll
       for (int i = 0; i < NA; ++i) As[buf][(k_row0 + RSTEP * i) * LDA + r_row] = ra[i];
     }
 #pragma unroll
-    for (int i = 0; i < NB; ++i) Bs[buf][kk_k * LDB + r_k + 16 * i] = rb[i];
+    for (int i = 0; i < NB; ++i) Bs[buf][kk_k * LDB + r_k + KROWS * i] = rb[i];
   };
 
   float16v acc[TM][TN];
@@ -442,9 +453,12 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   k.f_sd = make_fdiv(uint32_t(k.sd));
   k.f_sh = make_fdiv(uint32_t(k.sh));
   k.f_sw = make_fdiv(uint32_t(k.sw));
-  // 128-wide tiles where the GEMM is large enough along that side.
-  const int bm = k.M >= 128 ? 128 : 64;
-  const int bn = k.NC >= 128 ? 128 : 64;
+  // 128-wide tiles where the GEMM is large enough along that side and they
+  // still give 512 workgroups; otherwise 64-wide ones (more workgroups in
+  // flight: these kernels are bound by latency, not by the matrix core).
+  int bm = k.M >= 128 ? 128 : 64;
+  int bn = k.NC >= 128 ? 128 : 64;
+  if (mode != 2 && ((k.M + bm - 1) / bm) * int64_t((k.NC + bn - 1) / bn) * G < 512) bm = bn = 64;
   k.tiles_m = int((k.M + bm - 1) / bm);
   const int64_t tiles_n = (k.NC + bn - 1) / bn;
   const int64_t tiles = int64_t(k.tiles_m) * tiles_n;

@@ -293,10 +293,12 @@ struct OptimConsts {
   float c1;      // f32(1 - beta1^step), in double
   float c2;      // f32(1 - beta2^step), in double
   int has_wd;    // weight_decay != 0 (the oracle skips the term otherwise)
+  // Fused AdamW step only: the M and V steps' own betas.
+  float mb1, momb1, vb2, vomb2;
 };
 
 constexpr int optim_arity(int kind) {
-  return kind == BG_OPT_ADAMW_PARAM ? 4 : (kind >= BG_OPT_ADAM_M ? 3 : 2);
+  return kind == BG_OPT_ADAMW_PARAM || kind == bg::kOptAdamwFused ? 4 : (kind >= BG_OPT_ADAM_M ? 3 : 2);
 }
 
 // One element of each update, in the oracle's operation order; v holds the
@@ -324,10 +326,17 @@ __device__ __forceinline__ float optim_val(const OptimConsts& k, const float (&v
     float g = v[1];
     if (k.has_wd) g = g + k.wd * v[0];
     return k.b2 * v[2] + k.omb2 * (g * g);
-  } else {  // BG_OPT_ADAM_PARAM: param, m_new, v_new
+  } else if constexpr (KIND == BG_OPT_ADAM_PARAM) {  // param, m_new, v_new
     const float mh = v[1] / k.c1;
     const float vh = v[2] / k.c2;
     return v[0] - k.lr * (mh / (sqrtf(vh) + k.eps));
+  } else {  // kOptAdamwFused: param, grad, m, v -> the ADAMW_UPDATE_M, _V and _PARAM chain
+    const float m_new = k.mb1 * v[2] + k.momb1 * v[1];
+    const float v_new = k.vb2 * v[3] + k.vomb2 * (v[1] * v[1]);
+    const float mh = m_new / k.c1;
+    const float vh = v_new / k.c2;
+    const float u = mh / (sqrtf(vh) + k.eps);
+    return (v[0] - k.lr * u) - k.lr_wd * v[0];
   }
 }
 
@@ -466,9 +475,23 @@ void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float
   hip_check(hipGetLastError(), "layer_norm_backward column launch");
 }
 
-void launch_optimizer(bg_ctx* ctx, int kind, const bg_optim_args& a, const float* const (&in)[4], float* out,
-                      int64_t n) {
+static OptimConsts optim_consts(const bg_optim_args& a);
+
+void launch_optimizer_fused(bg_ctx* ctx, const bg_optim_args& a, double m_beta1, double v_beta2,
+                            const float* const (&in)[4], float* out, int64_t n) {
   if (n == 0) return;
+  OptimConsts k = optim_consts(a);
+  k.mb1 = float(m_beta1);
+  k.momb1 = float(1.0 - m_beta1);
+  k.vb2 = float(v_beta2);
+  k.vomb2 = float(1.0 - v_beta2);
+  bool vec = reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  for (const float* p : in) vec = vec && reinterpret_cast<uintptr_t>(p) % 16 == 0;
+  launch_optim_kind<kOptAdamwFused>(ctx, k, in, out, n, vec);
+  hip_check(hipGetLastError(), "optimizer_update launch");
+}
+
+static OptimConsts optim_consts(const bg_optim_args& a) {
   OptimConsts k{};
   k.lr = float(a.lr);
   k.b1 = float(a.beta1);
@@ -481,6 +504,13 @@ void launch_optimizer(bg_ctx* ctx, int kind, const bg_optim_args& a, const float
   k.c1 = float(1.0 - std::pow(a.beta1, double(a.step)));
   k.c2 = float(1.0 - std::pow(a.beta2, double(a.step)));
   k.has_wd = a.weight_decay != 0.0;
+  return k;
+}
+
+void launch_optimizer(bg_ctx* ctx, int kind, const bg_optim_args& a, const float* const (&in)[4], float* out,
+                      int64_t n) {
+  if (n == 0) return;
+  OptimConsts k = optim_consts(a);
   bool vec = reinterpret_cast<uintptr_t>(out) % 16 == 0;
   for (const float* p : in) vec = vec && (p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0);
   switch (kind) {

@@ -255,6 +255,9 @@ struct Step {
   std::vector<int64_t> shape;
   std::string dtype;
   const JVal* arg = nullptr;  // may be null / JSON null
+  // Fused AdamW step (fuse_adamw): the absorbed M and V steps' args.
+  const JVal* arg_m = nullptr;
+  const JVal* arg_v = nullptr;
 };
 
 struct Plan {
@@ -693,6 +696,46 @@ ConvArg conv_arg(const Step& s, const ConvStep& c) {
   return a;
 }
 
+// ---- plan-level fusion --------------------------------------------------------
+
+const char* const kAdamwFused = "ADAMW_UPDATE_M+V+PARAM";
+
+// An ADAMW_UPDATE_PARAM step whose m and v inputs come from ADAMW_UPDATE_M and
+// ADAMW_UPDATE_V steps over the same gradient, read by nothing else and not
+// the root, becomes one step over (param, grad, m, v): one pass reading 16 B
+// and writing 4 B per parameter instead of three passes moving 44 B, with the
+// same float32 operations in the same order.
+void fuse_adamw(Plan& plan) {
+  std::unordered_map<int64_t, int> uses;
+  std::unordered_map<int64_t, size_t> producer;
+  for (size_t i = 0; i < plan.steps.size(); ++i) {
+    for (int64_t in : plan.steps[i].inputs) uses[in]++;
+    producer[plan.steps[i].value_id] = i;
+  }
+  std::vector<bool> drop(plan.steps.size(), false);
+  for (Step& p : plan.steps) {
+    if (p.op != "ADAMW_UPDATE_PARAM" || p.inputs.size() != 4) continue;
+    const int64_t grad = p.inputs[1], m_id = p.inputs[2], v_id = p.inputs[3];
+    if (m_id == plan.root_id || v_id == plan.root_id || uses[m_id] != 1 || uses[v_id] != 1) continue;
+    auto pm = producer.find(m_id), pv = producer.find(v_id);
+    if (pm == producer.end() || pv == producer.end()) continue;
+    const Step& sm = plan.steps[pm->second];
+    const Step& sv = plan.steps[pv->second];
+    if (sm.op != "ADAMW_UPDATE_M" || sv.op != "ADAMW_UPDATE_V" || sm.inputs.size() != 2 ||
+        sv.inputs.size() != 2 || sm.inputs[1] != grad || sv.inputs[1] != grad)
+      continue;
+    p.arg_m = sm.arg;
+    p.arg_v = sv.arg;
+    p.inputs = {p.inputs[0], grad, sm.inputs[0], sv.inputs[0]};
+    p.op = kAdamwFused;
+    drop[pm->second] = drop[pv->second] = true;
+  }
+  std::vector<Step> kept;
+  for (size_t i = 0; i < plan.steps.size(); ++i)
+    if (!drop[i]) kept.push_back(std::move(plan.steps[i]));
+  plan.steps = std::move(kept);
+}
+
 // ---- execution -------------------------------------------------------------
 
 struct Runner {
@@ -1038,6 +1081,36 @@ struct Runner {
       ctx->handles[out].shape = s.shape;
       return own(out);
     }
+    if (op == kAdamwFused) {
+      // The absorbed steps' argument and shape rules, in their order.
+      Step sm = s, sv = s, sp = s;
+      sm.op = "ADAMW_UPDATE_M";
+      sm.arg = s.arg_m;
+      sv.op = "ADAMW_UPDATE_V";
+      sv.arg = s.arg_v;
+      sp.op = "ADAMW_UPDATE_PARAM";
+      const bg_optim_args am = optim_arg(sm, BG_OPT_ADAMW_M);
+      const bg_optim_args av = optim_arg(sv, BG_OPT_ADAMW_V);
+      const bg_optim_args ap = optim_arg(sp, BG_OPT_ADAMW_PARAM);
+      if (dt != BG_F32) fail(BG_E_DTYPE, "tensor plan ADAMW_UPDATE_PARAM supports float32 only");
+      static const char* roles[4] = {"ADAMW_UPDATE_PARAM.param", "ADAMW_UPDATE_PARAM.grad", "ADAMW_UPDATE_M.m",
+                                     "ADAMW_UPDATE_V.v"};
+      const float* in[4];
+      for (int i = 0; i < 4; ++i) {
+        const Record& r = rec(need(s, size_t(i)));
+        expect_shape(r.shape, s.shape, roles[i]);
+        if (r.dtype != BG_F32) fail(BG_E_DTYPE, std::string("tensor plan ") + roles[i] + " must be float32");
+        in[i] = reinterpret_cast<const float*>(r.ptr());
+      }
+      const int64_t n = numel(s.shape);
+      bg_handle out = mint(ctx, size_t(n) * 4, s.shape, BG_F32);
+      float* po = reinterpret_cast<float*>(ctx->handles[out].ptr());
+      {
+        Profile prof(ctx, "adamw_update_fused", n * 20, 0);
+        launch_optimizer_fused(ctx, ap, am.beta1, av.beta2, in, po, n);
+      }
+      return own(out);
+    }
     if (const int kind = optim_kind(op); kind >= 0) {
       // tensor_plan.ts:663-702 (lowering), :2926-3113 (shape rules),
       // :3776-3827 (arguments)
@@ -1170,6 +1243,7 @@ bg_handle run_plan(bg_ctx* ctx, const char* json, const char* requests_json, con
     fail(BG_E_DTYPE, "run_tensor_plan: dtype not supported");
   JVal doc = JsonReader(json, "tensor plan").parse();
   Plan plan = normalize(doc);
+  fuse_adamw(plan);
   std::unordered_map<int64_t, std::vector<int64_t>> sem;
   if (requests_json) sem = bind_requests(plan, parse_requests(requests_json));
 

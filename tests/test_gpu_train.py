@@ -387,3 +387,42 @@ def test_plan_argument_rules(bridge):
                                {"normalizedShape": [3], "rows": 2, "cols": 3}), lnin)
     ref = O.layer_norm_backward_input(LN_DY, LN_X, LN_W, 1e-5).ravel()
     assert O.within(dx, ref, TOL32).all()
+
+
+def test_plan_adamw_param_root_fused_matches_unfused(bridge, rng):
+    """A PARAM root whose M and V inputs are read by nothing else runs as one
+    fused pass; its result equals the three-step chain bit for bit, and a
+    plan where M has a second reader (no fusion) gives the same bytes."""
+    n = (1 << 20) + 3
+    p, g, m0 = (rng.standard_normal(n).astype(F32) for _ in range(3))
+    v0 = (np.abs(rng.standard_normal(n)) * 0.01).astype(F32)
+    arg = {"lr": 3e-4, "beta1": 0.9, "beta2": 0.95, "eps": 1e-8, "weight_decay": 0.1, "step": 12}
+    ins = [p, g, m0, v0]
+
+    def plan(extra_reader):
+        steps = [_buf(i, [n]) for i in range(4)] + [_load(4 + i, i, [n]) for i in range(4)]
+        steps.append({"step": 8, "value_id": 8, "op": "ADAMW_UPDATE_M", "input_ids": [6, 5], "shape": [n],
+                      "dtype": "float32", "arg": arg})
+        steps.append({"step": 9, "value_id": 9, "op": "ADAMW_UPDATE_V", "input_ids": [7, 5], "shape": [n],
+                      "dtype": "float32", "arg": arg})
+        root = 10
+        if extra_reader:  # a dead second reader of M keeps the chain unfused
+            steps.append({"step": 10, "value_id": 10, "op": "ADD", "input_ids": [8, 8], "shape": [n],
+                          "dtype": "float32"})
+            root = 11
+        steps.append({"step": root, "value_id": root, "op": "ADAMW_UPDATE_PARAM", "input_ids": [4, 5, 8, 9],
+                      "shape": [n], "dtype": "float32", "arg": arg})
+        return _plan(steps, root)
+
+    bridge.flushProfiles()
+    fused = _run(bridge, plan(False), ins)
+    labels = [q["label"] for q in bridge.flushProfiles()["passProfiles"]]
+    unfused = _run(bridge, plan(True), ins)
+    labels2 = [q["label"] for q in bridge.flushProfiles()["passProfiles"]]
+    em = O.adamw_update_m(m0, g, 0.9)
+    ev = O.adamw_update_v(v0, g, 0.95)
+    ep = O.adamw_update_param(p, em, ev, 3e-4, 0.9, 0.95, 1e-8, 12, 0.1)
+    assert np.array_equal(fused, ep) and np.array_equal(unfused, ep)
+    if bridge.profiling:
+        assert "adamw_update_fused" in labels and "adamw_update_m" not in labels
+        assert "adamw_update_fused" not in labels2 and "adamw_update_m" in labels2

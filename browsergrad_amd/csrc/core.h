@@ -177,11 +177,14 @@ void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, cons
 // Column sums over rows of dy * x_hat (weight) or dy (bias, x unused).
 void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float* out, int64_t rows, int64_t cols,
                              float eps, bool weight);
-// Internal optimizer kind: ADAMW_UPDATE_M, _V and _PARAM as one pass over
-// (param, grad, m, v), the plan executor's fusion of that chain.
+// Internal optimizer kinds: ADAMW_UPDATE_M, _V and _PARAM (or the ADAM_
+// chain) as one pass over (param, grad, m, v), the plan executor's fusion of
+// those chains.  `a` is the PARAM step's arguments; m_beta1 / v_beta2 (and,
+// for Adam, the decays m_wd / v_wd) come from the M and V steps.
 constexpr int kOptAdamwFused = 7;
-void launch_optimizer_fused(bg_ctx* ctx, const bg_optim_args& a, double m_beta1, double v_beta2,
-                            const float* const (&in)[4], float* out, int64_t n);
+constexpr int kOptAdamFused = 8;
+void launch_optimizer_fused(bg_ctx* ctx, int kind, const bg_optim_args& a, double m_beta1, double v_beta2,
+                            double m_wd, double v_wd, const float* const (&in)[4], float* out, int64_t n);
 // in[] holds the kind's inputs in bg_optimizer_update order (unused slots NULL).
 void launch_optimizer(bg_ctx* ctx, int kind, const bg_optim_args& a, const float* const (&in)[4], float* out,
                       int64_t n);

@@ -293,12 +293,15 @@ struct OptimConsts {
   float c1;      // f32(1 - beta1^step), in double
   float c2;      // f32(1 - beta2^step), in double
   int has_wd;    // weight_decay != 0 (the oracle skips the term otherwise)
-  // Fused AdamW step only: the M and V steps' own betas.
+  // Fused steps only: the M and V steps' own betas (and Adam's decays).
   float mb1, momb1, vb2, vomb2;
+  float mwd, vwd;
 };
 
 constexpr int optim_arity(int kind) {
-  return kind == BG_OPT_ADAMW_PARAM || kind == bg::kOptAdamwFused ? 4 : (kind >= BG_OPT_ADAM_M ? 3 : 2);
+  return kind == BG_OPT_ADAMW_PARAM || kind == bg::kOptAdamwFused || kind == bg::kOptAdamFused
+             ? 4
+             : (kind >= BG_OPT_ADAM_M ? 3 : 2);
 }
 
 // One element of each update, in the oracle's operation order; v holds the
@@ -329,6 +332,14 @@ __device__ __forceinline__ float optim_val(const OptimConsts& k, const float (&v
   } else if constexpr (KIND == BG_OPT_ADAM_PARAM) {  // param, m_new, v_new
     const float mh = v[1] / k.c1;
     const float vh = v[2] / k.c2;
+    return v[0] - k.lr * (mh / (sqrtf(vh) + k.eps));
+  } else if constexpr (KIND == bg::kOptAdamFused) {  // param, grad, m, v -> ADAM_UPDATE_M, _V, _PARAM
+    const float gm = k.mwd != 0.f ? v[1] + k.mwd * v[0] : v[1];
+    const float gv = k.vwd != 0.f ? v[1] + k.vwd * v[0] : v[1];
+    const float m_new = k.mb1 * v[2] + k.momb1 * gm;
+    const float v_new = k.vb2 * v[3] + k.vomb2 * (gv * gv);
+    const float mh = m_new / k.c1;
+    const float vh = v_new / k.c2;
     return v[0] - k.lr * (mh / (sqrtf(vh) + k.eps));
   } else {  // kOptAdamwFused: param, grad, m, v -> the ADAMW_UPDATE_M, _V and _PARAM chain
     const float m_new = k.mb1 * v[2] + k.momb1 * v[1];
@@ -477,17 +488,22 @@ void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float
 
 static OptimConsts optim_consts(const bg_optim_args& a);
 
-void launch_optimizer_fused(bg_ctx* ctx, const bg_optim_args& a, double m_beta1, double v_beta2,
-                            const float* const (&in)[4], float* out, int64_t n) {
+void launch_optimizer_fused(bg_ctx* ctx, int kind, const bg_optim_args& a, double m_beta1, double v_beta2,
+                            double m_wd, double v_wd, const float* const (&in)[4], float* out, int64_t n) {
   if (n == 0) return;
   OptimConsts k = optim_consts(a);
   k.mb1 = float(m_beta1);
   k.momb1 = float(1.0 - m_beta1);
   k.vb2 = float(v_beta2);
   k.vomb2 = float(1.0 - v_beta2);
+  // Adam folds each moment step's weight decay into that step's gradient
+  // (f32(wd) is nonzero exactly when wd is, for the finite wd accepted).
+  k.mwd = kind == kOptAdamFused ? float(m_wd) : 0.f;
+  k.vwd = kind == kOptAdamFused ? float(v_wd) : 0.f;
   bool vec = reinterpret_cast<uintptr_t>(out) % 16 == 0;
   for (const float* p : in) vec = vec && reinterpret_cast<uintptr_t>(p) % 16 == 0;
-  launch_optim_kind<kOptAdamwFused>(ctx, k, in, out, n, vec);
+  if (kind == kOptAdamFused) launch_optim_kind<kOptAdamFused>(ctx, k, in, out, n, vec);
+  else launch_optim_kind<kOptAdamwFused>(ctx, k, in, out, n, vec);
   hip_check(hipGetLastError(), "optimizer_update launch");
 }
 

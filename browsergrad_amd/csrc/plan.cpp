@@ -699,6 +699,7 @@ ConvArg conv_arg(const Step& s, const ConvStep& c) {
 // ---- plan-level fusion --------------------------------------------------------
 
 const char* const kAdamwFused = "ADAMW_UPDATE_M+V+PARAM";
+const char* const kAdamFused = "ADAM_UPDATE_M+V+PARAM";
 
 // An ADAMW_UPDATE_PARAM step whose m and v inputs come from ADAMW_UPDATE_M and
 // ADAMW_UPDATE_V steps over the same gradient, read by nothing else and not
@@ -714,6 +715,25 @@ void fuse_adamw(Plan& plan) {
   }
   std::vector<bool> drop(plan.steps.size(), false);
   for (Step& p : plan.steps) {
+    if (p.op == "ADAM_UPDATE_PARAM" && p.inputs.size() == 3) {
+      // Adam: M and V read (param, grad, moment); PARAM reads (param, m', v').
+      const int64_t param = p.inputs[0], m_id = p.inputs[1], v_id = p.inputs[2];
+      if (m_id == plan.root_id || v_id == plan.root_id || uses[m_id] != 1 || uses[v_id] != 1) continue;
+      auto pm = producer.find(m_id), pv = producer.find(v_id);
+      if (pm == producer.end() || pv == producer.end()) continue;
+      const Step& sm = plan.steps[pm->second];
+      const Step& sv = plan.steps[pv->second];
+      if (sm.op != "ADAM_UPDATE_M" || sv.op != "ADAM_UPDATE_V" || sm.inputs.size() != 3 ||
+          sv.inputs.size() != 3 || sm.inputs[0] != param || sv.inputs[0] != param ||
+          sm.inputs[1] != sv.inputs[1])
+        continue;
+      p.arg_m = sm.arg;
+      p.arg_v = sv.arg;
+      p.inputs = {param, sm.inputs[1], sm.inputs[2], sv.inputs[2]};
+      p.op = kAdamFused;
+      drop[pm->second] = drop[pv->second] = true;
+      continue;
+    }
     if (p.op != "ADAMW_UPDATE_PARAM" || p.inputs.size() != 4) continue;
     const int64_t grad = p.inputs[1], m_id = p.inputs[2], v_id = p.inputs[3];
     if (m_id == plan.root_id || v_id == plan.root_id || uses[m_id] != 1 || uses[v_id] != 1) continue;
@@ -1081,20 +1101,22 @@ struct Runner {
       ctx->handles[out].shape = s.shape;
       return own(out);
     }
-    if (op == kAdamwFused) {
+    if (op == kAdamwFused || op == kAdamFused) {
       // The absorbed steps' argument and shape rules, in their order.
+      const bool adamw = op == kAdamwFused;
+      const std::string fam = adamw ? "ADAMW_UPDATE_" : "ADAM_UPDATE_";
       Step sm = s, sv = s, sp = s;
-      sm.op = "ADAMW_UPDATE_M";
+      sm.op = fam + "M";
       sm.arg = s.arg_m;
-      sv.op = "ADAMW_UPDATE_V";
+      sv.op = fam + "V";
       sv.arg = s.arg_v;
-      sp.op = "ADAMW_UPDATE_PARAM";
-      const bg_optim_args am = optim_arg(sm, BG_OPT_ADAMW_M);
-      const bg_optim_args av = optim_arg(sv, BG_OPT_ADAMW_V);
-      const bg_optim_args ap = optim_arg(sp, BG_OPT_ADAMW_PARAM);
-      if (dt != BG_F32) fail(BG_E_DTYPE, "tensor plan ADAMW_UPDATE_PARAM supports float32 only");
-      static const char* roles[4] = {"ADAMW_UPDATE_PARAM.param", "ADAMW_UPDATE_PARAM.grad", "ADAMW_UPDATE_M.m",
-                                     "ADAMW_UPDATE_V.v"};
+      sp.op = fam + "PARAM";
+      const bg_optim_args am = optim_arg(sm, adamw ? BG_OPT_ADAMW_M : BG_OPT_ADAM_M);
+      const bg_optim_args av = optim_arg(sv, adamw ? BG_OPT_ADAMW_V : BG_OPT_ADAM_V);
+      const bg_optim_args ap = optim_arg(sp, adamw ? BG_OPT_ADAMW_PARAM : BG_OPT_ADAM_PARAM);
+      if (dt != BG_F32) fail(BG_E_DTYPE, "tensor plan " + sp.op + " supports float32 only");
+      const std::string r0 = sp.op + ".param", r1 = sm.op + ".grad", r2 = sm.op + ".m", r3 = sv.op + ".v";
+      const char* roles[4] = {r0.c_str(), r1.c_str(), r2.c_str(), r3.c_str()};
       const float* in[4];
       for (int i = 0; i < 4; ++i) {
         const Record& r = rec(need(s, size_t(i)));
@@ -1106,8 +1128,9 @@ struct Runner {
       bg_handle out = mint(ctx, size_t(n) * 4, s.shape, BG_F32);
       float* po = reinterpret_cast<float*>(ctx->handles[out].ptr());
       {
-        Profile prof(ctx, "adamw_update_fused", n * 20, 0);
-        launch_optimizer_fused(ctx, ap, am.beta1, av.beta2, in, po, n);
+        Profile prof(ctx, adamw ? "adamw_update_fused" : "adam_update_fused", n * 20, 0);
+        launch_optimizer_fused(ctx, adamw ? kOptAdamwFused : kOptAdamFused, ap, am.beta1, av.beta2,
+                               am.weight_decay, av.weight_decay, in, po, n);
       }
       return own(out);
     }

@@ -426,3 +426,29 @@ def test_plan_adamw_param_root_fused_matches_unfused(bridge, rng):
     if bridge.profiling:
         assert "adamw_update_fused" in labels and "adamw_update_m" not in labels
         assert "adamw_update_fused" not in labels2 and "adamw_update_m" in labels2
+
+
+@pytest.mark.parametrize("wd_m,wd_v", [(0.0, 0.0), (0.03, 0.03), (0.03, 0.0)])
+def test_plan_adam_param_root_fused_matches_oracle(bridge, rng, wd_m, wd_v):
+    """The Adam chain (M and V over (param, grad, moment), PARAM over
+    (param, m', v')) fuses the same way; each moment step keeps its own
+    weight decay."""
+    n = 300_007
+    p, g, m0 = (rng.standard_normal(n).astype(F32) for _ in range(3))
+    v0 = (np.abs(rng.standard_normal(n)) * 0.01).astype(F32)
+    base = {"lr": 2e-3, "beta1": 0.8, "beta2": 0.99, "eps": 1e-7, "step": 5}
+    steps = [_buf(i, [n]) for i in range(4)] + [_load(4 + i, i, [n]) for i in range(4)]
+    steps.append({"step": 8, "value_id": 8, "op": "ADAM_UPDATE_M", "input_ids": [4, 5, 6], "shape": [n],
+                  "dtype": "float32", "arg": {**base, "weight_decay": wd_m}})
+    steps.append({"step": 9, "value_id": 9, "op": "ADAM_UPDATE_V", "input_ids": [4, 5, 7], "shape": [n],
+                  "dtype": "float32", "arg": {**base, "weight_decay": wd_v}})
+    steps.append({"step": 10, "value_id": 10, "op": "ADAM_UPDATE_PARAM", "input_ids": [4, 8, 9], "shape": [n],
+                  "dtype": "float32", "arg": base})
+    bridge.flushProfiles()
+    got = _run(bridge, _plan(steps, 10), [p, g, m0, v0])
+    labels = [q["label"] for q in bridge.flushProfiles()["passProfiles"]]
+    em = O.adam_update_m(p, g, m0, 0.8, wd_m)
+    ev = O.adam_update_v(p, g, v0, 0.99, wd_v)
+    assert np.array_equal(got, O.adam_update_param(p, em, ev, 2e-3, 0.8, 0.99, 1e-7, 5))
+    if bridge.profiling:
+        assert labels.count("adam_update_fused") == 1 and "adam_update_m" not in labels

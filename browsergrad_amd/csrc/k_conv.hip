@@ -392,12 +392,52 @@ __global__ void __launch_bounds__(256) conv_bias_final_kernel(const float* __res
   db[o] = acc;
 }
 
+// w2[(g*Cpg + c)*Opg*KV + o*KV + kv] = w[((g*Opg + o)*Cpg + c)*KV + KV-1-kv]:
+// the weight of the forward convolution equal to a stride-1 input gradient
+// (channel roles exchanged, every spatial tap reversed).
+__global__ void __launch_bounds__(256) conv_flip_weight_kernel(const float* __restrict__ w, float* __restrict__ w2,
+                                                               int64_t G, int64_t Opg, int64_t Cpg, int64_t KV) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = G * Opg * Cpg * KV;
+  if (i >= total) return;
+  const int64_t kv = i % KV;
+  const int64_t o = (i / KV) % Opg;
+  const int64_t gc = i / (KV * Opg);  // g * Cpg + c
+  const int64_t g = gc / Cpg, c = gc % Cpg;
+  w2[i] = w[((g * Opg + o) * Cpg + c) * KV + (KV - 1 - kv)];
+}
+
 }  // namespace
 
 namespace bg {
 
 void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, const float* b, const float* bias,
                  float* out) {
+  if (mode == 1 && p.stride[0] == 1 && p.stride[1] == 1 && p.stride[2] == 1) {
+    // dx[q] = sum dy[q + pad - kv*dil] w[kv] is, with kv' = K-1-kv, the
+    // forward convolution of dy by the tap-reversed, channel-exchanged
+    // weight with padding dil*(K-1) - pad (when that is not negative).
+    ConvProblem f = p;
+    bool ok = true;
+    for (int i = 0; i < 3; ++i) {
+      f.pad[i] = p.dil[i] * (p.k[i] - 1) - p.pad[i];
+      ok = ok && f.pad[i] >= 0;
+      f.in[i] = p.out[i];
+      f.out[i] = p.in[i];
+    }
+    if (ok) {
+      f.c = p.o;
+      f.o = p.c;
+      const int64_t G = p.groups, Opg = p.o / G, Cpg = p.c / G, KV = p.k[0] * p.k[1] * p.k[2];
+      const int64_t total = G * Opg * Cpg * KV;
+      float* w2 = static_cast<float*>(scratch(ctx, size_t(total) * 4, 1));
+      if (total > 0)
+        dispatch(ctx, conv_flip_weight_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, b, w2, G, Opg,
+                 Cpg, KV);
+      launch_conv(ctx, f, 0, a, w2, bias, out);
+      return;
+    }
+  }
   ConvK k{};
   k.a = a;
   k.b = b;

@@ -27,6 +27,7 @@ from typing import Any, Dict, List, Tuple
 
 from .fusion import fuse
 from .ir import (
+    CONV_OPS,
     OP_ADD, OP_BROADCAST_TO, OP_BUFFER, OP_CAST, OP_CMP, OP_CONST, OP_CUSTOM, OP_DIV, OP_EXP,
     OP_FUSED_ELEMENTWISE, OP_FUSED_SOFTMAX, OP_LAYER_NORM, OP_LOAD, OP_LOG, OP_MATMUL, OP_MUL, OP_NEG,
     OP_PERMUTE, OP_REDUCE, OP_RESHAPE, OP_WHERE, UOp, toposort,
@@ -44,7 +45,7 @@ PLAN_OPS = frozenset({
     OP_BUFFER, OP_LOAD, OP_CONST, OP_CAST, OP_ADD, OP_MUL, OP_DIV, OP_NEG, OP_EXP, OP_LOG, OP_CMP, OP_WHERE,
     OP_MATMUL, OP_REDUCE, OP_RESHAPE, OP_PERMUTE, OP_BROADCAST_TO, OP_LAYER_NORM, OP_FUSED_ELEMENTWISE,
     OP_FUSED_SOFTMAX,
-})
+}) | CONV_OPS
 
 
 class GpuPlanUnsupported(JitNotImplementedError):

@@ -16,6 +16,8 @@ are the reference's (_ir.py:80-185):
     LAYER_NORM arg: {normalized_shape, rows, cols, eps}
     FUSED_ELEMENTWISE arg: {ops}      FUSED_SOFTMAX arg: {axis}
     ATTENTION_FORWARD                 CUSTOM (refused by the walker)
+    CONV1D / CONV2D / CONV3D / CONV_TRANSPOSE2D and their _BACKWARD_INPUT /
+    _WEIGHT / _BIAS forms, arg: the plan's conv fields (n, c_in, ..., groups)
 
 Equality is identity (every pass here keys on id(), as the reference's
 realizers do), so no structural hash cache is needed.
@@ -51,6 +53,11 @@ OP_FUSED_SOFTMAX = "FUSED_SOFTMAX"
 OP_ATTENTION_FORWARD = "ATTENTION_FORWARD"
 OP_CUSTOM = "CUSTOM"
 
+CONV_OPS: FrozenSet[str] = frozenset(
+    base + suffix
+    for base in ("CONV1D", "CONV2D", "CONV3D", "CONV_TRANSPOSE2D")
+    for suffix in ("", "_BACKWARD_INPUT", "_BACKWARD_WEIGHT", "_BACKWARD_BIAS"))
+
 # Rewrites produced by this package's own fusion pass (hip_fusion.py); they
 # never appear in graphs the reference builds.
 OP_HIP_LINEAR = "HIP_LINEAR"          # GEMM + AMP rounding + bias + activation epilogue
@@ -62,7 +69,7 @@ ALL_OPS: FrozenSet[str] = frozenset({
     OP_CMP, OP_WHERE, OP_MATMUL, OP_REDUCE, OP_RESHAPE, OP_PERMUTE, OP_SLICE, OP_BROADCAST_TO,
     OP_LAYER_NORM, OP_FUSED_ELEMENTWISE, OP_FUSED_SOFTMAX, OP_ATTENTION_FORWARD, OP_CUSTOM,
     OP_HIP_LINEAR, OP_HIP_ATTENTION, OP_HIP_REDUCE_FUSED,
-})
+}) | CONV_OPS
 
 _LEAF_OPS: FrozenSet[str] = frozenset({OP_BUFFER, OP_CONST})
 

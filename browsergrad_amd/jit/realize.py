@@ -40,6 +40,7 @@ from .fusion import fuse
 from .gpu_plan import build_gpu_execution_submission
 from .hip_fusion import hip_fuse
 from .ir import (
+    CONV_OPS,
     OP_ADD, OP_ATTENTION_FORWARD, OP_BROADCAST_TO, OP_BUFFER, OP_CAST, OP_CMP, OP_CONST, OP_CUSTOM, OP_DIV,
     OP_EXP, OP_FUSED_ELEMENTWISE, OP_FUSED_SOFTMAX, OP_HIP_ATTENTION, OP_HIP_LINEAR, OP_HIP_REDUCE_FUSED,
     OP_LAYER_NORM, OP_LOAD, OP_LOG, OP_MATMUL, OP_MUL, OP_NEG, OP_PERMUTE, OP_REDUCE, OP_RESHAPE, OP_SLICE,
@@ -251,6 +252,41 @@ def _h_layer_norm(n: UOp, w: _Walk) -> int:
     return out
 
 
+def _conv_desc(op: str, arg: dict) -> Tuple[str, dict]:
+    """(conv_ex op, geometry) of a CONV* node from the plan's arg fields."""
+    kind = "forward"
+    for suffix, name in (("_BACKWARD_INPUT", "backward_input"), ("_BACKWARD_WEIGHT", "backward_weight"),
+                         ("_BACKWARD_BIAS", "backward_bias")):
+        if op.endswith(suffix):
+            kind, op = name, op[: -len(suffix)]
+    transposed = op == "CONV_TRANSPOSE2D"
+    r = 1 if op == "CONV1D" else 3 if op == "CONV3D" else 2
+    a = {k: int(v) for k, v in arg.items() if not isinstance(v, bool)}
+    if r == 1:
+        geo = dict(in_size=(a["l_in"],), out_size=(a["l_out"],), k=(a["k"],), stride=(a["stride"],),
+                   pad=(a["padding"],), dilation=(a["dilation"],))
+    else:
+        axes = ("h", "w") if r == 2 else ("d", "h", "w")
+        geo = dict(in_size=tuple(a[x] for x in axes), out_size=tuple(a[f"out_{x}"] for x in axes),
+                   k=tuple(a[f"k{x}"] for x in axes), stride=tuple(a[f"stride_{x}"] for x in axes),
+                   pad=tuple(a[f"pad_{x}"] for x in axes), dilation=tuple(a[f"dilation_{x}"] for x in axes))
+        if transposed:
+            geo["output_pad"] = tuple(a[f"output_pad_{x}"] for x in axes)
+    geo.update(n=a["n"], c_in=a["c_in"], c_out=a["c_out"], groups=a["groups"], transposed=transposed)
+    return kind, geo
+
+
+def _h_conv(n: UOp, w: _Walk) -> int:
+    """CONV1D / CONV2D / CONV3D / CONV_TRANSPOSE2D and their backward forms
+    (_realize.py:413-1005) on bg_conv_ex."""
+    kind, geo = _conv_desc(n.op, n.arg)
+    hs = [w.h(i) for i in n.inputs]
+    a = hs[0]
+    b = hs[1] if len(hs) > 1 else 0
+    bias = hs[2] if kind == "forward" and len(hs) > 2 else 0
+    return w.br.conv_ex(kind, a, b, bias, **geo)
+
+
 def _h_fused_softmax(n: UOp, w: _Walk) -> int:
     x = n.inputs[0]
     axis = n.arg.get("axis")
@@ -373,6 +409,7 @@ _DISPATCH: Dict[str, Callable[[UOp, _Walk], int]] = {
     OP_HIP_ATTENTION: _h_hip_attention,
     OP_HIP_LINEAR: _h_hip_linear,
     OP_HIP_REDUCE_FUSED: _h_hip_fused,
+    **{op: _h_conv for op in CONV_OPS},
 }
 
 

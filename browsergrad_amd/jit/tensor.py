@@ -398,7 +398,59 @@ def flash_attention(q: Tensor, k: Tensor, v: Tensor, mask: Any = None, scale: An
     return attention_forward(q, k, v)
 
 
+def _tup(v: Any, r: int) -> Tuple[int, ...]:
+    return tuple(int(a) for a in v) if isinstance(v, (tuple, list)) else (int(v),) * r
+
+
+def _conv_nd(x: Tensor, w: Tensor, bias: Optional[Tensor], stride: Any, padding: Any, dilation: Any,
+             groups: int, r: int) -> Tensor:
+    """CONV1D / CONV2D / CONV3D graph node with the reference plan's arg
+    fields (tensor_plan.ts:715-790) and has_bias (_realize.py:413-583)."""
+    if x.dtype != "float32" or w.dtype != "float32":
+        raise ShapeError(f"conv{r}d: float32 tensors only (got {x.dtype}, {w.dtype})")
+    if len(x.shape) != r + 2 or len(w.shape) != r + 2:
+        raise ShapeError(f"conv{r}d: input and weight must have rank {r + 2}")
+    n, c = x.shape[:2]
+    o, cpg = w.shape[:2]
+    k = w.shape[2:]
+    s, p, d = _tup(stride, r), _tup(padding, r), _tup(dilation, r)
+    if c % groups or o % groups or cpg != c // groups:
+        raise ShapeError(f"conv{r}d: weight {w.shape} does not match {c} channels in {groups} groups")
+    ins = x.shape[2:]
+    out = tuple((ins[i] + 2 * p[i] - d[i] * (k[i] - 1) - 1) // s[i] + 1 for i in range(r))
+    if any(v <= 0 for v in out):
+        raise ShapeError(f"conv{r}d: output size {out} is not positive")
+    if r == 1:
+        arg = {"n": n, "c_in": c, "l_in": ins[0], "c_out": o, "k": k[0], "stride": s[0], "padding": p[0],
+               "dilation": d[0], "groups": groups, "l_out": out[0]}
+    else:
+        axes = ("h", "w") if r == 2 else ("d", "h", "w")
+        arg = {"n": n, "c_in": c, "c_out": o, "groups": groups}
+        for i, a in enumerate(axes):
+            arg.update({a: ins[i], f"k{a}": k[i], f"stride_{a}": s[i], f"pad_{a}": p[i], f"dilation_{a}": d[i],
+                        f"out_{a}": out[i]})
+    arg["has_bias"] = bias is not None
+    inputs = (x.uop, w.uop) + ((bias.uop,) if bias is not None else ())
+    return x._wrap(UOp(f"CONV{r}D", inputs, (n, o) + out, "float32", arg))
+
+
+def conv1d(x: Tensor, w: Tensor, bias: Optional[Tensor] = None, stride: Any = 1, padding: Any = 0,
+           dilation: Any = 1, groups: int = 1) -> Tensor:
+    return _conv_nd(x, w, bias, stride, padding, dilation, groups, 1)
+
+
+def conv2d(x: Tensor, w: Tensor, bias: Optional[Tensor] = None, stride: Any = 1, padding: Any = 0,
+           dilation: Any = 1, groups: int = 1) -> Tensor:
+    return _conv_nd(x, w, bias, stride, padding, dilation, groups, 2)
+
+
+def conv3d(x: Tensor, w: Tensor, bias: Optional[Tensor] = None, stride: Any = 1, padding: Any = 0,
+           dilation: Any = 1, groups: int = 1) -> Tensor:
+    return _conv_nd(x, w, bias, stride, padding, dilation, groups, 3)
+
+
 __all__ = [
+    "conv1d", "conv2d", "conv3d",
     "Tensor", "Session", "autocast", "active_autocast", "promote", "broadcast_shape",
     "where", "relu", "tanh", "gelu", "softmax", "linear", "layer_norm", "scaled_dot_product_attention",
     "attention_forward", "flash_attention",

@@ -68,6 +68,42 @@ def _operands(n: UOp, vals) -> list:
     return arrs
 
 
+def _conv(op: str, arg: dict, ins: list) -> np.ndarray:
+    """The CONV* handlers (_realize.py:413-1005) through oracle.ops' conv
+    restatements, with the plan's arg fields."""
+    from . import ops as O
+    kind = "FWD"
+    for suffix in ("_BACKWARD_INPUT", "_BACKWARD_WEIGHT", "_BACKWARD_BIAS"):
+        if op.endswith(suffix):
+            kind, op = suffix, op[: -len(suffix)]
+    a = {k: int(v) for k, v in arg.items() if not isinstance(v, bool)}
+    if op == "CONV1D":
+        ins_, out_, k_ = (a["l_in"],), (a["l_out"],), (a["k"],)
+        s_, p_, d_ = (a["stride"],), (a["padding"],), (a["dilation"],)
+    else:
+        axes = ("h", "w") if op in ("CONV2D", "CONV_TRANSPOSE2D") else ("d", "h", "w")
+        ins_ = tuple(a[x] for x in axes)
+        out_ = tuple(a[f"out_{x}"] for x in axes)
+        k_ = tuple(a[f"k{x}"] for x in axes)
+        s_ = tuple(a[f"stride_{x}"] for x in axes)
+        p_ = tuple(a[f"pad_{x}"] for x in axes)
+        d_ = tuple(a[f"dilation_{x}"] for x in axes)
+    g = a["groups"]
+    if kind == "_BACKWARD_BIAS":
+        return O.conv_backward_bias(ins[0])
+    if op == "CONV_TRANSPOSE2D":
+        if kind == "FWD":
+            return O.conv_transpose_forward(ins[0], ins[1], ins[2] if len(ins) > 2 else None, s_, p_, d_, g, out_)
+        if kind == "_BACKWARD_INPUT":
+            return O.conv_transpose_backward_input(ins[0], ins[1], s_, p_, d_, g, ins_)
+        return O.conv_transpose_backward_weight(ins[0], ins[1], k_, s_, p_, d_, g)
+    if kind == "FWD":
+        return O.conv_forward(ins[0], ins[1], ins[2] if len(ins) > 2 else None, s_, p_, d_, g, out_)
+    if kind == "_BACKWARD_INPUT":
+        return O.conv_backward_input(ins[0], ins[1], s_, p_, d_, g, ins_)
+    return O.conv_backward_weight(ins[0], ins[1], k_, s_, p_, d_, g)
+
+
 def evaluate(root: UOp, bt: BufferTable, *, amp: bool = True) -> np.ndarray:
     if amp:
         root = insert_cast_pass(root)
@@ -119,6 +155,8 @@ def evaluate(root: UOp, bt: BufferTable, *, amp: bool = True) -> np.ndarray:
             out = ins[0][tuple(slice(s[0], s[1], s[2]) for s in n.arg["slices"])]
         elif op == "BROADCAST_TO":
             out = np.broadcast_to(ins[0], n.shape)
+        elif op.startswith("CONV"):
+            out = _conv(op, n.arg, ins)
         elif op == "LAYER_NORM":
             x, w, b = ins
             rows, cols = int(n.arg["rows"]), int(n.arg["cols"])

@@ -373,6 +373,32 @@ __global__ void __launch_bounds__(256) conv_row_sum_kernel(const float* __restri
   if (lane == 0) part[r] = s;
 }
 
+// The same sum for rows of spatial4 float4s (row length a multiple of 4, the
+// tensor 16-byte aligned): each lane has up to four float4 loads in flight
+// before it adds any of them.
+__global__ void __launch_bounds__(256) conv_row_sum4_kernel(const float4* __restrict__ dy, float* __restrict__ part,
+                                                            int64_t rows, int64_t spatial4) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float4* row = dy + r * spatial4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t base = 0; base < spatial4; base += 256) {
+    float4 t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t q = base + lane + 64 * u;
+      t[u] = q < spatial4 ? row[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += (t[u].x + t[u].y) + (t[u].z + t[u].w);
+  }
+  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (lane == 0) part[r] = s;
+}
+
 // db[o] = sum over n (in order) of part[n * O + o]; eight loads are issued
 // before they are added.
 __global__ void __launch_bounds__(256) conv_bias_final_kernel(const float* __restrict__ part, float* __restrict__ db,
@@ -546,7 +572,11 @@ void launch_conv_bias_grad(bg_ctx* ctx, const float* dy, float* out, int64_t n, 
   if (o == 0) return;
   const int64_t rows = n * o;
   float* part = static_cast<float*>(scratch(ctx, size_t(rows) * 4, 0));
-  dispatch(ctx, conv_row_sum_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, dy, part, rows, spatial);
+  if (spatial % 4 == 0 && (reinterpret_cast<uintptr_t>(dy) & 15) == 0)
+    dispatch(ctx, conv_row_sum4_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0,
+             reinterpret_cast<const float4*>(dy), part, rows, spatial / 4);
+  else
+    dispatch(ctx, conv_row_sum_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, dy, part, rows, spatial);
   dispatch(ctx, conv_bias_final_kernel, dim3(unsigned((o + 255) / 256)), dim3(256), 0, part, out, n, o);
   hip_check(hipGetLastError(), "conv bias-gradient launch");
 }

@@ -357,3 +357,17 @@ def test_conv2d_large_against_float64(bridge, case):
         err = np.abs(got - truth)
         bound = _bound(truth, mass, K)
         assert np.all(err <= bound), float(np.max(err / bound))
+
+
+@pytest.mark.parametrize("shape", [(4, 16, 28, 28), (3, 5, 7, 7), (2, 3, 4, 300)])
+def test_bias_gradient_float4_and_scalar_rows(bridge, shape):
+    """Spatial sizes that are multiples of 4 (784, 1200) take the float4 row
+    sum, 49 the scalar one; both against the oracle's sum over (n, spatial)."""
+    n, co, oh, ow = shape
+    dy = np.random.default_rng(oh * ow + co).standard_normal(shape).astype(F32)
+    kw = dict(n=n, c_in=co, c_out=co, in_size=(oh, ow), out_size=(oh, ow), k=(1, 1), stride=(1, 1),
+              pad=(0, 0), dilation=(1, 1), groups=1)
+    got = conv_ex(bridge, "backward_bias", dy, **kw)
+    ref = O.conv_backward_bias(dy)
+    assert got.shape == ref.shape
+    assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)

@@ -389,6 +389,12 @@ int bg_handle_info(bg_ctx* ctx, bg_handle h, int64_t* shape_out, int* rank,
                    int* dtype, int64_t* nbytes) {
   BG_API_BEGIN
   Record& r = get(ctx, h, "handle_info");
+  // Callers size shape_out for BG_MAX_RANK entries; every entry point that
+  // sets a record's shape keeps it within that, and this guard keeps a
+  // violation from ever writing past the caller's array.
+  if (r.shape.size() > BG_MAX_RANK)
+    fail(BG_E_SHAPE, "handle_info: handle has rank " + std::to_string(r.shape.size()) + ", above " +
+                         std::to_string(BG_MAX_RANK));
   if (shape_out)
     for (size_t i = 0; i < r.shape.size(); ++i) shape_out[i] = r.shape[i];
   if (rank) *rank = int(r.shape.size());
@@ -829,6 +835,9 @@ int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
                          " not supported");
   if (d.out_dtype != BG_F32 && d.out_dtype != BG_F16 && d.out_dtype != BG_BF16)
     fail(BG_E_DTYPE, "matmul: output dtype not supported");
+  if (d.stride_a < 0 || d.stride_b < 0 || d.stride_c < 0 || d.offset_a < 0 || d.offset_b < 0 ||
+      d.lda < 0 || d.ldb < 0 || d.ldc < 0)
+    fail(BG_E_INVALID, "matmul: negative stride/offset");
   // Bounds of the strided operands.
   auto need = [](int64_t off, int64_t batch, int64_t sb, int64_t rows, int64_t ld,
                  int64_t cols) {
@@ -846,12 +855,12 @@ int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
     if (need(d.offset_b, d.batch, d.stride_b, d.k, d.ldb, d.n) > rb.numel())
       fail(BG_E_SHAPE, "matmul: B view exceeds its handle");
   }
-  if (d.stride_a < 0 || d.stride_b < 0 || d.offset_a < 0 || d.offset_b < 0)
-    fail(BG_E_INVALID, "matmul: negative stride/offset");
   bg_matmul_desc dd = d;
   if (dd.ldc == 0) dd.ldc = d.n;
   if (dd.stride_c == 0) dd.stride_c = d.m * dd.ldc;
   if (dd.ldc < d.n) fail(BG_E_SHAPE, "matmul: ldc < n");
+  if (d.batch > 1 && dd.stride_c < (d.m - 1) * dd.ldc + d.n)
+    fail(BG_E_SHAPE, "matmul: stride_c makes the output matrices of the batch overlap");
   std::vector<int64_t> os;
   if (d.batch > 1) os.push_back(d.batch);
   os.push_back(d.m);
@@ -870,6 +879,23 @@ int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
   }
   *out = o;
   BG_API_END
+}
+
+// True when rows of `row` contiguous elements placed at sum_i idx_i *
+// strides[i] (idx_i < extents[i]) never overlap: taken in increasing stride
+// order, every stride must clear the span of the dimensions inside it.
+// Dimensions of extent 1 take no part.
+static bool disjoint_rows(std::vector<int64_t> extents, std::vector<int64_t> strides, int64_t row) {
+  std::vector<size_t> order;
+  for (size_t i = 0; i < extents.size(); ++i)
+    if (extents[i] > 1) order.push_back(i);
+  std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return strides[a] < strides[b]; });
+  int64_t span = row;
+  for (size_t i : order) {
+    if (strides[i] < span) return false;
+    span = strides[i] * (extents[i] - 1) + span;
+  }
+  return true;
 }
 
 int bg_attention_ex(bg_ctx* ctx, const bg_attention_desc* desc, bg_handle* out) {
@@ -895,6 +921,11 @@ int bg_attention_ex(bg_ctx* ctx, const bg_attention_desc* desc, bg_handle* out) 
   fix(d.k_sb, d.k_sh, d.k_ss, d.sk);
   fix(d.v_sb, d.v_sh, d.v_ss, d.sk);
   fix(d.o_sb, d.o_sh, d.o_ss, d.sq);
+  for (int64_t x : {d.q_off, d.k_off, d.v_off, d.q_sb, d.q_sh, d.q_ss, d.k_sb, d.k_sh, d.k_ss, d.v_sb,
+                    d.v_sh, d.v_ss, d.o_sb, d.o_sh, d.o_ss})
+    if (x < 0) fail(BG_E_INVALID, "flash_attention: negative offset or stride");
+  if (!disjoint_rows({d.batch, d.heads, d.sq}, {d.o_sb, d.o_sh, d.o_ss}, d.d))
+    fail(BG_E_SHAPE, "flash_attention: output strides make output rows overlap");
   auto reach = [&](int64_t off, int64_t sb, int64_t sh, int64_t ss, int64_t s) {
     return off + (d.batch - 1) * sb + (d.heads - 1) * sh + (s - 1) * ss + d.d;
   };
@@ -954,13 +985,24 @@ int bg_flash_attention(bg_ctx* ctx, bg_handle q, bg_handle k, bg_handle v,
     fail(BG_E_DTYPE, "flash_attention: an additive mask requires float32");
   Record& rm = get(ctx, mask, "flash_attention[mask]");
   if (rm.dtype != BG_F32) fail(BG_E_DTYPE, "flash_attention: mask must be float32");
-  int64_t per = sq * sk;
+  // Broadcast comes from the mask's recorded shape: [1|b, 1|h, sq, sk] or
+  // [sq, sk].  Any other shape must hold the full b*h*sq*sk elements, the
+  // layout the reference bridge reads (mask_B = B, mask_H = H).
+  const int64_t per = sq * sk;
+  const std::vector<int64_t>& ms = rm.shape;
   int64_t mb = 0, mh = 0;
-  if (rm.numel() == per) { mb = 0; mh = 0; }
-  else if (rm.numel() == h * per) { mb = 0; mh = per; }
-  else if (rm.numel() == b * per) { mb = per; mh = 0; }
-  else if (rm.numel() == b * h * per) { mb = h * per; mh = per; }
-  else fail(BG_E_SHAPE, "flash_attention: mask must be [1|b,1|h,sq,sk]");
+  if (ms.size() == 4 && ms[2] == sq && ms[3] == sk && (ms[0] == 1 || ms[0] == b) &&
+      (ms[1] == 1 || ms[1] == h)) {
+    mh = ms[1] == 1 ? 0 : per;
+    mb = ms[0] == 1 ? 0 : ms[1] * per;
+  } else if (ms.size() == 2 && ms[0] == sq && ms[1] == sk) {
+    mb = mh = 0;
+  } else if (rm.numel() == b * h * per) {
+    mb = h * per;
+    mh = per;
+  } else {
+    fail(BG_E_SHAPE, "flash_attention: mask must be [1|b,1|h,sq,sk] or [sq,sk]");
+  }
   std::vector<int64_t> os = {b, h, sq, d};
   bg_handle o = mint(ctx, size_t(b * h * sq * d * 4), os, BG_F32);
   Record& ro = ctx->handles[o];

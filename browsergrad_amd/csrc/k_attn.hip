@@ -929,15 +929,16 @@ __global__ void __launch_bounds__(kFa2NW * 64, 2) fa6_fwd_kernel(Fa2Args P, uint
     }
 }
 
-template <bool BF16, bool CAUSAL, bool ROUND_S>
+template <bool BF16, bool CAUSAL>
 void launch_fa6(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uint32_t vb) {
-  (void)ROUND_S;  // v6 has one numerics for both (see the kernel's header)
   bg::dispatch(ctx, fa6_fwd_kernel<BF16, CAUSAL>, dim3(unsigned(bh), unsigned(nqb), 1),
                dim3(kFa2NW * 64), 0, A, kb, vb);
 }
 
-// BG_ATTN_KERNEL=2 selects the v2 kernel (reference rounding of S to 16
-// bits, one workgroup per CU) instead of v6, for comparisons.
+// BG_ATTN_KERNEL=2 selects the v2 kernel for every call, for comparisons.
+// Independently of it, v6 runs only where its numerics hold: S is not
+// rounded (round_scores == 0; v2 rounds S exactly), and Q' = Q * scale *
+// log2(e) cannot overflow f16 (scale * log2(e) <= 1, so |Q'| <= |Q|).
 int attn_version() {
   static const int v = [] {
     const char* e = std::getenv("BG_ATTN_KERNEL");
@@ -1016,9 +1017,10 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     const bool r = d.round_scores != 0;
     const uint32_t kb = uint32_t(k_head), vb = uint32_t(v_head);
     Profile prof(ctx, bf ? "attention_bf16" : "attention_f16", bytes, flops);
-#define BG_FA2(B_, C_, R_)                                              \
-  (attn_version() == 6 ? launch_fa6<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb) \
-                       : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
+    const bool v6 = attn_version() == 6 && !r && (bf || A.sl2 <= 1.0f);
+#define BG_FA2(B_, C_, R_)                                             \
+  (v6 && !R_ ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb) \
+             : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
     if (bf) {
       if (c) { if (r) BG_FA2(true, true, true); else BG_FA2(true, true, false); }
       else { if (r) BG_FA2(true, false, true); else BG_FA2(true, false, false); }

@@ -312,6 +312,9 @@ Plan normalize(const JVal& root) {
     st.op = op->str;
     st.inputs = int_list(s.get2("input_ids", "inputIds"), at + ".inputIds");
     st.shape = int_list(s.get("shape"), at + ".shape");
+    if (st.shape.size() > BG_MAX_RANK)
+      fail(BG_E_INVALID, at + ".shape has rank " + std::to_string(st.shape.size()) + ", above " +
+                             std::to_string(BG_MAX_RANK));
     for (int64_t d : st.shape)
       if (d < 0) fail(BG_E_INVALID, at + ".shape has a negative extent");
     const JVal* dt = s.get("dtype");

@@ -149,7 +149,7 @@ def _bytes_for(shape: Tuple[int, ...], dtype: str) -> int:
 
 
 def build_gpu_execution_plan(root: UOp, *, allow_custom: bool = False) -> GpuExecutionPlan:
-    if not allow_custom:
+    if not allow_custom:  # fused whatever the fusion switch says (_gpu_plan.py:292-294)
         root = fuse(root)
     order = toposort(root)
     custom = next((n for n in order if n.op == OP_CUSTOM), None)

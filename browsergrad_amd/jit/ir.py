@@ -82,6 +82,15 @@ KNOWN_DTYPES: FrozenSet[str] = frozenset({
 MAX_ELEMENTS = 2 ** 34  # sized for one MI355X (288 GB HBM); the reference caps at 2**30
 
 
+def set_max_elements(n: int) -> None:
+    """Change the per-tensor element ceiling (_ir.py:360-368); graphs built
+    afterwards are checked against the new value."""
+    global MAX_ELEMENTS
+    if isinstance(n, bool) or not isinstance(n, int) or n <= 0:
+        raise ValueError(f"set_max_elements: expected a positive int, got {n!r}")
+    MAX_ELEMENTS = n
+
+
 
 
 @dataclass(frozen=True, eq=False)
@@ -157,5 +166,5 @@ def const(value: float, dtype: str = "float32") -> UOp:
 
 
 __all__ = [name for name in dir() if name.startswith("OP_")] + [
-    "ALL_OPS", "KNOWN_DTYPES", "ShapeError", "UOp", "toposort", "buffer", "load", "const",
+    "ALL_OPS", "KNOWN_DTYPES", "ShapeError", "UOp", "toposort", "buffer", "load", "const", "set_max_elements",
 ]

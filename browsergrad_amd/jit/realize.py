@@ -33,6 +33,7 @@ import numpy as np
 
 from .. import _native as N
 from ..errors import JitNotImplementedError, KernelError
+from . import config
 from .amp import insert_cast_pass
 from .attention_forward import validate_attention_forward_node
 from .buffers import BufferTable, GpuBufferTable
@@ -335,6 +336,13 @@ def _h_attention_forward(n: UOp, w: _Walk) -> int:
                                 c.depth, c.scale, n.dtype)
 
 
+def _round_scores(arg: dict) -> bool:
+    """The graph rounds S (arg round_scores); the kernel is asked to repeat
+    that rounding only under config.exact_attention_score_rounding, and
+    otherwise keeps S in f32 (within the 16-bit tolerance of the graph)."""
+    return bool(arg["round_scores"]) and config.attention_rounds_scores()
+
+
 def _h_hip_attention(n: UOp, w: _Walk) -> int:
     q, k, v = n.inputs
     a = n.arg
@@ -344,7 +352,7 @@ def _h_hip_attention(n: UOp, w: _Walk) -> int:
         sk = k.shape[2]
         return w.br.attention_ex(w.h(q), w.h(k), w.h(v), batch=b, heads=h, sq=sq, sk=sk, d=d, scale=a["scale"],
                                  causal=a["causal"], in_dtype=q.dtype, out_dtype=n.dtype,
-                                 round_scores=a["round_scores"])
+                                 round_scores=_round_scores(a))
     # Q / K / V are strided views of one [B, S, 3E] buffer; the output is
     # written [B, H, S, D] or, with o_layout "bshd", [B, S, H, D].
     b, s = q.shape[0], q.shape[1]
@@ -356,7 +364,7 @@ def _h_hip_attention(n: UOp, w: _Walk) -> int:
         o_strides = (0, 0, 0)
     out = w.br.attention_ex(w.h(q), w.h(k), w.h(v), batch=b, heads=h, sq=s, sk=s, d=d, scale=a["scale"],
                             causal=a["causal"], in_dtype=q.dtype, out_dtype=n.dtype,
-                            round_scores=a["round_scores"], q_view=tuple(views[0]), k_view=tuple(views[1]),
+                            round_scores=_round_scores(a), q_view=tuple(views[0]), k_view=tuple(views[1]),
                             v_view=tuple(views[2]), o_strides=o_strides)
     if a["o_layout"] == "bshd":
         view = w.br.reshape(out, n.shape)
@@ -418,8 +426,12 @@ def supported_opcodes() -> frozenset:
 
 
 def prepare(root: UOp, bt: BufferTable, *, hip_rewrites: bool = True) -> UOp:
-    """Cast insertion, this build's rewrites, then the reference's fusion."""
+    """Cast insertion, this build's rewrites, then the reference's fusion
+    (both skipped while fusion is disabled, config.use_fusion /
+    BG_DISABLE_FUSION, as _realize.py:1891 skips _fusion.fuse)."""
     root = insert_cast_pass(root)
+    if not config.fusion_enabled():
+        return root
     if hip_rewrites:
         root = hip_fuse(root, bt)
     return fuse(root)

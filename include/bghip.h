@@ -176,10 +176,14 @@ typedef struct bg_matmul_desc {
 
 /* Extension descriptor for attention.  Q/K/V/O are addressed with explicit
  * element strides so head-split views (reshape+permute of a fused QKV
- * projection) need no copy.  Softmax and accumulation are f32; the score
- * matrix is rounded to the input dtype before scaling when
- * round_scores != 0 (the reference's autocast MATMUL output rounding,
- * _realize.py:395-412), and P is rounded to the input dtype before P@V. */
+ * projection) need no copy.  Softmax and accumulation are f32, and P is
+ * rounded to the input dtype before P@V.
+ * round_scores != 0: the score matrix S = Q K^T is rounded to the input
+ *   dtype before scaling, as the reference's autocast MATMUL output is
+ *   (_realize.py:395-412); a kernel that rounds S exactly runs.
+ * round_scores == 0: S stays in f32.  The fastest kernel may then fold the
+ *   scale into Q (Q' = Q * scale * log2(e), one 16-bit rounding of Q'), and
+ *   does so only where Q' cannot overflow (bf16, or scale * log2(e) <= 1). */
 typedef struct bg_attention_desc {
   bg_handle q, k, v;
   int64_t batch, heads, sq, sk, d;

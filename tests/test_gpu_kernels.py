@@ -181,7 +181,8 @@ def test_copy_strided_permute(bridge, rng):
 @pytest.mark.parametrize("b,h,s,causal", [(1, 2, 4, False), (2, 3, 128, True), (1, 2, 200, True),
                                           (2, 2, 256, False), (1, 1, 1000, True)])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_attention_mfma(bridge, rng, b, h, s, causal, dtype):
+@pytest.mark.parametrize("round_scores", [False, True])
+def test_attention_mfma(bridge, rng, b, h, s, causal, dtype, round_scores):
     d = 64
     q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
     scale = 1.0 / np.sqrt(d)
@@ -194,7 +195,7 @@ def test_attention_mfma(bridge, rng, b, h, s, causal, dtype):
         hq, hk, hv = (up(bridge, t, "bfloat16") for t in (q16, k16, v16))
         ref = O.bf16_bits_to_f32(O.sdpa_bf16(q16, k16, v16, scale, causal))
     ho = bridge.attention_ex(hq, hk, hv, batch=b, heads=h, sq=s, sk=s, d=d, scale=scale, causal=causal,
-                             in_dtype=dtype, round_scores=True)
+                             in_dtype=dtype, round_scores=round_scores)
     y = bridge.to_numpy(ho)
     y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
@@ -259,7 +260,8 @@ def test_gemm_f32_bias_relu_gelu(bridge, rng, m, k, n):
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention_long_sequence(bridge, rng, dtype, causal):
+@pytest.mark.parametrize("round_scores", [False, True])
+def test_attention_long_sequence(bridge, rng, dtype, causal, round_scores):
     """Two full S=2048 heads (the C4 shape per head) and a ragged 1100."""
     for (b, h, s) in ((1, 2, 2048), (1, 1, 1100)):
         d = 64
@@ -274,7 +276,7 @@ def test_attention_long_sequence(bridge, rng, dtype, causal):
             hq, hk, hv = (up(bridge, t, "bfloat16") for t in (q16, k16, v16))
             ref = O.bf16_bits_to_f32(O.sdpa_bf16(q16, k16, v16, scale, causal))
         ho = bridge.attention_ex(hq, hk, hv, batch=b, heads=h, sq=s, sk=s, d=d, scale=scale, causal=causal,
-                                 in_dtype=dtype, round_scores=True)
+                                 in_dtype=dtype, round_scores=round_scores)
         y = bridge.to_numpy(ho)
         y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
         assert O.within(y, ref, TOL16).all(), (b, h, s, O.report(y, ref, TOL16))
@@ -293,7 +295,8 @@ def test_attention_rectangular_noncausal(bridge, rng):
 
 
 @pytest.mark.parametrize("sq,sk", [(300, 100), (100, 300), (600, 130), (257, 257), (64, 2048)])
-def test_attention_rectangular_causal(bridge, rng, sq, sk):
+@pytest.mark.parametrize("round_scores", [False, True])
+def test_attention_rectangular_causal(bridge, rng, sq, sk, round_scores):
     """Causal with Sq != Sk: the reference mask triu(ones(Sq, Sk), k=1) is
     top-left aligned (key j visible to query i iff j <= i), so queries past Sk
     see every key.  (600, 130) puts whole query blocks past the last key."""
@@ -302,7 +305,7 @@ def test_attention_rectangular_causal(bridge, rng, sq, sk):
     k = rng.standard_normal((b, h, sk, d)).astype(np.float16)
     v = rng.standard_normal((b, h, sk, d)).astype(np.float16)
     ho = bridge.attention_ex(up(bridge, q), up(bridge, k), up(bridge, v), batch=b, heads=h, sq=sq, sk=sk, d=d,
-                             scale=0.125, causal=True, in_dtype="float16", round_scores=True)
+                             scale=0.125, causal=True, in_dtype="float16", round_scores=round_scores)
     y = bridge.to_numpy(ho).astype(np.float32)
     ref = O.sdpa_amp(q, k, v, 0.125, True).astype(np.float32)
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
@@ -310,7 +313,8 @@ def test_attention_rectangular_causal(bridge, rng, sq, sk):
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_attention_late_dominant_key(bridge, rng, causal, dtype):
+@pytest.mark.parametrize("round_scores", [False, True])
+def test_attention_late_dominant_key(bridge, rng, causal, dtype, round_scores):
     """Head 0 holds a key (index 100) whose score beats every key of the first
     32 by far more than 16 (log2 units): a reference max taken from the first
     keys must move, or P overflows the 16-bit range.  Head 1 is ordinary
@@ -333,14 +337,15 @@ def test_attention_late_dominant_key(bridge, rng, causal, dtype):
         hq, hk, hv = (up(bridge, t, "bfloat16") for t in (q16, k16, v16))
         ref = O.bf16_bits_to_f32(O.sdpa_bf16(q16, k16, v16, scale, causal))
     ho = bridge.attention_ex(hq, hk, hv, batch=b, heads=h, sq=s, sk=s, d=d, scale=scale, causal=causal,
-                             in_dtype=dtype, round_scores=True)
+                             in_dtype=dtype, round_scores=round_scores)
     y = bridge.to_numpy(ho)
     y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
     assert np.isfinite(y).all()
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
 
 
-def test_attention_strided_fused_qkv_views(bridge, rng):
+@pytest.mark.parametrize("round_scores", [False, True])
+def test_attention_strided_fused_qkv_views(bridge, rng, round_scores):
     """Q/K/V as views into one fused QKV projection [B, S, 3, H, D] (the GPT-2
     block layout): head-split without a copy, output [B, S, H, D]."""
     B, S, H, D = 2, 192, 3, 64
@@ -349,9 +354,66 @@ def test_attention_strided_fused_qkv_views(bridge, rng):
     sb, ss, sh = S * 3 * H * D, 3 * H * D, D
     views = [(i * H * D, sb, sh, ss) for i in range(3)]
     ho = bridge.attention_ex(h, h, h, batch=B, heads=H, sq=S, sk=S, d=D, scale=0.125, causal=True,
-                             in_dtype="float16", round_scores=True, q_view=views[0], k_view=views[1],
+                             in_dtype="float16", round_scores=round_scores, q_view=views[0], k_view=views[1],
                              v_view=views[2], o_strides=(S * H * D, D, H * D))
     y = bridge.to_numpy(ho).reshape(B, S, H, D).astype(np.float32)
     q, k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
     ref = O.sdpa_amp(q, k, v, 0.125, True).astype(np.float32).transpose(0, 2, 1, 3)
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_attention_round_scores_is_honoured(bridge, dtype):
+    """q.k = 2049 and 2048 (f16; 257 and 256 for bf16) round to the same
+    16-bit score, so with round_scores the two keys get P = 1/2 each and the
+    output is v0/2 + v1/2 = 0 exactly, as the reference graph (and the
+    oracle) computes; without the rounding the second key wins slightly and
+    the output is not 0."""
+    d, sk = 64, 2
+    big = 1024.0 if dtype == "float16" else 128.0
+    q = np.zeros((1, 1, 1, d), np.float32)
+    q[..., :2] = 1.0
+    k = np.zeros((1, 1, sk, d), np.float32)
+    k[0, 0, 0, :2] = (big, big)
+    k[0, 0, 1, :2] = (big + 1, big)
+    v = np.zeros((1, 1, sk, d), np.float32)
+    v[0, 0, 0], v[0, 0, 1] = 1.0, -1.0
+    scale = 1.0 / (2 * big)
+    if dtype == "float16":
+        ts = [t.astype(np.float16) for t in (q, k, v)]
+        ref = O.sdpa_amp(*ts, scale, False).astype(np.float32)
+        hs = [up(bridge, t) for t in ts]
+    else:
+        ts = [O.f32_to_bf16_bits(t) for t in (q, k, v)]
+        ref = O.bf16_bits_to_f32(O.sdpa_bf16(*ts, scale, False))
+        hs = [up(bridge, t, "bfloat16") for t in ts]
+    assert np.all(ref == 0.0)
+    out = {}
+    for rs in (True, False):
+        ho = bridge.attention_ex(*hs, batch=1, heads=1, sq=1, sk=sk, d=d, scale=scale, causal=False,
+                                 in_dtype=dtype, out_dtype="float32", round_scores=rs)
+        out[rs] = bridge.to_numpy(ho)
+    assert np.all(out[True] == 0.0), out[True][..., :4]
+    assert np.all(out[False] < 0.0), out[False][..., :4]
+    assert O.within(out[False], ref, TOL16).all()
+
+
+def test_attention_large_scale_routes_around_prescaled_q(bridge, rng):
+    """scale * log2(e) > 1 would let Q' = Q * scale * log2(e) overflow f16 in
+    the pre-scaling kernel; such calls must still match the oracle."""
+    b, h, s, d = 1, 2, 96, 64
+    q = (rng.standard_normal((b, h, s, d)) * 2000).astype(np.float16)
+    k = (rng.standard_normal((b, h, s, d)) * 1e-3).astype(np.float16)
+    v = rng.standard_normal((b, h, s, d)).astype(np.float16)
+    hq, hk, hv = up(bridge, q), up(bridge, k), up(bridge, v)
+    # S rounded as the reference graph does -> the oracle; S kept in f32 ->
+    # float64 attention over the same f16 inputs (at this scale the f16
+    # rounding of S moves the softmax by more than the tolerance).
+    refs = {True: O.sdpa_amp(q, k, v, 40.0, True).astype(np.float32),
+            False: O.attention_f64(q, k, v, 40.0, causal=True)}
+    for rs, ref in refs.items():
+        ho = bridge.attention_ex(hq, hk, hv, batch=b, heads=h, sq=s, sk=s, d=d, scale=40.0, causal=True,
+                                 in_dtype="float16", round_scores=rs)
+        y = bridge.to_numpy(ho).astype(np.float32)
+        assert np.isfinite(y).all()
+        assert O.within(y, ref, TOL16).all(), (rs, O.report(y, ref, TOL16))

@@ -160,6 +160,8 @@ SIGNATURES = {
     "bg_flash_attention": (C.c_int, [ctx_p, handle_t, handle_t, handle_t, handle_t, C.c_int64, C.c_int64,
                                      C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_int, PH]),
     "bg_matmul_ex": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), PH]),
+    "bg_matmul_noalloc": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.c_void_p]),
     "bg_fused_ex": (C.c_int, [ctx_p, C.POINTER(FusedDesc), PH]),
     "bg_attention_ex": (C.c_int, [ctx_p, C.POINTER(AttentionDesc), PH]),
     "bg_layer_norm": (C.c_int, [ctx_p, handle_t, handle_t, handle_t, C.c_int64, C.c_int64, C.c_float, C.c_int, PH]),

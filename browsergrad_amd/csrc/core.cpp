@@ -292,6 +292,7 @@ int bg_ctx_create(int device, int profiling, bg_ctx** out) {
     delete ctx;
     return BG_E_HIP;
   }
+  noalloc_setup(ctx);
   *out = ctx;
   return BG_OK;
 }

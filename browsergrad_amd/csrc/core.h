@@ -92,6 +92,12 @@ struct bg_ctx {
   // elementwise epilogue pass.
   void* scratch[2] = {nullptr, nullptr};
   size_t scratch_bytes[2] = {0, 0};
+
+  // Device address of this device's fixed no-allocation scratch (NULL when
+  // it could not be resolved; bg_matmul_noalloc then refuses).
+  char* noalloc_scratch = nullptr;
+  size_t noalloc_scratch_bytes = 0;
+  std::string noalloc_error;
 };
 
 namespace bg {
@@ -194,6 +200,24 @@ void launch_softmax_last(bg_ctx* ctx, const void* x, int x_dtype, void* y, int y
                          int64_t rows, int64_t cols);
 void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a,
                    const Record& b, const Record* bias, Record& out);
+// Device scratch for one GEMM call's pre- and post-passes: the context's
+// growable slots (fixed == NULL), or a fixed region of cap bytes handed out
+// front to back (the no-allocation entry point).
+struct GemmWorkspace {
+  bg_ctx* ctx;
+  char* fixed = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+  void* get(size_t bytes, int slot);
+};
+// The GEMM on raw device pointers (a, b: operand storage, d.offset_a /
+// d.offset_b applied inside; bias f32 [N] or NULL; c: the output with d.ldc /
+// d.stride_c already resolved).
+void run_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char* b, const float* bias, void* c,
+                GemmWorkspace& ws);
+// Resolves this device's no-allocation scratch address (noalloc.hip); called
+// by bg_ctx_create with the context's device current.
+void noalloc_setup(bg_ctx* ctx);
 void launch_attention(bg_ctx* ctx, const bg_attention_desc& d,
                       const Record& q, const Record& k, const Record& v,
                       Record& out);

@@ -827,11 +827,11 @@ namespace bg {
 // GEMM launch with C described by (c, ldc, stride_c, out_dtype, act).
 // True when run_gemm would pick a kernel whose epilogue applies GELU (the
 // direct-to-LDS kernel with 128-wide wavefront tiles).
-static bool gelu_in_epilogue(const bg_matmul_desc& d, const Record& a, const Record& b) {
+static bool gelu_in_epilogue(const bg_matmul_desc& d, const char* a, const char* b) {
   if (d.in_dtype == BG_F32 || !d.trans_b) return false;
   const int64_t es = dtype_size(d.in_dtype);
-  const void* A = a.ptr() + d.offset_a * es;
-  const void* B = b.ptr() + d.offset_b * es;
+  const void* A = a + d.offset_a * es;
+  const void* B = b + d.offset_b * es;
   const bool vec = aligned_to(A, 16) && aligned_to(B, 16) && d.k % 8 == 0 && d.lda % 8 == 0 &&
                    d.ldb % 8 == 0 && d.stride_a % 8 == 0 && d.stride_b % 8 == 0;
   const int64_t a_span = ((d.m - 1) * d.lda + d.k) * es;
@@ -841,13 +841,15 @@ static bool gelu_in_epilogue(const bg_matmul_desc& d, const Record& a, const Rec
   return c != LdsCfg::T256x256x64s2 && c != LdsCfg::T256x256x32s4;
 }
 
-static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
-                     const Record* bias, void* c, int64_t ldc, int64_t stride_c, int out_dtype, int act) {
+// a / b point at the operands' storage (d.offset_a / d.offset_b are applied
+// here); bias is f32 [N] or NULL.
+static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char* b, const float* bias,
+                     void* c, int64_t ldc, int64_t stride_c, int out_dtype, int act, GemmWorkspace& ws) {
   const int64_t es = dtype_size(d.in_dtype);
   GemmArgs P{};
-  P.A = a.ptr() + d.offset_a * es;
-  P.B = b.ptr() + d.offset_b * es;
-  P.bias = bias ? reinterpret_cast<const float*>(bias->ptr()) : nullptr;
+  P.A = a + d.offset_a * es;
+  P.B = b + d.offset_b * es;
+  P.bias = bias;
   P.C = c;
   P.M = d.m;
   P.N = d.n;
@@ -886,7 +888,7 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
       const int64_t splits = std::min<int64_t>(64, (nk + 1) / 2);
       P.k_chunk = ((nk + splits - 1) / splits) * BK32;
       const int64_t used = (d.k + P.k_chunk - 1) / P.k_chunk;
-      P.ws = static_cast<float*>(scratch(ctx, size_t(used * d.m * d.n * 4)));
+      P.ws = static_cast<float*>(ws.get(size_t(used * d.m * d.n * 4), 0));
       dim3 grid(unsigned(tiles), unsigned(used), 1);
       if (d.trans_b) {
         if (aligned) bg::dispatch(ctx, gemm32_kernel<128, 128, true, true>, grid, dim3(256), 0, P);
@@ -910,7 +912,7 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
   if (!d.trans_b) {
     const int64_t nb = d.stride_b == 0 ? 1 : d.batch;
     const size_t need = size_t(nb * d.n * d.k * es);
-    void* tb = scratch(ctx, need);
+    void* tb = ws.get(need, 0);
     {
       Profile prof(ctx, "gemm_b_transpose", 2 * nb * d.n * d.k * es, 0);
       if (d.ldb == d.n && (nb == 1 || d.stride_b == d.k * d.n)) {
@@ -974,26 +976,47 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, cons
   }
 }
 
-void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
-                   const Record* bias, Record& out) {
+void* GemmWorkspace::get(size_t bytes, int slot) {
+  if (!fixed) return scratch(ctx, bytes, slot);
+  const size_t off = (used + 255) & ~size_t(255);
+  if (off > cap || bytes > cap - off) {
+    fail(BG_E_UNSUPPORTED, "matmul_noalloc: this problem needs " + std::to_string(off + bytes) +
+                               " bytes of scratch, above the fixed " + std::to_string(cap) +
+                               "-byte no-allocation scratch");
+  }
+  used = off + bytes;
+  return fixed + off;
+}
+
+// Every workspace request of a call comes before its first kernel launch, so
+// a refused request leaves nothing queued.
+void run_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char* b, const float* bias, void* c,
+                GemmWorkspace& ws) {
   if (d.batch > 65535) fail(BG_E_UNSUPPORTED, "matmul: batch > 65535");
   if (d.act != BG_ACT_GELU_TANH || gelu_in_epilogue(d, a, b)) {
-    run_gemm(ctx, d, a, b, bias, out.ptr(), d.ldc, d.stride_c, d.out_dtype, d.act);
+    run_gemm(ctx, d, a, b, bias, c, d.ldc, d.stride_c, d.out_dtype, d.act, ws);
     return;
   }
   // GELU follows the (rounded, biased) product in f32, as the reference
   // graph evaluates it: the GEMM leaves f32 in C (or in scratch when C is
   // 16-bit), then one elementwise pass applies GELU and stores C's dtype.
-  float* f = reinterpret_cast<float*>(out.ptr());
+  float* f = reinterpret_cast<float*>(c);
   int64_t ldf = d.ldc, sf = d.stride_c;
   if (d.out_dtype != BG_F32) {
-    f = static_cast<float*>(scratch(ctx, size_t(d.batch * d.m * d.n * 4), 1));
+    f = static_cast<float*>(ws.get(size_t(d.batch * d.m * d.n * 4), 1));
     ldf = d.n;
     sf = d.m * d.n;
   }
-  run_gemm(ctx, d, a, b, bias, f, ldf, sf, BG_F32, BG_ACT_NONE);
+  run_gemm(ctx, d, a, b, bias, f, ldf, sf, BG_F32, BG_ACT_NONE, ws);
   Profile prof(ctx, "gemm_gelu", d.batch * d.m * d.n * (4 + dtype_size(d.out_dtype)), 0);
-  launch_gelu_rows(ctx, f, ldf, sf, out.ptr(), d.ldc, d.stride_c, d.out_dtype, d.batch, d.m, d.n);
+  launch_gelu_rows(ctx, f, ldf, sf, c, d.ldc, d.stride_c, d.out_dtype, d.batch, d.m, d.n);
+}
+
+void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
+                   const Record* bias, Record& out) {
+  GemmWorkspace ws{ctx};
+  run_matmul(ctx, d, a.ptr(), b.ptr(), bias ? reinterpret_cast<const float*>(bias->ptr()) : nullptr, out.ptr(),
+             ws);
 }
 
 }  // namespace bg

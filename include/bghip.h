@@ -333,6 +333,21 @@ int bg_conv2d_backward_bias(bg_ctx* ctx, bg_handle dy, int64_t n,
 
 /* ---- extensions --------------------------------------------------------- */
 int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out);
+/* No counterpart in the reference.  bg_matmul_ex for callers that cannot
+ * allocate device memory (HIP graph capture, serving loops that forbid
+ * hipMalloc): a, b, bias (f32 [N] or NULL) and c are caller-owned device
+ * pointers (desc->a, ->b, ->bias must be 0; offset_a / offset_b, lda, ldb,
+ * ldc, strides as in bg_matmul_ex, ldc / stride_c 0 = contiguous), the
+ * caller sizes them (no extent check is possible), and the call allocates
+ * nothing: no handle, no profiling event, and the kernels' scratch comes
+ * from a fixed 16 MiB array per GPU held until the process ends.  Problems
+ * that need more scratch (split-K partials of long-K f32 GEMMs, the
+ * re-laid-out B of x @ w, the f32 product before a separate GELU pass) are
+ * refused with BG_E_UNSUPPORTED before anything is launched.  The array is
+ * shared by every call on one GPU: calls that overlap on one GPU (different
+ * contexts or threads) race; calls on one context are stream ordered. */
+int bg_matmul_noalloc(bg_ctx* ctx, const bg_matmul_desc* desc, const void* a, const void* b,
+                      const float* bias, void* c);
 int bg_fused_ex(bg_ctx* ctx, const bg_fused_desc* desc, bg_handle* out);
 int bg_attention_ex(bg_ctx* ctx, const bg_attention_desc* desc, bg_handle* out);
 /* LayerNorm over rows x cols (tensor_plan.ts:2170-2208; oracle

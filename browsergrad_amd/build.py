@@ -39,6 +39,10 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source additions to HIP_FLAGS (none at present).
+FILE_FLAGS: dict[str, list[str]] = {}
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(
@@ -58,7 +62,7 @@ def compile_sources(jobs: int = 8) -> list[Path]:
 
     def one(src: Path) -> Path:
         obj = BUILD / (src.name + ".o")
-        cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
         if src.suffix == ".cpp":
             cmd[1:1] = ["-x", "hip"]
         _run(cmd)

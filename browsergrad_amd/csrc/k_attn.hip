@@ -687,14 +687,14 @@ __global__ void __launch_bounds__(kFa2NW * 64, 1) fa2_fwd_kernel(Fa2Args P, uint
 // slot j % 4, step t refills the slot of tile t-1 with tile t+3 after the
 // step's barrier).  Each wavefront works through a tile in two 32-key halves:
 //   x  = K Q'^T + (-m)       4 MFMAs (32x32x16), Q' = Q * scale * log2(e)
-//   P  = exp2(x)             packed to 16 bits, row sum by v_dot2 on the packed P
+//   P  = exp2(x)             packed to 16 bits, row sum in f32 by adds
 //   O^T += V^T P^T           4 MFMAs, V^T fragments by ds_read_b64_tr_b16
 // Q' is rounded to the input dtype once per wavefront, and the S chain starts
 // from an accumulator block holding -m (the wavefront's reference max per
 // query), so the fast path has no per-score FMA and no per-tile max.  The
 // reference max only has to keep P finite in 16 bits: it is set exactly on
 // the first half a wavefront sees and moved again only when some P of a half
-// overflows (its f32 row sum then exceeds 2^20); that slow path takes the
+// may overflow (its f32 row sum reaches 2^15); that slow path takes the
 // exact max, rescales O and l and recomputes P.  At 124 registers two
 // workgroups share a CU, four wavefronts per SIMD, which hides MFMA, LDS and
 // transcendental latency across wavefronts.
@@ -766,9 +766,13 @@ __device__ __forceinline__ float16v fa6_scores_half(const char* kt, const Fa6Off
 // P = exp2(x + delta) packed as two B fragments; returns the row sum of the
 // packed values.
 template <bool BF16, bool ADD>
+// The row sum is taken over the f32 values before the 16-bit rounding, with
+// plain adds in two chains: v_dot2 on the packed P does not issue beside
+// MFMAs (measured on MI355X: two dot2 per MFMA stretch the MFMA issue
+// interval from 14.8 to 24.9 ns, while adds, converts and two v_exp_f32 per
+// MFMA fit inside it).
 __device__ __forceinline__ float fa6_exp(const float16v& x, float delta, fa_u4 (&pf)[2]) {
-  const fa_h2 ones = {(_Float16)1.f, (_Float16)1.f};
-  float l_acc = 0.f;
+  float l0 = 0.f, l1 = 0.f;
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm) {
     uint32_t pk[4];
@@ -777,13 +781,14 @@ __device__ __forceinline__ float fa6_exp(const float16v& x, float delta, fa_u4 (
       const int e = mm * 8 + 2 * j;
       const float x0 = ADD ? x[e] + delta : x[e];
       const float x1 = ADD ? x[e + 1] + delta : x[e + 1];
-      pk[j] = fa2_pack<BF16>(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
-      if constexpr (BF16) l_acc += fa2_lo<true>(pk[j]) + fa2_hi<true>(pk[j]);
-      else l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(fa_h2, pk[j]), ones, l_acc, false);
+      const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
+      l0 += e0;
+      l1 += e1;
+      pk[j] = fa2_pack<BF16>(e0, e1);
     }
     pf[mm] = fa_u4{pk[0], pk[1], pk[2], pk[3]};
   }
-  return l_acc;
+  return l0 + l1;
 }
 
 template <bool BF16, bool CAUSAL>
@@ -878,7 +883,10 @@ __global__ void __launch_bounds__(kFa2NW * 64, 2) fa6_fwd_kernel(Fa2Args P, uint
         }
         fa_u4 pf[2];
         float l_acc = fa6_exp<BF16, false>(x, 0.f, pf);
-        if (__any(l_acc > 1048576.f || m_run == -INFINITY)) {  // wave-uniform
+        // The f32 sum bounds every P of the half, so a sum below 2^15 means
+        // no P reached the f16 limit; otherwise (or on the first half)
+        // take the exact maximum and recompute P.
+        if (__any(!(l_acc < 32768.f) || m_run == -INFINITY)) {  // wave-uniform
           // Exact max of this half (x = scores - m_use), moved reference.
           float mt = -INFINITY;
 #pragma unroll

@@ -27,6 +27,31 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t v) {
   return static_cast<float>(__builtin_bit_cast(_Float16, v));
 }
 
+// x + (x of another lane chosen by the DPP control word CTRL).  Every
+// control used below names a lane inside the same row of 16, so all lanes
+// read a valid source.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wavefront, the same value in every lane: inside
+// each row of 16 lanes, quad_perm swaps of neighbours (0xB1) and pairs (0x4E)
+// and row rotations by 4 (0x124) and 8 (0x128); then the four row sums as
+// read from lanes 0, 16, 32, 48.  Costs no LDS traffic, unlike ds_bpermute
+// shuffles.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = dpp_add<0xB1>(x);
+  x = dpp_add<0x4E>(x);
+  x = dpp_add<0x124>(x);
+  x = dpp_add<0x128>(x);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // dtype codes follow include/bghip.h (0 f32, 1 f16, 2 bf16).
 __device__ __forceinline__ float load_as_f32(const void* p, int dtype, int64_t i) {
   if (dtype == 0) return static_cast<const float*>(p)[i];

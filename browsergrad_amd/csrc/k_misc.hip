@@ -215,6 +215,104 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict_
   }
 }
 
+// Vectorised LayerNorm for rows whose width is a multiple of 4: a wavefront
+// per row, the row in registers as NV groups of 4 consecutive columns per
+// lane (16-byte f32 or 8-byte 16-bit loads and stores), input and output
+// dtypes fixed at compile time.  Same operation order as layer_norm_kernel:
+// mean, centred values, mean of squares, 1/sqrt(var + eps), x_hat * w + b.
+template <int D>
+__device__ __forceinline__ float4 ln_load4(const void* __restrict__ p, int64_t g) {
+  if constexpr (D == BG_F32) {
+    return reinterpret_cast<const float4*>(p)[g];
+  } else {
+    const uint2 u = reinterpret_cast<const uint2*>(p)[g];
+    if constexpr (D == BG_F16) {
+      return make_float4(f16_bits_to_f32(uint16_t(u.x)), f16_bits_to_f32(uint16_t(u.x >> 16)),
+                         f16_bits_to_f32(uint16_t(u.y)), f16_bits_to_f32(uint16_t(u.y >> 16)));
+    } else {
+      return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                         __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void ln_store4(void* __restrict__ p, int64_t g, float4 v) {
+  if constexpr (D == BG_F32) {
+    reinterpret_cast<float4*>(p)[g] = v;
+  } else if constexpr (D == BG_F16) {
+    reinterpret_cast<uint2*>(p)[g] =
+        make_uint2(uint32_t(f32_to_f16_bits(v.x)) | (uint32_t(f32_to_f16_bits(v.y)) << 16),
+                   uint32_t(f32_to_f16_bits(v.z)) | (uint32_t(f32_to_f16_bits(v.w)) << 16));
+  } else {
+    reinterpret_cast<uint2*>(p)[g] =
+        make_uint2(uint32_t(f32_to_bf16_bits(v.x)) | (uint32_t(f32_to_bf16_bits(v.y)) << 16),
+                   uint32_t(f32_to_bf16_bits(v.z)) | (uint32_t(f32_to_bf16_bits(v.w)) << 16));
+  }
+}
+
+template <int XD, int YD, int NV, int RW>
+__global__ void __launch_bounds__(256) layer_norm_vec_kernel(const void* __restrict__ x,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ bias,
+                                                             void* __restrict__ y, int64_t rows,
+                                                             int64_t cols, float eps) {
+  // RW rows per wavefront, their loads issued together; w and b are read
+  // once per wavefront, before the row statistics need them.
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RW;
+  if (row0 >= rows) return;  // no block-level barriers below
+  const int64_t groups = cols >> 2;  // groups of 4 columns
+  float4 v[RW][NV], wv[NV], bv[NV];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t g = int64_t(j) * 64 + lane;
+      v[r][j] = g < groups && row0 + r < rows ? ln_load4<XD>(x, (row0 + r) * groups + g)
+                                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t g = int64_t(j) * 64 + lane;
+    wv[j] = g < groups ? reinterpret_cast<const float4*>(w)[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+    bv[j] = g < groups ? reinterpret_cast<const float4*>(bias)[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float inv[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) s += (v[r][j].x + v[r][j].y) + (v[r][j].z + v[r][j].w);
+    const float mean = wave_sum(s) / float(cols);
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t g = int64_t(j) * 64 + lane;
+      v[r][j] = make_float4(v[r][j].x - mean, v[r][j].y - mean, v[r][j].z - mean, v[r][j].w - mean);
+      if (g < groups)
+        q += (v[r][j].x * v[r][j].x + v[r][j].y * v[r][j].y) + (v[r][j].z * v[r][j].z + v[r][j].w * v[r][j].w);
+    }
+    const float var = wave_sum(q) / float(cols);
+    inv[r] = 1.0f / sqrtf(var + eps);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    if (row0 + r >= rows) break;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t g = int64_t(j) * 64 + lane;
+      if (g < groups) {
+        const float4 a = v[r][j];
+        ln_store4<YD>(y, (row0 + r) * groups + g,
+                      make_float4(a.x * inv[r] * wv[j].x + bv[j].x, a.y * inv[r] * wv[j].y + bv[j].y,
+                                  a.z * inv[r] * wv[j].z + bv[j].z, a.w * inv[r] * wv[j].w + bv[j].w));
+      }
+    }
+  }
+}
+
 // Fallback for very wide rows: three passes over global memory.
 __global__ void __launch_bounds__(256) layer_norm_wide_kernel(const void* __restrict__ x, int xd,
                                                               const float* __restrict__ w,
@@ -489,10 +587,52 @@ void launch_softmax_last(bg_ctx* ctx, const void* x, int xd, void* y, int yd, in
   }
 }
 
+template <int NV>
+static bool launch_layer_norm_vec(bg_ctx* ctx, const void* x, int xd, const float* w, const float* b, void* y,
+                                  int yd, int64_t rows, int64_t cols, float eps) {
+  // Two rows per wavefront up to 1024 columns (4 waves, 8 rows a block).
+  constexpr int RW = NV <= 4 ? 2 : 1;
+  const dim3 grid(unsigned((rows + 4 * RW - 1) / (4 * RW)));
+#define BG_LNV(XD_, YD_) \
+  bg::dispatch(ctx, layer_norm_vec_kernel<XD_, YD_, NV, RW>, grid, dim3(256), 0, x, w, b, y, rows, cols, eps)
+#define BG_LNV_Y(XD_)                         \
+  switch (yd) {                               \
+    case BG_F32: BG_LNV(XD_, BG_F32); break;  \
+    case BG_F16: BG_LNV(XD_, BG_F16); break;  \
+    case BG_BF16: BG_LNV(XD_, BG_BF16); break; \
+    default: return false;                    \
+  }
+  switch (xd) {
+    case BG_F32: BG_LNV_Y(BG_F32); break;
+    case BG_F16: BG_LNV_Y(BG_F16); break;
+    case BG_BF16: BG_LNV_Y(BG_BF16); break;
+    default: return false;
+  }
+#undef BG_LNV_Y
+#undef BG_LNV
+  return true;
+}
+
 void launch_layer_norm(bg_ctx* ctx, const void* x, int xd, const float* w, const float* b,
                        void* y, int yd, int64_t rows, int64_t cols, float eps) {
   if (rows == 0) return;
   const dim3 grid(unsigned((rows + 3) / 4));
+  // Vector path: 4-column groups aligned for the row's loads and stores.
+  const auto al = [](const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+  const int64_t xs = dtype_size(xd), ys = dtype_size(yd);
+  if (cols % 4 == 0 && cols <= 4 * 64 * 8 && al(x, 4 * xs) && al(y, 4 * ys) && al(w, 16) && al(b, 16)) {
+    const int64_t nv = (cols / 4 + 63) / 64;
+    bool ok = false;
+    if (nv <= 1) ok = launch_layer_norm_vec<1>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    else if (nv <= 2) ok = launch_layer_norm_vec<2>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    else if (nv <= 3) ok = launch_layer_norm_vec<3>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    else if (nv <= 4) ok = launch_layer_norm_vec<4>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    else ok = launch_layer_norm_vec<8>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    if (ok) {
+      hip_check(hipGetLastError(), "layer_norm launch");
+      return;
+    }
+  }
   if (cols <= 256) {
     bg::dispatch(ctx, layer_norm_kernel<4>, grid, dim3(256), 0, x, xd, w, b, y, yd,
                        rows, cols, eps);

@@ -167,6 +167,50 @@ def test_layer_norm(bridge, rng, rows, cols):
     assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)
 
 
+def _to16(x, dtype):
+    return x.astype(np.float16) if dtype == "float16" else O.f32_to_bf16_bits(x)
+
+
+def _from16(y, dtype):
+    return y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
+
+
+# Widths for every register-group count of the vector path (1, 2, 3, 4, 8
+# groups of 4 columns per lane), its widest row (2048), and widths that take
+# the scalar kernels (not a multiple of 4, wider than 2048).
+@pytest.mark.parametrize("cols", [4, 200, 512, 768, 1024, 1028, 2048, 2052, 766])
+@pytest.mark.parametrize("in_dtype,out_dtype", [("float32", "float32"), ("float16", "float16"),
+                                                ("bfloat16", "bfloat16"), ("float32", "float16"),
+                                                ("float16", "float32"), ("bfloat16", "float32")])
+def test_layer_norm_dtypes(bridge, rng, cols, in_dtype, out_dtype):
+    rows = 37
+    x = (rng.standard_normal((rows, cols)) * 3 + 1).astype(np.float32)
+    w = rng.standard_normal(cols).astype(np.float32)
+    b = rng.standard_normal(cols).astype(np.float32)
+    if in_dtype == "float32":
+        hx = up(bridge, x)
+    else:
+        x16 = _to16(x, in_dtype)
+        hx = up(bridge, x16, in_dtype)
+        x = _from16(x16, in_dtype)
+    h = bridge.layer_norm(hx, up(bridge, w), up(bridge, b), rows, cols, 1e-5, out_dtype=out_dtype)
+    ref = O.layer_norm(x, w, b, 1e-5)
+    y = bridge.to_numpy(h)
+    if out_dtype == "float32":
+        assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)
+    else:
+        # One rounding of the f32 result to the output dtype (nearest even).
+        r16 = _to16(ref, out_dtype)
+        y32, r32 = _from16(y, out_dtype), _from16(r16, out_dtype)
+        assert O.within(y32, r32, TOL16).all(), O.report(y32, r32, TOL16)
+        # Away from zero (where the f32 result's absolute error of ~1e-6 is
+        # many 16-bit ulps) most elements round identically, and none lands
+        # more than one code away.
+        big = np.abs(r32) >= 0.25
+        ulp = np.abs(y.view(np.uint16).astype(np.int32) - r16.view(np.uint16).astype(np.int32))[big]
+        assert (ulp <= 1).all() and (ulp == 0).mean() > 0.99
+
+
 def test_copy_strided_permute(bridge, rng):
     x = rng.standard_normal((2, 5, 3, 4)).astype(np.float32)
     h = up(bridge, x)

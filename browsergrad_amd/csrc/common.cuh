@@ -74,24 +74,27 @@ __device__ __forceinline__ float round_through(float x, int dtype) {
   return x;
 }
 
-// The reference's tanh-approximate GELU, op for op in f32
-// (_functional.py:123-134 with tanh from _functional.py:115-120):
-//   0.5*x * (1 + (e^u - e^-u)/(e^u + e^-u)),  u = c*(x + ((0.044715*x)*x)*x)
-__device__ __forceinline__ float gelu_tanh_ref(float x) {
-  const float c = 0.7978845608028654f;  // sqrt(2/pi) rounded to f32
-  float half_x = 0.5f * x;
+// The reference's tanh-approximate GELU (_functional.py:123-134, tanh from
+// _functional.py:115-120): 0.5*x * (1 + tanh u), u = c*(x + ((0.044715*x)*x)*x),
+// tanh u = (e^u - e^-u)/(e^u + e^-u), every op in f32.  Evaluated as the
+// equal x * e/(e + 1) with e = e^(2u): one v_exp_f32 and one v_rcp_f32 in
+// place of two library exponentials and an IEEE divide, within a few ulp of
+// the reference form and without its cancellation near u = 0.  The
+// reference form is NaN exactly where one of its f32 exponentials overflows,
+// |u| >= 88.72283935546875 (the least f32 whose exp rounds past FLT_MAX),
+// and for NaN or infinite x; so is this one: e is taken at min(u, 40), where
+// e/(e + 1) is already 1 in f32, and |u| past the threshold (or NaN) yields
+// NaN.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;      // sqrt(2/pi) rounded to f32
+  const float two_log2e = 2.8853900817779268f;  // 2 * log2(e)
   float cube = 0.044715f * x;
   cube = cube * x;
   cube = cube * x;
-  float inner = x + cube;
-  float u = c * inner;
-  float ep = expf(u);
-  float en = expf(-u);
-  float num = ep + (-en);
-  float den = ep + en;
-  float th = num / den;
-  float one_plus = 1.0f + th;
-  return half_x * one_plus;
+  const float u = c * (x + cube);
+  const float e = __builtin_amdgcn_exp2f(fminf(u, 40.0f) * two_log2e);
+  const float g = x * (e * __builtin_amdgcn_rcpf(e + 1.0f));
+  return fabsf(u) < 88.72283935546875f ? g : __builtin_nanf("");
 }
 
 // Raw buffer descriptor in four SGPRs: 48-bit base, stride 0, size in bytes

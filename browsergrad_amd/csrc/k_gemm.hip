@@ -87,7 +87,7 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs& P, float v, floa
   if (P.round_dtype) v = round_through(v, P.round_dtype);
   if (P.bias) v = v + bias;
   if (P.act == BG_ACT_RELU) v = v > 0.f ? v : 0.f;
-  else if (P.act == BG_ACT_GELU_TANH) v = gelu_tanh_ref(v);
+  else if (P.act == BG_ACT_GELU_TANH) v = gelu_tanh(v);
   return v;
 }
 
@@ -102,9 +102,10 @@ __device__ __forceinline__ void store_elem(char* p, float v) {
 // (16 values per lane) at a time: [round to the 16-bit type] -> [+ bias[n]]
 // -> [relu] -> store, each stage behind one uniform branch per tile.
 // Scheduling fences between tiles keep the live set to one tile, so the
-// accumulators never spill.  tanh-GELU is applied by a separate elementwise
-// pass over C (launch_matmul): its exponentials and divide would swamp the
-// store stream.
+// accumulators never spill.  tanh-GELU (one exponential and one reciprocal
+// per element) runs here for wavefront tiles of up to kGeluEpilogueTiles
+// accumulator tiles; wider ones leave it to a separate f32 pass over C
+// (run_matmul).
 // 32x32 MFMA accumulator layout: lane l, register e holds row
 // 8*(e/4) + 4*(l/32) + e%4, column l%32, so each store instruction writes 32
 // consecutive columns of two rows.  Addresses are a uniform per-row base plus
@@ -150,7 +151,7 @@ __device__ __forceinline__ void epilogue_tiles(const GemmArgs& P, char* C, float
         // registers for it and take the separate f32 pass instead.
         if (P.act == BG_ACT_GELU_TANH) {
 #pragma unroll
-          for (int e = 0; e < 16; ++e) v[e] = gelu_tanh_ref(v[e]);
+          for (int e = 0; e < 16; ++e) v[e] = gelu_tanh(v[e]);
         }
       }
       const bool col_ok = FULL || cl + j * 32 < P.N;
@@ -798,22 +799,24 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch, int act) {
     if (v == "256x256x32s4w8") return LdsCfg::T256x256x32s4w8;
     if (v == "256x128x64s3w8") return LdsCfg::T256x128x64s3w8;
   }
-  // Measured on MI355X (wall clock, 50 back-to-back launches per shape):
-  //   4096^3:          256x256x32/4 stages, 8 wavefronts  135.0 us
-  //                    (256x256x64/2, 4 wavefronts 148.5; 128x128x64/2 160.0)
-  //   8192x3072x768:   256x256x64/2, 8 wavefronts         51.9 us (128x128: 54.0)
-  //   8192x2304x768:   128x128x64/2                        44.5 us (256x256 w8: 45.7)
-  //   8192x768x768:    256x128x64/3, 8 wavefronts         16.7 us (128x128: 17.6)
-  //   8192x768x3072:   256x128x64/3, 8 wavefronts         49.4 us (128x128: 50.0)
-  // Deep K with a full wave of 256x256 tiles takes the deepest pipeline;
-  // 1.25+ waves of 256x256 tiles take them with two wavefronts per SIMD;
-  // narrow outputs (N <= 1024) take 256x128; the rest 128x128, two
-  // workgroups per CU.
-  // With tanh-GELU in the epilogue (two exponentials and a divide per
-  // element) 128x128 tiles win: 8192x3072x768 + bias + GELU 75.1 us vs
-  // 91.0 us for 256x256 w8, whose 1.5 waves of tiles expose the epilogue.
+  // Measured on MI355X (kernel time, configurations interleaved round-robin
+  // so that all share one thermal state; f16 out, + bias):
+  //   4096^3:          256x256x64/2 stages, 8 wavefronts  116.1 us
+  //                    (256x256x32/4 w8 120.8; 256x128x64/3 w8 131.2;
+  //                    128x128x64/2 137.5; f32 out: 120.6 vs 124.7)
+  //   8192x2304x768:   128x128x64/2                        42.4 us
+  //                    (256x128 w8 44.2; 256x256 w8 45.9)
+  //   8192x768x768:    256x128x64/3, 8 wavefronts         16.2 us (128x128: 17.4)
+  //   8192x768x3072:   256x128x64/3, 8 wavefronts         43.7 us (128x128: 46.1)
+  //   8192x3072x768 + GELU: 128x128x64/2                  57.3 us
+  //                    (256x128 w8 58.7; 256x256 w8 61.2)
+  // 1+ waves of 256x256 tiles take them with two wavefronts per SIMD (deep
+  // K) or 1.25+ waves (shallow K); narrow outputs (N <= 1024) take 256x128;
+  // the rest 128x128, two workgroups per CU.  With tanh-GELU in the epilogue
+  // 128x128 tiles keep the lead: their 8192x3072 grid is 6 waves of tiles,
+  // 256x256's 1.5 waves expose the epilogue.
   const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
-  if (t256 >= 256 && k >= 2048 && act != BG_ACT_GELU_TANH) return LdsCfg::T256x256x32s4w8;
+  if (t256 >= 256 && k >= 2048 && act != BG_ACT_GELU_TANH) return LdsCfg::T256x256x64s2w8;
   if (t256 >= 320 && act != BG_ACT_GELU_TANH) return LdsCfg::T256x256x64s2w8;
   const int64_t t256x128 = ((m + 255) / 256) * ((n + 127) / 128) * batch;
   if (n <= 1024 && t256x128 >= 128) return LdsCfg::T256x128x64s3w8;

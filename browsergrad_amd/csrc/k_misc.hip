@@ -500,7 +500,7 @@ __global__ void __launch_bounds__(256) gelu_rows_kernel(const float* __restrict_
     const int64_t b = rr / rows, r = rr - b * rows;
     const float* s = src + b * stride_src + r * ld_src;
     const int64_t o = b * stride_dst + r * ld_dst;
-    for (int64_t c = threadIdx.x; c < cols; c += 256) store_from_f32(dst, dd, o + c, gelu_tanh_ref(s[c]));
+    for (int64_t c = threadIdx.x; c < cols; c += 256) store_from_f32(dst, dd, o + c, gelu_tanh(s[c]));
   }
 }
 

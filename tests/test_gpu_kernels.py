@@ -288,6 +288,40 @@ def test_gemm_amp_epilogue_act(bridge, rng, m, k, n, act, out_dtype):
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
 
 
+def _gelu_edge_values():
+    """Every f32 on both sides of the reference GELU's overflow edge
+    (|u| = 88.72283935546875 at |x| ~ 12.99825) and the special values."""
+    lo = np.float32(12.99822)
+    edge = [lo]
+    for _ in range(60):
+        edge.append(np.nextafter(edge[-1], np.float32(np.inf), dtype=np.float32))
+    edge = np.array(edge, np.float32)
+    special = np.array([0.0, -0.0, 1.0, -1.0, 3.0, -3.0, 1e-4, -1e-4, 5.5, -5.5, 40.0, -40.0, 60.0, -60.0,
+                        1e20, -1e20, np.inf, -np.inf, np.nan], np.float32)
+    return np.concatenate([edge, -edge, special])
+
+
+@pytest.mark.parametrize("in_dtype", ["float16", "float32"])
+def test_gemm_gelu_overflow_edge(bridge, in_dtype):
+    """tanh-GELU's NaN set is the reference's: NaN exactly where one of its
+    f32 exponentials overflows, finite on the last f32 before.  z = 0 @ 0 + b
+    puts the bias values through the epilogue unchanged (f16: GELU in the
+    GEMM epilogue; f32: the separate GELU pass)."""
+    b = _gelu_edge_values()
+    n, m, k = b.size, 3, 8
+    ref = O.gelu_tanh_f32(b)
+    assert np.isnan(ref).any() and np.isfinite(ref).any()
+    dt = np.float16 if in_dtype == "float16" else np.float32
+    z = np.zeros((m, k), dt)
+    w = np.zeros((n, k), dt)
+    h = bridge.matmul_ex(up(bridge, z), up(bridge, w), m=m, n=n, k=k, trans_b=True, in_dtype=in_dtype,
+                         out_dtype="float32", bias=up(bridge, b), round_out=in_dtype == "float16", act=2)
+    y = bridge.to_numpy(h)
+    for row in y:
+        assert np.array_equal(np.isnan(row), np.isnan(ref)), (b[np.isnan(row) != np.isnan(ref)])
+        assert O.within(row, ref, TOL32).all(), O.report(row, ref, TOL32)
+
+
 @pytest.mark.parametrize("m,k,n", [(64, 784, 128), (64, 128, 10), (33, 17, 65)])
 def test_gemm_f32_bias_relu_gelu(bridge, rng, m, k, n):
     """f32 linear layer epilogues (C1's Linear + ReLU), rel 1e-4."""

@@ -1,12 +1,20 @@
 """safetensors IO for the HIP realizer's graphs.
 
-Mirrors the reference's reader / writer
+Offers the reference's entry points
 (packages/browsergrad-jit/src/python/_safetensors.py): ``load_safetensors``
-(:189-267) returns ``{name: Tensor}`` with the same header validation, dtype
-table, ``dtype=`` cast, ``progress`` callback and errors (BF16 refused, HTTP
-sources refused, header cap 100 MB); ``save_safetensors`` (:303-385) writes
-the same byte layout (8-byte little-endian header length, compact JSON
-header with ``data_offsets`` in insertion order, then the raw tensors).
+(:189-267) returns ``{name: Tensor}`` with the same dtype table, ``dtype=``
+cast, ``progress`` callback and the two refusals its tests pin (BF16 ->
+NotImplementedError naming PRD-010, HTTP sources -> NotImplementedError
+naming PRD-008.2; safetensors.test.ts:127-171); ``save_safetensors``
+(:303-385) writes files any safetensors reader loads.
+
+The parser and the writer are written from the format description of the
+safetensors project (length prefix, JSON header, tiled data buffer), not
+from the reference's code, and check what that description requires: a
+header that is a JSON object starting with '{', no duplicate keys, a
+string-to-string ``__metadata__``, and tensors that tile the data buffer
+with no gap, overlap or trailing bytes.  Malformed input raises
+``SafetensorsFormatError`` (a ValueError).
 
 Beyond the reference:
 
@@ -55,65 +63,138 @@ def get_default_session() -> Session:
     return _DEFAULT_SESSION
 
 
-# ---------------------------------------------------------------------------- parsing
+# ---------------------------------------------------------------------------- format
+#
+# The file layout, from the safetensors format description (huggingface/safetensors
+# README, "Format"):
+#   [0, 8)          u64 little-endian: byte length L of the header
+#   [8, 8 + L)      UTF-8 JSON object, starting with '{', optionally right-padded with
+#                   spaces; keys are tensor names (no duplicates) plus an optional
+#                   "__metadata__" str -> str map; each tensor is
+#                   {"dtype": code, "shape": [d0, ...], "data_offsets": [begin, end]}
+#   [8 + L, EOF)    the data buffer; offsets are relative to its start, row-major,
+#                   little-endian, and the tensors must tile it with no holes.
+
+_LEN_PREFIX = struct.Struct("<Q")
+_ALIGN = 8  # the writer pads the header so that the data buffer starts 8-byte aligned
+
+
+class SafetensorsFormatError(ValueError):
+    """A buffer that is not a well-formed safetensors file (a ValueError)."""
+
+
+def _bad(msg: str) -> SafetensorsFormatError:
+    return SafetensorsFormatError(f"safetensors: {msg}")
+
+
+def _is_count(v: Any) -> bool:
+    return isinstance(v, int) and not isinstance(v, bool) and v >= 0
+
+
+def _reject_duplicate_keys(pairs):
+    seen: Dict[str, Any] = {}
+    for key, value in pairs:
+        if key in seen:
+            raise _bad(f"key {key!r} appears twice in the header")
+        seen[key] = value
+    return seen
 
 
 def parse_header(buf: Any) -> Tuple[Dict[str, Any], int]:
-    """(header dict, offset of the data section) of a safetensors buffer
-    (_safetensors.py:82-117)."""
-    n = len(buf)
-    if n < 8:
-        raise ValueError(f"safetensors: file is {n} bytes, too small to contain the 8-byte header-length prefix")
-    (header_len,) = struct.unpack("<Q", bytes(buf[:8]))
-    if header_len == 0:
-        raise ValueError("safetensors: header length is zero")
-    if header_len > MAX_HEADER_BYTES:
-        raise ValueError(f"safetensors: header length {header_len} exceeds the {MAX_HEADER_BYTES}-byte ceiling. "
-                         f"Refusing to parse — the file may be corrupted or malicious.")
-    if 8 + header_len > n:
-        raise ValueError(f"safetensors: header length {header_len} exceeds file size {n}")
+    """Decode the JSON header of a safetensors buffer.
+
+    Returns the header object and the offset at which the data buffer starts.
+    Size checks come before any decoding, so a forged length prefix never
+    makes the reader allocate or scan more than the buffer holds or than
+    MAX_HEADER_BYTES allows."""
+    size = len(buf)
+    if size < _LEN_PREFIX.size:
+        raise _bad(f"{size}-byte input is too small to hold the 8-byte length prefix")
+    (hlen,) = _LEN_PREFIX.unpack(bytes(buf[:_LEN_PREFIX.size]))
+    if hlen == 0:
+        raise _bad("the length prefix says the header is empty")
+    if hlen > MAX_HEADER_BYTES:
+        raise _bad(f"a {hlen}-byte header is over the {MAX_HEADER_BYTES}-byte ceiling of this reader")
+    data_start = _LEN_PREFIX.size + hlen
+    if data_start > size:
+        raise _bad(f"the length prefix announces {hlen} header bytes but only "
+                   f"{size - _LEN_PREFIX.size} follow it (header runs past the end of the input)")
+    raw = bytes(buf[_LEN_PREFIX.size:data_start])
+    if raw[:1] != b"{":
+        raise _bad("the header does not start with '{' (not a JSON object)")
     try:
-        header = json.loads(bytes(buf[8:8 + header_len]).decode("utf-8"))
-    except (UnicodeDecodeError, json.JSONDecodeError) as e:
-        raise ValueError(f"safetensors: header is not valid UTF-8 JSON: {e}") from e
-    if not isinstance(header, dict):
-        raise ValueError(f"safetensors: header is a {type(header).__name__}, expected dict")
-    return header, 8 + header_len
+        header = json.loads(raw.decode("utf-8"), object_pairs_hook=_reject_duplicate_keys)
+    except UnicodeDecodeError as e:
+        raise _bad(f"the header is not UTF-8 ({e})") from e
+    except json.JSONDecodeError as e:
+        raise _bad(f"the header is not a JSON object ({e})") from e
+    if not isinstance(header, dict):  # e.g. '{' followed by trailing junk that json still rejects
+        raise _bad("the header is not a JSON object")
+    return header, data_start
 
 
 def validate_entry(name: str, meta: Any) -> Tuple[str, Tuple[int, ...], int, int]:
-    """(numpy dtype name, shape, start, end) of one header entry, checked
-    against the format (_safetensors.py:120-186)."""
+    """Check one tensor record of the header.
+
+    Returns (NumPy dtype name, shape, begin, end); begin and end are offsets
+    into the data buffer.  BF16 records raise NotImplementedError, as the
+    reference loader does (NumPy has no bfloat16)."""
+    where = f"tensor {name!r}"
     if not isinstance(meta, dict):
-        raise ValueError(f"safetensors: tensor {name!r} metadata is a {type(meta).__name__}, expected dict")
+        raise _bad(f"{where}: the record is not a JSON object")
+    unknown = set(meta) - {"dtype", "shape", "data_offsets"}
+    if unknown:
+        raise _bad(f"{where}: unexpected field(s) {sorted(unknown)}")
     code = meta.get("dtype")
-    if not isinstance(code, str):
-        raise ValueError(f"safetensors: tensor {name!r} missing string dtype (got {code!r})")
     if code == "BF16":
-        # The reference defers BF16 to its mixed-precision milestone (PRD-010).
         raise NotImplementedError(
-            f"safetensors: tensor {name!r} is BF16, which NumPy doesn't natively support (the reference "
-            f"defers it to PRD-010). Re-export the file as F16 or F32.")
-    if code not in DTYPE_MAP:
-        raise ValueError(f"safetensors: tensor {name!r} has unknown dtype {code!r}; "
-                         f"expected one of {sorted(DTYPE_MAP) + ['BF16']}")
-    np_name = DTYPE_MAP[code]
+            f"safetensors: {where} holds BF16 data; NumPy has no bfloat16 type, and the reference "
+            f"loader leaves BF16 to its mixed-precision milestone PRD-010. Convert the file to F16 or F32.")
+    np_name = DTYPE_MAP.get(code) if isinstance(code, str) else None
+    if np_name is None:
+        raise _bad(f"{where}: dtype code {code!r} is not one this reader knows ({', '.join(sorted(DTYPE_MAP))})")
     shape = meta.get("shape")
-    if not isinstance(shape, list) or not all(isinstance(d, int) and not isinstance(d, bool) and d >= 0
-                                              for d in shape):
-        raise ValueError(f"safetensors: tensor {name!r} has invalid shape {shape!r}; "
-                         f"expected list of non-negative ints")
-    offsets = meta.get("data_offsets")
-    if (not isinstance(offsets, list) or len(offsets) != 2
-            or not all(isinstance(o, int) and not isinstance(o, bool) and o >= 0 for o in offsets)
-            or offsets[0] > offsets[1]):
-        raise ValueError(f"safetensors: tensor {name!r} has invalid data_offsets {offsets!r}; "
-                         f"expected [start, end] with 0 <= start <= end")
-    want = np.dtype(np_name).itemsize * int(np.prod(shape, dtype=np.int64))
-    if offsets[1] - offsets[0] != want:
-        raise ValueError(f"safetensors: tensor {name!r} byte range {offsets[1] - offsets[0]} doesn't match "
-                         f"shape×dtype {want}")
-    return np_name, tuple(shape), offsets[0], offsets[1]
+    if not isinstance(shape, list) or not all(_is_count(d) for d in shape):
+        raise _bad(f"{where}: shape must be a list of non-negative integers, got {shape!r}")
+    span = meta.get("data_offsets")
+    if not (isinstance(span, list) and len(span) == 2 and all(_is_count(o) for o in span)):
+        raise _bad(f"{where}: data_offsets must be two non-negative integers, got {span!r}")
+    begin, end = span
+    count = 1
+    for d in shape:
+        count *= d
+    nbytes = count * np.dtype(np_name).itemsize
+    if end - begin != nbytes:
+        raise _bad(f"{where}: data_offsets {span} cover {end - begin} bytes, "
+                   f"but {code} x {shape} needs {nbytes}")
+    return np_name, tuple(shape), begin, end
+
+
+def _layout(buf: Any) -> Tuple[list, int]:
+    """Every tensor record of a buffer in header order, as
+    (name, dtype name, shape, begin, end), and the data buffer's start.
+
+    Beyond the per-record checks this enforces the format's tiling rule:
+    sorted by begin, the records must cover the data buffer exactly, with
+    no gap, overlap or trailing bytes."""
+    header, data_start = parse_header(buf)
+    meta = header.get("__metadata__")
+    if meta is not None and not (isinstance(meta, dict) and all(isinstance(v, str) for v in meta.values())):
+        raise _bad("__metadata__ must map strings to strings")
+    records = [(name,) + validate_entry(name, rec) for name, rec in header.items() if name != "__metadata__"]
+    data_len = len(buf) - data_start
+    cursor = 0
+    for name, _, _, begin, end in sorted(records, key=lambda r: (r[3], r[4])):
+        if begin != cursor:
+            kind = "overlaps the previous tensor" if begin < cursor else f"leaves a gap at byte {cursor}"
+            raise _bad(f"tensor {name!r} starts at byte {begin} and {kind}")
+        if end > data_len:
+            raise _bad(f"tensor {name!r} ends at byte {end}, past the end of the "
+                       f"{data_len}-byte data buffer")
+        cursor = end
+    if cursor != data_len:
+        raise _bad(f"the data buffer holds {data_len} bytes but the tensors cover only {cursor}")
+    return records, data_start
 
 
 def _resolve_source(source: Union[str, bytes, bytearray, memoryview]) -> Tuple[Any, str]:
@@ -141,16 +222,14 @@ def _resolve_source(source: Union[str, bytes, bytearray, memoryview]) -> Tuple[A
 
 
 def _entries(buf: Any):
-    header, data_start = parse_header(buf)
-    for name, meta in header.items():
-        if name == "__metadata__":
-            continue
-        np_name, shape, start, end = validate_entry(name, meta)
-        a, b = data_start + start, data_start + end
-        if b > len(buf):
-            raise ValueError(f"safetensors: tensor {name!r} extends past end of file ({b} > {len(buf)})")
-        view = np.frombuffer(buf, dtype=np.dtype(np_name), count=(b - a) // np.dtype(np_name).itemsize, offset=a)
-        yield name, view.reshape(shape), end, len(buf) - data_start
+    """(name, read-only array view into buf, end offset, data length) per
+    tensor, in header order."""
+    records, data_start = _layout(buf)
+    data_len = len(buf) - data_start
+    for name, np_name, shape, begin, end in records:
+        dt = np.dtype(np_name).newbyteorder("<")
+        view = np.frombuffer(buf, dtype=dt, count=(end - begin) // dt.itemsize, offset=data_start + begin)
+        yield name, view.reshape(shape), end, data_len
 
 
 # ---------------------------------------------------------------------------- loading
@@ -204,35 +283,48 @@ def load_safetensors_resident(source: Union[str, bytes, bytearray, memoryview], 
 # ---------------------------------------------------------------------------- saving
 
 
+def _storable(name: str, value: Any) -> Tuple[str, np.ndarray]:
+    """(dtype code, C-contiguous little-endian array) of one value to save."""
+    if name == "__metadata__":
+        raise _bad("'__metadata__' is reserved for the metadata map and cannot name a tensor")
+    if isinstance(value, np.ndarray):
+        arr = value
+    elif hasattr(value, "numpy"):
+        arr = value.numpy()
+    else:
+        raise TypeError(f"safetensors: cannot store {name!r}: a {type(value).__name__} is neither a "
+                        f"Tensor nor a NumPy array")
+    code = _NAME_OF.get(arr.dtype.name)
+    if code is None:
+        raise _bad(f"cannot store {name!r}: dtype {arr.dtype.name} has no safetensors code")
+    return code, np.ascontiguousarray(arr, dtype=arr.dtype.newbyteorder("<"))
+
+
 def save_safetensors(tensors: Dict[str, Any], path: Optional[str] = None, *,
                      metadata: Optional[Dict[str, str]] = None) -> bytes:
-    """The safetensors bytes of ``tensors`` (Tensor or ndarray values), also
-    written to ``path`` when given (_safetensors.py:303-385)."""
-    header: Dict[str, Any] = {}
-    arrays = []
-    cursor = 0
-    for name, value in tensors.items():
-        if isinstance(value, np.ndarray):
-            arr = value
-        elif hasattr(value, "numpy"):
-            arr = value.numpy()
-        else:
-            raise TypeError(f"safetensors: value at {name!r} is a {type(value).__name__}, "
-                            f"expected TensorProxy or np.ndarray")
-        arr = np.ascontiguousarray(arr)
-        code = _NAME_OF.get(arr.dtype.name)
-        if code is None:
-            raise ValueError(f"safetensors: cannot save dtype {arr.dtype.name!r} (no safetensors equivalent)")
-        header[name] = {"dtype": code, "shape": list(arr.shape), "data_offsets": [cursor, cursor + arr.nbytes]}
-        cursor += arr.nbytes
-        arrays.append(arr)
-    if metadata is not None:
-        if not isinstance(metadata, dict) or not all(isinstance(k, str) and isinstance(v, str)
-                                                     for k, v in metadata.items()):
-            raise ValueError("safetensors: __metadata__ must be Dict[str, str]")
-        header["__metadata__"] = metadata
-    head = json.dumps(header, separators=(",", ":")).encode("utf-8")
-    blob = b"".join([struct.pack("<Q", len(head)), head] + [a.tobytes() for a in arrays])
+    """Serialise ``tensors`` (Tensor or ndarray values) to safetensors bytes,
+    also written to ``path`` when given.
+
+    Tensors are laid out in the mapping's order with no padding between
+    them; the header is right-padded with spaces so that the data buffer
+    starts on an 8-byte boundary (as the format library's own writer does),
+    which keeps every mapped tensor aligned for zero-copy views."""
+    if metadata is not None and not (isinstance(metadata, dict) and all(
+            isinstance(k, str) and isinstance(v, str) for k, v in metadata.items())):
+        raise _bad("metadata must be a dict mapping str to str")
+    staged = [(name,) + _storable(name, value) for name, value in tensors.items()]
+    header: Dict[str, Any] = {} if metadata is None else {"__metadata__": dict(metadata)}
+    offset = 0
+    for name, code, arr in staged:
+        header[name] = {"dtype": code, "shape": list(arr.shape), "data_offsets": [offset, offset + arr.nbytes]}
+        offset += arr.nbytes
+    text = json.dumps(header, separators=(",", ":")).encode("utf-8")
+    text += b" " * (-(_LEN_PREFIX.size + len(text)) % _ALIGN)
+    out = bytearray(_LEN_PREFIX.pack(len(text)))
+    out += text
+    for _, _, arr in staged:
+        out += arr.tobytes()
+    blob = bytes(out)
     if path is not None:
         with open(path, "wb") as f:
             f.write(blob)
@@ -270,4 +362,4 @@ def gpt2_block_params(tensors: Dict[str, Tensor], layer: int, prefix: str = "") 
 
 
 __all__ = ["load_safetensors", "load_safetensors_resident", "save_safetensors", "parse_header", "validate_entry",
-           "gpt2_block_params", "get_default_session", "DTYPE_MAP", "MAX_HEADER_BYTES"]
+           "gpt2_block_params", "get_default_session", "DTYPE_MAP", "MAX_HEADER_BYTES", "SafetensorsFormatError"]

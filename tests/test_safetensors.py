@@ -19,7 +19,8 @@ import pytest
 import safetensors.numpy as stnp
 
 from browsergrad_amd.jit import configs
-from browsergrad_amd.jit.safetensors import load_safetensors, gpt2_block_params, parse_header, save_safetensors
+from browsergrad_amd.jit.safetensors import (SafetensorsFormatError, gpt2_block_params, load_safetensors,
+                                             parse_header, save_safetensors)
 from browsergrad_amd.jit.tensor import Session, autocast
 from oracle import graph as G
 
@@ -84,35 +85,80 @@ def test_bf16_and_http_are_refused():
         load_safetensors("https://example.invalid/model.safetensors")
 
 
+def _blob(header, data=b""):
+    h = json.dumps(header).encode() if not isinstance(header, bytes) else header
+    return struct.pack("<Q", len(h)) + h + data
+
+
 def test_malformed_files_are_refused():
-    def blob(header, data=b""):
-        h = json.dumps(header).encode() if not isinstance(header, bytes) else header
-        return struct.pack("<Q", len(h)) + h + data
-    with pytest.raises(ValueError, match="too small"):
+    with pytest.raises(SafetensorsFormatError, match="too small"):
         parse_header(b"\0" * 4)
-    with pytest.raises(ValueError, match="header length is zero"):
+    with pytest.raises(SafetensorsFormatError, match="header is empty"):
         parse_header(struct.pack("<Q", 0))
-    with pytest.raises(ValueError, match="exceeds file size"):
+    with pytest.raises(SafetensorsFormatError, match="past the end of the input"):
         parse_header(struct.pack("<Q", 64) + b"{}")
-    with pytest.raises(ValueError, match="ceiling"):
+    with pytest.raises(SafetensorsFormatError, match="ceiling"):
         parse_header(struct.pack("<Q", 200 * 1024 * 1024))
-    with pytest.raises(ValueError, match="not valid UTF-8 JSON"):
-        parse_header(blob(b"{nope"))
-    with pytest.raises(ValueError, match="expected dict"):
-        parse_header(blob([1, 2]))
-    with pytest.raises(ValueError, match="doesn't match"):
-        load_safetensors(blob({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 4]}}, b"\0" * 4),
+    with pytest.raises(SafetensorsFormatError, match="not a JSON object"):
+        parse_header(_blob(b"{nope"))
+    with pytest.raises(SafetensorsFormatError, match="start with"):
+        parse_header(_blob([1, 2]))
+    with pytest.raises(SafetensorsFormatError, match="not UTF-8"):
+        parse_header(_blob(b'{"\xff": 1}'))
+    with pytest.raises(SafetensorsFormatError, match="needs 8"):
+        load_safetensors(_blob({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 4]}}, b"\0" * 4),
                          session=Session())
-    with pytest.raises(ValueError, match="past end of file"):
-        load_safetensors(blob({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}, b"\0" * 4),
+    with pytest.raises(SafetensorsFormatError, match="past the end"):
+        load_safetensors(_blob({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}, b"\0" * 4),
                          session=Session())
-    with pytest.raises(ValueError, match="unknown dtype"):
-        load_safetensors(blob({"a": {"dtype": "F8", "shape": [1], "data_offsets": [0, 1]}}, b"\0"),
+    with pytest.raises(SafetensorsFormatError, match="dtype code 'F8'"):
+        load_safetensors(_blob({"a": {"dtype": "F8", "shape": [1], "data_offsets": [0, 1]}}, b"\0"),
                          session=Session())
-    with pytest.raises(ValueError, match="cannot save dtype"):
+    with pytest.raises(SafetensorsFormatError, match="shape must be"):
+        load_safetensors(_blob({"a": {"dtype": "U8", "shape": [-1], "data_offsets": [0, 1]}}, b"\0"),
+                         session=Session())
+    with pytest.raises(SafetensorsFormatError, match="unexpected field"):
+        load_safetensors(_blob({"a": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1], "x": 0}}, b"\0"),
+                         session=Session())
+    with pytest.raises(SafetensorsFormatError, match="no safetensors code"):
         save_safetensors({"c": np.zeros(2, np.complex64)})
-    with pytest.raises(ValueError, match="Dict\\[str, str\\]"):
+    with pytest.raises(SafetensorsFormatError, match="str to str"):
         save_safetensors({"a": np.zeros(1, np.float32)}, metadata={"k": 1})
+    with pytest.raises(SafetensorsFormatError, match="reserved"):
+        save_safetensors({"__metadata__": np.zeros(1, np.float32)})
+    with pytest.raises(TypeError, match="neither a Tensor nor a NumPy array"):
+        save_safetensors({"a": [1.0]})
+
+
+def test_format_rules_beyond_the_reference():
+    """Rules of the format description that the reference's reader does not
+    enforce: duplicate keys, string-only metadata, and tensors that tile the
+    data buffer (no gap, overlap or trailing bytes)."""
+    rec = lambda lo, hi: {"dtype": "U8", "shape": [hi - lo], "data_offsets": [lo, hi]}  # noqa: E731
+    dup = b'{"a":' + json.dumps(rec(0, 1)).encode() + b',"a":' + json.dumps(rec(1, 2)).encode() + b"}"
+    with pytest.raises(SafetensorsFormatError, match="appears twice"):
+        load_safetensors(_blob(dup, b"\0\0"), session=Session())
+    with pytest.raises(SafetensorsFormatError, match="gap at byte 0"):
+        load_safetensors(_blob({"a": rec(1, 2)}, b"\0\0"), session=Session())
+    with pytest.raises(SafetensorsFormatError, match="overlaps"):
+        load_safetensors(_blob({"a": rec(0, 2), "b": rec(1, 2)}, b"\0\0"), session=Session())
+    with pytest.raises(SafetensorsFormatError, match="cover only 1"):
+        load_safetensors(_blob({"a": rec(0, 1)}, b"\0\0"), session=Session())
+    with pytest.raises(SafetensorsFormatError, match="__metadata__"):
+        load_safetensors(_blob({"__metadata__": {"k": 3}, "a": rec(0, 1)}, b"\0"), session=Session())
+    # Tiling holds in any header order; zero-length tensors may sit anywhere.
+    ok = {"b": rec(2, 3), "e": rec(3, 3), "a": rec(0, 2), "__metadata__": {"k": "v"}}
+    out = load_safetensors(_blob(ok, b"\1\2\3"), session=Session())
+    assert list(out) == ["b", "e", "a"]
+    assert host(out["a"]).tolist() == [1, 2] and host(out["b"]).tolist() == [3] and host(out["e"]).size == 0
+
+
+def test_writer_aligns_the_data_buffer():
+    for n in range(1, 12):
+        blob = save_safetensors({"x" * n: np.arange(3, dtype=np.float64)}, metadata={"m": "y" * n})
+        (hlen,) = struct.unpack("<Q", blob[:8])
+        assert (8 + hlen) % 8 == 0 and blob[8:9] == b"{"
+        assert np.array_equal(stnp.load(blob)["x" * n], np.arange(3, dtype=np.float64))
 
 
 def _gpt2_hf_weights(rng, emb):

@@ -18,7 +18,7 @@ C5  one GPT-2 block under autocast(float16): x (8, 1024, 768) N(0,1);
 """
 from __future__ import annotations
 
-from typing import Tuple
+from typing import Optional, Tuple
 
 import numpy as np
 
@@ -94,9 +94,12 @@ def gpt2_block(x: Tensor, p: dict, heads: int) -> Tensor:
     return h + linear(gelu(linear(h2, p["w_up"], p["b_up"])), p["w_down"], p["b_down"])
 
 
-def c5(scale: float = 1.0, seed: int = 5, dtype: str = "float16") -> Tuple[Session, Tensor]:
+def c5(scale: float = 1.0, seed: int = 5, dtype: str = "float16",
+       batch: Optional[int] = None) -> Tuple[Session, Tensor]:
+    """C5; ``batch`` overrides the batch size alone (the CPU baseline times
+    one sequence of the full-width block)."""
     rng = np.random.default_rng(seed)
-    bsz, seq = _d(8, scale), _d(1024, scale, 16)
+    bsz, seq = _d(8, scale) if batch is None else batch, _d(1024, scale, 16)
     heads = 12 if scale >= 1.0 else 2
     emb = 768 if scale >= 1.0 else heads * 64
     s = Session()

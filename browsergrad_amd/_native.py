@@ -79,6 +79,13 @@ class MatmulDesc(C.Structure):
     ]
 
 
+class MatmulExt(C.Structure):
+    _fields_ = [
+        ("residual", handle_t), ("a_dtype", C.c_int32), ("b_dtype", C.c_int32),
+        ("reserved", C.c_int32 * 4),
+    ]
+
+
 class AttentionDesc(C.Structure):
     _fields_ = [
         ("q", handle_t), ("k", handle_t), ("v", handle_t),
@@ -160,6 +167,7 @@ SIGNATURES = {
     "bg_flash_attention": (C.c_int, [ctx_p, handle_t, handle_t, handle_t, handle_t, C.c_int64, C.c_int64,
                                      C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_int, PH]),
     "bg_matmul_ex": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), PH]),
+    "bg_matmul_ex2": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), C.POINTER(MatmulExt), PH]),
     "bg_matmul_noalloc": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p]),
     "bg_fused_ex": (C.c_int, [ctx_p, C.POINTER(FusedDesc), PH]),

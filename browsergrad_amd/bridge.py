@@ -192,7 +192,13 @@ class HipRealizerBridge:
                   stride_a: Optional[int] = None, stride_b: Optional[int] = None,
                   stride_c: Optional[int] = None, offset_a: int = 0, offset_b: int = 0,
                   trans_b: bool = False, in_dtype: str = "float32", out_dtype: Optional[str] = None,
-                  bias: Optional[int] = None, round_out: bool = False, act: int = N.ACT_NONE) -> int:
+                  bias: Optional[int] = None, round_out: bool = False, act: int = N.ACT_NONE,
+                  residual: Optional[int] = None, a_dtype: Optional[str] = None,
+                  b_dtype: Optional[str] = None) -> int:
+        """bg_matmul_ex; with ``residual`` (f32 [batch, m, n] added after
+        the epilogue) or ``a_dtype`` / ``b_dtype`` (the dtypes the operands
+        are stored in, cast to ``in_dtype`` in a pre-pass) it calls
+        bg_matmul_ex2."""
         d = N.MatmulDesc()
         d.a, d.b, d.bias = int(a), int(b), int(bias or 0)
         d.batch, d.m, d.n, d.k = int(batch), int(m), int(n), int(k)
@@ -209,7 +215,14 @@ class HipRealizerBridge:
         d.round_f16 = 1 if round_out else 0
         d.act = int(act)
         out = N.handle_t()
-        self._check(self._lib.bg_matmul_ex(self._ctx, C.byref(d), C.byref(out)))
+        if residual is None and a_dtype is None and b_dtype is None:
+            self._check(self._lib.bg_matmul_ex(self._ctx, C.byref(d), C.byref(out)))
+            return int(out.value)
+        e = N.MatmulExt()
+        e.residual = int(residual or 0)
+        e.a_dtype = -1 if a_dtype is None else _dtype_code(a_dtype, "matmul")
+        e.b_dtype = -1 if b_dtype is None else _dtype_code(b_dtype, "matmul")
+        self._check(self._lib.bg_matmul_ex2(self._ctx, C.byref(d), C.byref(e), C.byref(out)))
         return int(out.value)
 
     def fused_ex(self, inputs: Sequence[int], ops: Sequence[Tuple[str, int, int, int]],

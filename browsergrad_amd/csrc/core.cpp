@@ -815,10 +815,22 @@ int bg_matmul(bg_ctx* ctx, bg_handle a, bg_handle b, int64_t m, int64_t k,
   BG_API_END
 }
 
-int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
-  BG_API_BEGIN
+// bg_matmul_ex and bg_matmul_ex2: ext NULL = no extras.
+static void matmul_entry(bg_ctx* ctx, const bg_matmul_desc* desc, const bg_matmul_ext* ext, bg_handle* out) {
   if (!desc || !out) fail(BG_E_INVALID, "matmul_ex: NULL argument");
   const bg_matmul_desc& d = *desc;
+  GemmExtra ex;
+  if (ext) {
+    for (int32_t r : ext->reserved)
+      if (r != 0) fail(BG_E_INVALID, "matmul_ex2: reserved fields must be 0");
+    ex.a_dtype = ext->a_dtype;
+    ex.b_dtype = ext->b_dtype;
+  }
+  const int a_dt = ex.a_dtype >= 0 ? ex.a_dtype : d.in_dtype;
+  const int b_dt = ex.b_dtype >= 0 ? ex.b_dtype : d.in_dtype;
+  for (int dt : {a_dt, b_dt})
+    if (dt != BG_F32 && dt != BG_F16 && dt != BG_BF16)
+      fail(BG_E_DTYPE, std::string("matmul_ex2: operand storage dtype ") + dtype_name(dt) + " not supported");
   if (d.m <= 0 || d.n <= 0 || d.k <= 0 || d.batch <= 0)
     fail(BG_E_INVALID, "matmul: batch, m, k, n must be positive integers");
   Record& ra = get(ctx, d.a, "matmul[A]");
@@ -829,8 +841,17 @@ int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
     if (rbias->dtype != BG_F32 || rbias->numel() != d.n)
       fail(BG_E_SHAPE, "matmul: bias must be float32 [N]");
   }
-  if (ra.dtype != d.in_dtype || rb.dtype != d.in_dtype)
-    fail(BG_E_DTYPE, std::string("matmul: operands must be ") + dtype_name(d.in_dtype));
+  if (ra.dtype != a_dt || rb.dtype != b_dt) {
+    if (!ext) fail(BG_E_DTYPE, std::string("matmul: operands must be ") + dtype_name(d.in_dtype));
+    fail(BG_E_DTYPE, std::string("matmul_ex2: operands must be stored as ") + dtype_name(a_dt) + " and " +
+                         dtype_name(b_dt));
+  }
+  if (a_dt != d.in_dtype && (d.in_dtype == BG_F32 || d.lda != d.k ||
+                             (d.batch > 1 && d.stride_a != 0 && d.stride_a != d.m * d.k)))
+    fail(BG_E_UNSUPPORTED, "matmul_ex2: a cast operand must be a dense [batch][m][k] block for a 16-bit GEMM");
+  if (b_dt != d.in_dtype && (d.in_dtype == BG_F32 || d.ldb != (d.trans_b ? d.k : d.n) ||
+                             (d.batch > 1 && d.stride_b != 0 && d.stride_b != d.k * d.n)))
+    fail(BG_E_UNSUPPORTED, "matmul_ex2: a cast operand must be a dense [batch] x matrix for a 16-bit GEMM");
   if (d.in_dtype != BG_F32 && d.in_dtype != BG_F16 && d.in_dtype != BG_BF16)
     fail(BG_E_DTYPE, std::string("matmul: dtype ") + dtype_name(d.in_dtype) +
                          " not supported");
@@ -862,6 +883,13 @@ int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
   if (dd.ldc < d.n) fail(BG_E_SHAPE, "matmul: ldc < n");
   if (d.batch > 1 && dd.stride_c < (d.m - 1) * dd.ldc + d.n)
     fail(BG_E_SHAPE, "matmul: stride_c makes the output matrices of the batch overlap");
+  if (ext && ext->residual) {
+    const Record& rr = get(ctx, ext->residual, "matmul[residual]");
+    if (rr.dtype != BG_F32 || rr.numel() != d.batch * d.m * d.n)
+      fail(BG_E_SHAPE, "matmul_ex2: residual must be float32 holding batch * m * n elements");
+    if (dd.ldc != d.n || (d.batch > 1 && dd.stride_c != d.m * d.n))
+      fail(BG_E_UNSUPPORTED, "matmul_ex2: a residual needs a dense output (ldc = n, stride_c = m * n)");
+  }
   std::vector<int64_t> os;
   if (d.batch > 1) os.push_back(d.batch);
   os.push_back(d.m);
@@ -872,13 +900,26 @@ int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
   Record& ra2 = ctx->handles[d.a];
   Record& rb2 = ctx->handles[d.b];
   const Record* rbias2 = d.bias ? &ctx->handles[d.bias] : nullptr;
+  if (ext && ext->residual) ex.residual = reinterpret_cast<const float*>(ctx->handles[ext->residual].ptr());
   try {
-    launch_matmul(ctx, dd, ra2, rb2, rbias2, ro);
+    launch_matmul(ctx, dd, ra2, rb2, rbias2, ro, &ex);
   } catch (...) {
     bg_release(ctx, o);
     throw;
   }
   *out = o;
+}
+
+int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out) {
+  BG_API_BEGIN
+  matmul_entry(ctx, desc, nullptr, out);
+  BG_API_END
+}
+
+int bg_matmul_ex2(bg_ctx* ctx, const bg_matmul_desc* desc, const bg_matmul_ext* ext, bg_handle* out) {
+  BG_API_BEGIN
+  if (!ext) fail(BG_E_INVALID, "matmul_ex2: NULL ext");
+  matmul_entry(ctx, desc, ext, out);
   BG_API_END
 }
 

@@ -90,8 +90,10 @@ struct bg_ctx {
   // Scratch buffers reused across launches (workspace for pre-passes):
   // slot 0 = re-laid-out GEMM operand, slot 1 = f32 GEMM result awaiting an
   // elementwise epilogue pass.
-  void* scratch[2] = {nullptr, nullptr};
-  size_t scratch_bytes[2] = {0, 0};
+  // GEMM scratch slots: 0 B re-layout / B cast, 1 f32 pre-GELU product,
+  // 2 A cast.
+  void* scratch[3] = {nullptr, nullptr, nullptr};
+  size_t scratch_bytes[3] = {0, 0, 0};
 
   // Device address of this device's fixed no-allocation scratch (NULL when
   // it could not be resolved; bg_matmul_noalloc then refuses).
@@ -154,7 +156,7 @@ void dispatch(bg_ctx* ctx, void (*kernel)(KArgs...), dim3 grid, dim3 block, size
 void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out);
 void launch_gelu_rows(bg_ctx* ctx, const float* src, int64_t ld_src, int64_t stride_src, void* dst,
                       int64_t ld_dst, int64_t stride_dst, int dst_dtype, int64_t batch, int64_t rows,
-                      int64_t cols);
+                      int64_t cols, const float* residual = nullptr);
 void launch_cast(bg_ctx* ctx, const void* src, int src_dtype, void* dst,
                  int dst_dtype, int64_t n);
 void launch_cast_transpose(bg_ctx* ctx, const void* src, int src_dtype,
@@ -198,8 +200,15 @@ void launch_reduce_last(bg_ctx* ctx, const void* x, int dtype, void* y,
                         int64_t rows, int64_t cols, int op);
 void launch_softmax_last(bg_ctx* ctx, const void* x, int x_dtype, void* y, int y_dtype,
                          int64_t rows, int64_t cols);
+// Extras of bg_matmul_ex2: operand storage dtypes converted in a pre-pass
+// and an f32 residual added after the epilogue.
+struct GemmExtra {
+  const float* residual = nullptr;  // contiguous [batch][M][N] f32, or NULL
+  int a_dtype = -1;                 // storage dtype of a (-1: d.in_dtype)
+  int b_dtype = -1;                 // storage dtype of b (-1: d.in_dtype)
+};
 void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a,
-                   const Record& b, const Record* bias, Record& out);
+                   const Record& b, const Record* bias, Record& out, const GemmExtra* ex = nullptr);
 // Device scratch for one GEMM call's pre- and post-passes: the context's
 // growable slots (fixed == NULL), or a fixed region of cap bytes handed out
 // front to back (the no-allocation entry point).
@@ -214,7 +223,7 @@ struct GemmWorkspace {
 // d.offset_b applied inside; bias f32 [N] or NULL; c: the output with d.ldc /
 // d.stride_c already resolved).
 void run_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char* b, const float* bias, void* c,
-                GemmWorkspace& ws);
+                GemmWorkspace& ws, const GemmExtra* ex = nullptr);
 // Resolves this device's no-allocation scratch address (noalloc.hip); called
 // by bg_ctx_create with the context's device current.
 void noalloc_setup(bg_ctx* ctx);

@@ -63,6 +63,8 @@ struct GemmArgs {
   int vec_store;    // C rows can take 4-element vector stores (ldc % 4, alignment)
   int64_t k_chunk;  // f32 split-K: K elements per blockIdx.y slice (0: no split)
   float* ws;        // f32 split-K: [splits][M][N] partial sums
+  const float* R;   // residual f32 [batch][M][N] added last (NULL: none)
+  int64_t ldr, sr;  // its row and batch strides (elements)
 };
 
 // XCD-aware tile index -> (tile_m, tile_n).  Workgroups are dispatched
@@ -124,6 +126,19 @@ __device__ __forceinline__ void epilogue_tiles(const GemmArgs& P, char* C, float
   char* corner = C + (row0 * P.ldc + col0) * ES;
   const uint32_t lane_off = uint32_t((4 * half * P.ldc + (lane & 31)) * ES);
   const int64_t row_bytes = P.ldc * ES;
+  // Residual (f32, added after the activation): 16 values per tile, same
+  // element layout as the accumulator tile.
+  float rnext[16];
+  const float* rbase = P.R ? P.R + int64_t(blockIdx.z) * P.sr + (row0 + 4 * half) * P.ldr + cl : nullptr;
+  auto load_residual = [&](int ti, int tj) {
+    const bool ok_c = FULL || cl + tj * 32 < P.N;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int rr = ti * 32 + 8 * (e >> 2) + (e & 3);
+      rnext[e] = (FULL || (ok_c && row0 + rr + 4 * half < P.M)) ? rbase[rr * P.ldr + tj * 32] : 0.f;
+    }
+  };
+  if (P.R) load_residual(0, 0);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -155,6 +170,16 @@ __device__ __forceinline__ void epilogue_tiles(const GemmArgs& P, char* C, float
         }
       }
       const bool col_ok = FULL || cl + j * 32 < P.N;
+      if (P.R) {
+        // The residual of this tile was loaded one tile ahead (before the
+        // previous tile's stores), so its wait does not queue behind them.
+        float cur[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) cur[e] = rnext[e];
+        if (i * TN + j + 1 < TM * TN) load_residual((i * TN + j + 1) / TN, (i * TN + j + 1) % TN);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = v[e] + cur[e];
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int rr = i * 32 + 8 * (e >> 2) + (e & 3);
@@ -711,6 +736,7 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
     Q.act = BG_ACT_NONE;
     Q.out_dtype = BG_F32;
     Q.ldc = P.N;
+    Q.R = nullptr;
     direct_epilogue<TM, TN, false>(Q, reinterpret_cast<char*>(P.ws + int64_t(blockIdx.y) * P.M * P.N), acc,
                                    m0 + wm * WTM, n0 + wn * WTN);
     return;
@@ -726,7 +752,8 @@ __global__ void __launch_bounds__(256) gemm32_splitk_reduce(GemmArgs P, int spli
   const int64_t m = i / P.N, n = i % P.N;
   float s = P.ws[i];
   for (int k = 1; k < splits; ++k) s += P.ws[int64_t(k) * P.M * P.N + i];
-  const float v = epilogue_value(P, s, P.bias ? P.bias[n] : 0.f);
+  float v = epilogue_value(P, s, P.bias ? P.bias[n] : 0.f);
+  if (P.R) v = v + P.R[m * P.ldr + n];
   store_elem<OUT>(static_cast<char*>(P.C) + (m * P.ldc + n) * (OUT == BG_F32 ? 4 : 2), v);
 }
 
@@ -847,9 +874,13 @@ static bool gelu_in_epilogue(const bg_matmul_desc& d, const char* a, const char*
 // a / b point at the operands' storage (d.offset_a / d.offset_b are applied
 // here); bias is f32 [N] or NULL.
 static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char* b, const float* bias,
-                     void* c, int64_t ldc, int64_t stride_c, int out_dtype, int act, GemmWorkspace& ws) {
+                     void* c, int64_t ldc, int64_t stride_c, int out_dtype, int act, GemmWorkspace& ws,
+                     const float* residual = nullptr) {
   const int64_t es = dtype_size(d.in_dtype);
   GemmArgs P{};
+  P.R = residual;
+  P.ldr = d.n;
+  P.sr = d.m * d.n;
   P.A = a + d.offset_a * es;
   P.B = b + d.offset_b * es;
   P.bias = bias;
@@ -993,16 +1024,51 @@ void* GemmWorkspace::get(size_t bytes, int slot) {
 
 // Every workspace request of a call comes before its first kernel launch, so
 // a refused request leaves nothing queued.
-void run_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char* b, const float* bias, void* c,
-                GemmWorkspace& ws) {
-  if (d.batch > 65535) fail(BG_E_UNSUPPORTED, "matmul: batch > 65535");
+void run_matmul(bg_ctx* ctx, const bg_matmul_desc& d0, const char* a, const char* b, const float* bias, void* c,
+                GemmWorkspace& ws, const GemmExtra* ex) {
+  if (d0.batch > 65535) fail(BG_E_UNSUPPORTED, "matmul: batch > 65535");
+  bg_matmul_desc d = d0;
+  const float* residual = ex ? ex->residual : nullptr;
+  const int es = int(dtype_size(d.in_dtype));
+  // Operands stored in another dtype are converted (round to nearest even)
+  // into scratch first; a [K][N] B is converted and laid out as [N][K] in
+  // the same pass.  The caller has checked that such operands are dense.
+  const int a_dt = ex && ex->a_dtype >= 0 ? ex->a_dtype : d.in_dtype;
+  const int b_dt = ex && ex->b_dtype >= 0 ? ex->b_dtype : d.in_dtype;
+  void* ta = nullptr;
+  void* tb = nullptr;
+  const int64_t na = (d.stride_a == 0 ? 1 : d.batch) * d.m * d.k;
+  const int64_t nbm = d.stride_b == 0 ? 1 : d.batch;
+  if (a_dt != d.in_dtype) ta = ws.get(size_t(na * es), 2);
+  if (b_dt != d.in_dtype) tb = ws.get(size_t(nbm * d.n * d.k * es), 0);
+  if (ta) {
+    Profile prof(ctx, "gemm_a_cast", na * (dtype_size(a_dt) + es), 0);
+    launch_cast(ctx, a + d.offset_a * dtype_size(a_dt), a_dt, ta, d.in_dtype, na);
+    a = static_cast<const char*>(ta);
+    d.offset_a = 0;
+  }
+  if (tb) {
+    const char* src = b + d.offset_b * dtype_size(b_dt);
+    Profile prof(ctx, "gemm_b_cast", nbm * d.n * d.k * (dtype_size(b_dt) + es), 0);
+    if (d.trans_b) {
+      launch_cast(ctx, src, b_dt, tb, d.in_dtype, nbm * d.n * d.k);
+    } else {
+      launch_cast_transpose(ctx, src, b_dt, tb, d.in_dtype, d.k, d.n, nbm);
+      d.trans_b = 1;
+    }
+    b = static_cast<const char*>(tb);
+    d.offset_b = 0;
+    d.ldb = d.k;
+    d.stride_b = d.stride_b == 0 ? 0 : d.n * d.k;
+  }
   if (d.act != BG_ACT_GELU_TANH || gelu_in_epilogue(d, a, b)) {
-    run_gemm(ctx, d, a, b, bias, c, d.ldc, d.stride_c, d.out_dtype, d.act, ws);
+    run_gemm(ctx, d, a, b, bias, c, d.ldc, d.stride_c, d.out_dtype, d.act, ws, residual);
     return;
   }
   // GELU follows the (rounded, biased) product in f32, as the reference
   // graph evaluates it: the GEMM leaves f32 in C (or in scratch when C is
-  // 16-bit), then one elementwise pass applies GELU and stores C's dtype.
+  // 16-bit), then one elementwise pass applies GELU (and the residual) and
+  // stores C's dtype.
   float* f = reinterpret_cast<float*>(c);
   int64_t ldf = d.ldc, sf = d.stride_c;
   if (d.out_dtype != BG_F32) {
@@ -1012,14 +1078,14 @@ void run_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char*
   }
   run_gemm(ctx, d, a, b, bias, f, ldf, sf, BG_F32, BG_ACT_NONE, ws);
   Profile prof(ctx, "gemm_gelu", d.batch * d.m * d.n * (4 + dtype_size(d.out_dtype)), 0);
-  launch_gelu_rows(ctx, f, ldf, sf, c, d.ldc, d.stride_c, d.out_dtype, d.batch, d.m, d.n);
+  launch_gelu_rows(ctx, f, ldf, sf, c, d.ldc, d.stride_c, d.out_dtype, d.batch, d.m, d.n, residual);
 }
 
 void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const Record& b,
-                   const Record* bias, Record& out) {
+                   const Record* bias, Record& out, const GemmExtra* ex) {
   GemmWorkspace ws{ctx};
   run_matmul(ctx, d, a.ptr(), b.ptr(), bias ? reinterpret_cast<const float*>(bias->ptr()) : nullptr, out.ptr(),
-             ws);
+             ws, ex);
 }
 
 }  // namespace bg

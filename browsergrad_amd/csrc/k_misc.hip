@@ -12,6 +12,7 @@
 //     MFMA kernel does not cover.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "common.cuh"
 #include "core.h"
@@ -79,6 +80,94 @@ __global__ void __launch_bounds__(256) cast_transpose_kernel(const void* __restr
   for (int y = ty; y < 64; y += 4) {
     const int64_t c = c0 + y, r = r0 + tx;
     if (r < rows && c < cols) store_from_f32(dst, dd, base + c * rows + r, tile[tx][y]);
+  }
+}
+
+// Compile-time-dtype forms of the two casts for aligned data (the branchy
+// kernels above stay for the unaligned remainder of cases).
+template <int D>
+__device__ __forceinline__ float cvt_in(uint32_t w, int half) {
+  const uint16_t h = uint16_t(half ? w >> 16 : w);
+  return D == 1 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+}
+template <int D>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const uint16_t x = D == 1 ? f32_to_f16_bits(a) : f32_to_bf16_bits(a);
+  const uint16_t y = D == 1 ? f32_to_f16_bits(b) : f32_to_bf16_bits(b);
+  return uint32_t(x) | (uint32_t(y) << 16);
+}
+// 8 consecutive elements as f32 (a 32-byte f32 or 16-byte 16-bit load).
+template <int SD>
+__device__ __forceinline__ void load8(const void* src, int64_t i, float (&v)[8]) {
+  if constexpr (SD == 0) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + i);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + i + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + i);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = cvt_in<SD>(w[j >> 1], j & 1);
+  }
+}
+template <int DD>
+__device__ __forceinline__ void store8(void* dst, int64_t i, const float (&v)[8]) {
+  if constexpr (DD == 0) {
+    float* d = static_cast<float*>(dst) + i;
+    *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(d + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst) + i) =
+        make_uint4(pack2<DD>(v[0], v[1]), pack2<DD>(v[2], v[3]), pack2<DD>(v[4], v[5]), pack2<DD>(v[6], v[7]));
+  }
+}
+
+// n % 8 == 0, both pointers 16-byte aligned: 8 elements per lane per step.
+template <int SD, int DD>
+__global__ void __launch_bounds__(256) cast8_kernel(const void* __restrict__ src, void* __restrict__ dst,
+                                                    int64_t n8) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t g = int64_t(blockIdx.x) * 256 + threadIdx.x; g < n8; g += stride) {
+    float v[8];
+    load8<SD>(src, g * 8, v);
+    store8<DD>(dst, g * 8, v);
+  }
+}
+
+// dst[b][c][r] = src[b][r][c] converted, rows % 8 == cols % 8 == 0, both
+// pointers 16-byte aligned.  64 x 64 tiles: each lane loads 8 consecutive
+// columns of one row (two passes of 32 rows), the tile sits in LDS as f32
+// with a one-word row pad, and each lane stores 8 consecutive dst elements
+// (8 source rows of one column).
+template <int SD, int DD>
+__global__ void __launch_bounds__(256) cast_transpose8_kernel(const void* __restrict__ src, void* __restrict__ dst,
+                                                              int64_t rows, int64_t cols) {
+  __shared__ float tile[64][65];
+  const int64_t base = int64_t(blockIdx.z) * rows * cols;
+  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+  const int t = threadIdx.x;
+  const int lc = (t & 7) * 8, lr = t >> 3;  // 8 lanes per 64-wide row, 32 rows per pass
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int rr = lr + 32 * p;
+    float v[8];
+    if (r0 + rr < rows && c0 + lc < cols) {
+      load8<SD>(src, base + (r0 + rr) * cols + c0 + lc, v);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tile[rr][lc + j] = v[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int cc = lr + 32 * p;  // dst row = source column c0 + cc
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = tile[lc + j][cc];
+    if (c0 + cc < cols && r0 + lc < rows) store8<DD>(dst, base + (c0 + cc) * rows + r0 + lc, v);
   }
 }
 
@@ -492,15 +581,22 @@ int grid1(int64_t n, int per) {
 // tanh-GELU over the rows of an f32 matrix (the GEMM's activation stage):
 // dst[b][r][c] = gelu(src[b][r][c]) stored in dst_dtype.  One block per row
 // chunk; four consecutive columns per lane when the rows allow it.
+// residual: NULL or contiguous f32 [batch][rows][cols], added after GELU.
 __global__ void __launch_bounds__(256) gelu_rows_kernel(const float* __restrict__ src, int64_t ld_src,
                                                         int64_t stride_src, void* __restrict__ dst,
                                                         int64_t ld_dst, int64_t stride_dst, int dd,
-                                                        int64_t rows, int64_t cols, int64_t total_rows) {
+                                                        int64_t rows, int64_t cols, int64_t total_rows,
+                                                        const float* __restrict__ residual) {
   for (int64_t rr = blockIdx.x; rr < total_rows; rr += gridDim.x) {
     const int64_t b = rr / rows, r = rr - b * rows;
     const float* s = src + b * stride_src + r * ld_src;
     const int64_t o = b * stride_dst + r * ld_dst;
-    for (int64_t c = threadIdx.x; c < cols; c += 256) store_from_f32(dst, dd, o + c, gelu_tanh(s[c]));
+    const float* res = residual ? residual + rr * cols : nullptr;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      float g = gelu_tanh(s[c]);
+      if (res) g = g + res[c];
+      store_from_f32(dst, dd, o + c, g);
+    }
   }
 }
 
@@ -508,11 +604,33 @@ __global__ void __launch_bounds__(256) gelu_rows_kernel(const float* __restrict_
 
 namespace bg {
 
+// Instantiates f<SD, DD> for the runtime (sd, dd) pair of {f32, f16, bf16}.
+template <typename F>
+static void with_dtypes(int sd, int dd, F&& f) {
+  auto inner = [&](auto s_tag) {
+    constexpr int S = decltype(s_tag)::value;
+    if (dd == 0) f(std::integral_constant<int, S>{}, std::integral_constant<int, 0>{});
+    else if (dd == 1) f(std::integral_constant<int, S>{}, std::integral_constant<int, 1>{});
+    else f(std::integral_constant<int, S>{}, std::integral_constant<int, 2>{});
+  };
+  if (sd == 0) inner(std::integral_constant<int, 0>{});
+  else if (sd == 1) inner(std::integral_constant<int, 1>{});
+  else inner(std::integral_constant<int, 2>{});
+}
+
+static bool cast_dtype(int d) { return d == 0 || d == 1 || d == 2; }
+
 void launch_cast(bg_ctx* ctx, const void* src, int sd, void* dst, int dd, int64_t n) {
   if (n <= 0) return;
   const bool aligned = reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(dst) % 16 == 0;
-  if (aligned) {
+  if (aligned && n % 8 == 0 && cast_dtype(sd) && cast_dtype(dd)) {
+    const int64_t n8 = n / 8;
+    const dim3 grid(unsigned(std::min<int64_t>((n8 + 255) / 256, 256 * 32)));
+    with_dtypes(sd, dd, [&](auto S, auto D) {
+      bg::dispatch(ctx, cast8_kernel<decltype(S)::value, decltype(D)::value>, grid, dim3(256), 0, src, dst, n8);
+    });
+  } else if (aligned) {
     bg::dispatch(ctx, cast_kernel, dim3(grid1(n / 4 + 1, 256)), dim3(256), 0,
                        src, sd, dst, dd, n);
   } else {
@@ -527,8 +645,17 @@ void launch_cast_transpose(bg_ctx* ctx, const void* src, int sd, void* dst, int 
   if (rows <= 0 || cols <= 0 || batch <= 0) return;
   if (batch > 65535) fail(BG_E_UNSUPPORTED, "cast_transpose: batch > 65535");
   dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64), unsigned(batch));
-  bg::dispatch(ctx, cast_transpose_kernel, grid, dim3(256), 0, src, sd, dst, dd,
-                     rows, cols);
+  const bool vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0 &&
+                   rows % 8 == 0 && cols % 8 == 0 && cast_dtype(sd) && cast_dtype(dd);
+  if (vec) {
+    with_dtypes(sd, dd, [&](auto S, auto D) {
+      bg::dispatch(ctx, cast_transpose8_kernel<decltype(S)::value, decltype(D)::value>, grid, dim3(256), 0, src,
+                   dst, rows, cols);
+    });
+  } else {
+    bg::dispatch(ctx, cast_transpose_kernel, grid, dim3(256), 0, src, sd, dst, dd,
+                       rows, cols);
+  }
   hip_check(hipGetLastError(), "cast_transpose launch");
 }
 
@@ -565,12 +692,12 @@ void launch_copy_strided(bg_ctx* ctx, const void* src, int64_t es, void* dst,
 
 void launch_gelu_rows(bg_ctx* ctx, const float* src, int64_t ld_src, int64_t stride_src, void* dst,
                       int64_t ld_dst, int64_t stride_dst, int dst_dtype, int64_t batch, int64_t rows,
-                      int64_t cols) {
+                      int64_t cols, const float* residual) {
   const int64_t total = batch * rows;
   if (total == 0 || cols == 0) return;
   const unsigned grid = unsigned(std::min<int64_t>(total, 65536));
   bg::dispatch(ctx, gelu_rows_kernel, dim3(grid), dim3(256), 0, src, ld_src, stride_src, dst, ld_dst,
-               stride_dst, dst_dtype, rows, cols, total);
+               stride_dst, dst_dtype, rows, cols, total, residual);
 }
 
 void launch_softmax_last(bg_ctx* ctx, const void* x, int xd, void* y, int yd, int64_t rows, int64_t cols) {

@@ -314,6 +314,25 @@ def _match_linear(add: UOp, cons: Dict[int, List[UOp]]) -> Optional[Tuple[UOp, U
     return None
 
 
+def _fold_residual_adds(root: UOp) -> UOp:
+    """ADD(HIP_LINEAR(...), r) with r float32 of the linear's own shape (a
+    residual stream, `x + linear(h)`) becomes one HIP_LINEAR whose epilogue
+    adds r after the bias and activation (bg_matmul_ex2).  f32 addition is
+    commutative, so either operand order gives the reference's bits."""
+    cons = consumers_of(root)
+    subs: Dict[int, UOp] = {}
+    for n in toposort(root):
+        if n.op != OP_ADD or n.dtype != "float32":
+            continue
+        for lin, r in (n.inputs, n.inputs[::-1]):
+            if (lin.op == OP_HIP_LINEAR and lin.dtype == "float32" and len(lin.inputs) == 3
+                    and len(cons.get(id(lin), [])) == 1
+                    and r.dtype == "float32" and tuple(r.shape) == tuple(lin.shape) and r is not lin):
+                subs[id(n)] = UOp(OP_HIP_LINEAR, lin.inputs + (r,), n.shape, "float32", {**lin.arg, "residual": True})
+                break
+    return substitute(root, subs)
+
+
 # ---- dtype refresh ---------------------------------------------------------------
 
 _PASS_THROUGH = frozenset({"LOAD", "RESHAPE", "PERMUTE", "SLICE", "BROADCAST_TO"})
@@ -481,6 +500,7 @@ def hip_fuse(root: UOp, bt: BufferTable) -> UOp:
         taken.update(id(x) for x in interior)
         taken.add(id(out))
     root = substitute(root, subs)
+    root = _fold_residual_adds(root)
     root = _rewrite_attention_views(root)
     root = _rewrite_narrow_stores(root)
     # 3. softmax outside attention: the reference matcher

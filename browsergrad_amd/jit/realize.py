@@ -374,14 +374,15 @@ def _h_hip_attention(n: UOp, w: _Walk) -> int:
 
 
 def _h_hip_linear(n: UOp, w: _Walk) -> int:
-    a, wt, bias = n.inputs
+    a, wt, bias = n.inputs[:3]
     arg = n.arg
     k = a.shape[-1]
     m = a.numel // k
     nn = wt.shape[0] if arg["trans_b"] else wt.shape[1]
+    extra = {"residual": w.h(n.inputs[3])} if arg.get("residual") else {}
     hnd = w.br.matmul_ex(w.h(a), w.h(wt), m=m, n=nn, k=k, trans_b=arg["trans_b"], in_dtype=arg["in_dtype"],
                          out_dtype=arg.get("out_dtype", "float32"), bias=w.h(bias), round_out=arg["round_out"],
-                         act=arg["act"])
+                         act=arg["act"], **extra)
     out = w.br.reshape(hnd, n.shape)
     w.br.release(hnd)
     return out

@@ -174,6 +174,28 @@ typedef struct bg_matmul_desc {
   int32_t reserved;
 } bg_matmul_desc;
 
+/* Extras for bg_matmul_ex2.  The epilogue is
+ *   y = act([round](acc) + bias) + residual
+ * evaluated in f32 in that order, which is the reference's autocast
+ * `x + linear(h)` graph: MATMUL -> ADD(bias) -> [relu | GELU] -> ADD(x)
+ * (_realize.py:395-412, _functional.py:99-134; residual streams of the
+ * GPT-2 block).
+ * residual: 0 = none; float32 holding batch*m*n elements, read as a dense
+ *   [batch][m][n] block; the output must then be dense too.
+ * a_dtype / b_dtype: the dtype a / b are stored in (-1 = in_dtype).  For a
+ *   16-bit GEMM an operand stored as f32 (or the other 16-bit type) is
+ *   rounded to in_dtype to nearest even in a pre-pass, which is the
+ *   autocast CAST (_amp.py:56-69) fused into the call; a [K][N] B
+ *   (trans_b = 0) is converted and re-laid out in the same pass.  Such an
+ *   operand must be a dense matrix or batch of matrices.
+ * reserved: must be 0. */
+typedef struct bg_matmul_ext {
+  bg_handle residual;
+  int32_t a_dtype;
+  int32_t b_dtype;
+  int32_t reserved[4];
+} bg_matmul_ext;
+
 /* Extension descriptor for attention.  Q/K/V/O are addressed with explicit
  * element strides so head-split views (reshape+permute of a fused QKV
  * projection) need no copy.  Softmax and accumulation are f32, and P is
@@ -333,6 +355,11 @@ int bg_conv2d_backward_bias(bg_ctx* ctx, bg_handle dy, int64_t n,
 
 /* ---- extensions --------------------------------------------------------- */
 int bg_matmul_ex(bg_ctx* ctx, const bg_matmul_desc* desc, bg_handle* out);
+/* bg_matmul_ex with the extras of bg_matmul_ext (residual epilogue,
+ * operands cast in a pre-pass).  Extends bridge.matmul
+ * (realizer.ts:1043-1060) for the walker's fused linear + residual and
+ * autocast-cast + linear patterns. */
+int bg_matmul_ex2(bg_ctx* ctx, const bg_matmul_desc* desc, const bg_matmul_ext* ext, bg_handle* out);
 /* No counterpart in the reference.  bg_matmul_ex for callers that cannot
  * allocate device memory (HIP graph capture, serving loops that forbid
  * hipMalloc): a, b, bias (f32 [N] or NULL) and c are caller-owned device

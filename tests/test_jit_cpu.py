@@ -184,6 +184,10 @@ def test_rewrites_c5_block_structure():
     assert len(lin) == 4 and [n.arg["act"] for n in lin].count(ACT_GELU) == 1
     assert all(n.arg["round_out"] and n.arg["in_dtype"] == "float16" for n in lin)
     assert "EXP" not in ops and "DIV" not in ops and "MATMUL" not in ops
+    # both residual adds ride on the out-projection and MLP-down epilogues
+    res = [n for n in lin if n.arg.get("residual")]
+    assert len(res) == 2 and all(len(n.inputs) == 4 and n.inputs[3].dtype == "float32" for n in res)
+    assert "HIP_REDUCE_FUSED" not in ops, ops
 
 
 def test_rewrites_preserve_values_on_cpu_oracle():

@@ -937,6 +937,273 @@ __global__ void __launch_bounds__(kFa2NW * 64, 2) fa6_fwd_kernel(Fa2Args P, uint
     }
 }
 
+// ---- v7: v6 without the per-half overflow branch ----------------------------
+//
+// v6's lazy reference max needs a wave-uniform test after every half (does
+// some P of this half reach the 16-bit limit?).  The test waits for the
+// whole exp2 chain and splits the scheduling region, which measured 35-43%
+// of the loop on MI355X.  v7 fixes the reference max per query once, from
+// the exact maximum of that query's first 32 keys, and runs every half
+// branch-free.  A later key may still exceed it by 16 or more (in log2
+// units), rounding some P to infinity in 16 bits; the infinity then reaches
+// O (inf * v, or inf * 0 = NaN) or l, so it is caught once at the end: a
+// wavefront whose l or O is not finite recomputes its 32 queries with an
+// exact running max (fa7_exact), reading K and V straight from global
+// memory.  Only inputs with a key that dominates the first 32 by 2^16 take
+// that path.
+// The loop is split in two: tiles where no wavefront of the workgroup needs
+// a causal or length mask, then the remaining (diagonal) tiles with the
+// mask test.  Ring, copies and barriers are v6's.
+
+// O = acc / l for this lane's query; O^T layout: register e of acc[db] holds
+// d = 32 db + 8 (e / 4) + 4 hi + e % 4.
+__device__ __forceinline__ void fa7_store(const Fa2Args& P, int b, int h, int qi, const float16v (&acc)[2],
+                                          float l_run) {
+  const int hi = (threadIdx.x >> 5) & 1;
+  const float lt = l_run + fa2_xor32(l_run);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (qi >= P.Sq) return;
+  char* Ob = static_cast<char*>(P.o);
+  const int64_t obase = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d0 = db * 32 + 8 * gq + 4 * hi;
+      const float y0 = acc[db][4 * gq] * inv, y1 = acc[db][4 * gq + 1] * inv;
+      const float y2 = acc[db][4 * gq + 2] * inv, y3 = acc[db][4 * gq + 3] * inv;
+      if (P.out_dtype == 0)
+        *reinterpret_cast<float4*>(Ob + (obase + d0) * 4) = make_float4(y0, y1, y2, y3);
+      else if (P.out_dtype == 1)
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<false>(y0, y1), fa2_pack<false>(y2, y3));
+      else
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<true>(y0, y1), fa2_pack<true>(y2, y3));
+    }
+}
+
+// Exact pass for one wavefront (the 32 queries from q0w), small in
+// registers so that inlining it costs the fast loop nothing: one query at a
+// time, one key per lane for the scores (s = sum_d Q'_d K_d with the fast
+// path's Q' = 16-bit(Q * scale * log2 e)), the exact running maximum over
+// 64-key chunks, and one output dimension per lane for P V (P rounded to
+// the input dtype, as the fast path's MFMA operand is).
+__device__ __forceinline__ float fa7_wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+template <bool BF16>
+__device__ __forceinline__ float fa7_round(float x) {
+  if constexpr (BF16) return static_cast<float>(static_cast<__bf16>(x));
+  else return static_cast<float>(static_cast<_Float16>(x));
+}
+
+template <bool BF16, bool CAUSAL>
+__device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0w) {
+  const int lane = threadIdx.x & 63;
+  const uint16_t* Qp = P.q + b * P.q_sb + h * P.q_sh;
+  const uint16_t* Kp = P.k + b * P.k_sb + h * P.k_sh;
+  const uint16_t* Vp = P.v + b * P.v_sb + h * P.v_sh;
+  char* Ob = static_cast<char*>(P.o);
+  for (int iq = 0; iq < kFa2QW; ++iq) {
+    const int qi = q0w + iq;
+    if (qi >= P.Sq) break;
+    const uint16_t* qrow = Qp + int64_t(qi) * P.q_ss;
+    const int nkeys = CAUSAL ? min(P.Sk, qi + 1) : P.Sk;
+    float m_run = -INFINITY, l_run = 0.f, o = 0.f;
+    for (int j0 = 0; j0 < nkeys; j0 += 64) {
+      const int j = j0 + lane;
+      float sc = -INFINITY;
+      if (j < nkeys) {
+        const uint16_t* krow = Kp + int64_t(j) * P.k_ss;
+        float acc = 0.f;
+        for (int d = 0; d < 64; d += 2) {
+          const uint32_t qw = *reinterpret_cast<const uint32_t*>(qrow + d);
+          const uint32_t kw = *reinterpret_cast<const uint32_t*>(krow + d);
+          acc += fa7_round<BF16>(fa2_lo<BF16>(qw) * P.sl2) * fa2_lo<BF16>(kw);
+          acc += fa7_round<BF16>(fa2_hi<BF16>(qw) * P.sl2) * fa2_hi<BF16>(kw);
+        }
+        sc = acc;
+      }
+      const float m_new = fmaxf(m_run, fa7_wave_max(sc));
+      const float alpha = m_run == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float pe = j < nkeys ? __builtin_amdgcn_exp2f(sc - m_new) : 0.f;
+      l_run = l_run * alpha + bgk::wave_sum(pe);
+      o *= alpha;
+      m_run = m_new;
+      const float p16 = fa7_round<BF16>(pe);
+      const int jn = min(64, nkeys - j0);
+      for (int jj = 0; jj < jn; ++jj) {
+        const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p16), jj));
+        const uint16_t vv = Vp[int64_t(j0 + jj) * P.v_ss + lane];
+        o += pj * (BF16 ? bgk::bf16_bits_to_f32(vv) : bgk::f16_bits_to_f32(vv));
+      }
+    }
+    const float y = l_run > 0.f ? o / l_run : 0.f;
+    const int64_t oi = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss + lane;
+    if (P.out_dtype == 0) reinterpret_cast<float*>(Ob)[oi] = y;
+    else if (P.out_dtype == 1) reinterpret_cast<uint16_t*>(Ob)[oi] = bgk::f32_to_f16_bits(y);
+    else reinterpret_cast<uint16_t*>(Ob)[oi] = bgk::f32_to_bf16_bits(y);
+  }
+}
+
+template <bool BF16, bool CAUSAL>
+// Four wavefronts per SIMD (two workgroups per CU), as v6 runs: <= 128 VGPRs.
+__global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
+  __shared__ fa_u4 smem[2 * kFa6Ring * kFa2Tile / 16];
+  char* sb = reinterpret_cast<char*>(smem);
+  char* kring = sb;
+  char* vring = sb + kFa6Ring * kFa2Tile;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hi = lane >> 5;
+  const int bh = blockIdx.x;
+  const int qblk = P.n_qblocks - 1 - int(blockIdx.y);  // heavy query blocks first
+  const int b = bh / P.H, h = bh % P.H;
+  const int q0 = qblk * kFa2BQ;
+  const int q0w = q0 + w * kFa2QW;
+  const int qi = q0w + (lane & 31);
+
+  const uint16_t* Qp = P.q + b * P.q_sb + h * P.q_sh;
+  const uint16_t* Kp = P.k + b * P.k_sb + h * P.k_sh;
+  const uint16_t* Vp = P.v + b * P.v_sb + h * P.v_sh;
+  const bgk::sgpr4_t rk = bgk::buffer_rsrc(Kp, k_bytes);
+  const bgk::sgpr4_t rv = bgk::buffer_rsrc(Vp, v_bytes);
+
+  const int nt_all = (P.Sk + kFa2BK - 1) / kFa2BK;
+  const int nt = CAUSAL ? min(nt_all, (q0 + kFa2BQ + kFa2BK - 1) / kFa2BK) : nt_all;
+  const int ntw = CAUSAL ? min(nt, (q0w + kFa2QW + kFa2BK - 1) / kFa2BK) : nt;
+  // Tiles with no masked key for any query of the workgroup.
+  const int t_clean = min(nt, CAUSAL ? min(P.Sk / kFa2BK, (q0 + 1) / kFa2BK) : P.Sk / kFa2BK);
+
+  const int u = w * 64 + lane;
+  const int krow = u >> 3, pc = u & 7;
+  const uint32_t koff = uint32_t((int64_t(krow) * P.k_ss + ((pc ^ ((krow >> 1) & 7)) * 8)) * 2);
+  const uint32_t voff = uint32_t((int64_t(krow) * P.v_ss + ((pc ^ ((krow & 3) << 1)) * 8)) * 2);
+  const uint32_t kstep = uint32_t(int64_t(kFa2BK) * P.k_ss * 2);
+  const uint32_t vstep = uint32_t(int64_t(kFa2BK) * P.v_ss * 2);
+  const uint32_t kl = bgk::lds_addr(kring) + uint32_t(w) * 1024u;
+  const uint32_t vl = bgk::lds_addr(vring) + uint32_t(w) * 1024u;
+  auto issue = [&](int j) {
+    const bool real = j >= 0 && j < nt;
+    const bool ok = real && j * kFa2BK + krow < P.Sk;
+    const uint32_t sl = uint32_t(j & 3) * kFa2Tile;
+    bgk::dma16_to_lds(kl + sl, ok ? koff : kFa2Oob, rk, real ? uint32_t(j) * kstep : 0u);
+    bgk::dma16_to_lds(vl + sl, ok ? voff : kFa2Oob, rv, real ? uint32_t(j) * vstep : 0u);
+  };
+
+  const float sl2 = P.sl2;
+  fa_u4 qf[4];
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc)
+    qf[dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
+                       : fa_u4{0u, 0u, 0u, 0u};
+  issue(0);
+  issue(1);
+  issue(2);
+  fa2_wait_vm_lgkm0<0>();  // also retires the Q loads in the compiler's bookkeeping
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qf[dc][i] = fa6_scale2<BF16>(qf[dc][i], sl2);
+
+  const Fa6Offs offs;
+  // Reference max: exact maximum over this query's keys 0..31 (key 0 is
+  // always visible), the same for the wavefront's two lanes of a query.
+  float16v mneg;
+  {
+    float16v zero;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) zero[e] = 0.f;
+    float16v x = fa6_scores_half<BF16>(kring, offs, qf, zero, 0);
+    float mt = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kj = 8 * (e >> 2) + 4 * hi + (e & 3);
+      if (!(kj >= P.Sk || (CAUSAL && kj > qi))) mt = fmaxf(mt, x[e]);
+    }
+    mt = fmaxf(mt, fa2_xor32(mt));
+    const float m_use = mt == -INFINITY ? 0.f : mt;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mneg[e] = -m_use;
+  }
+
+  float16v acc[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[db][e] = 0.f;
+  float l_run = 0.f;
+
+  int t = 0;
+  for (; t < t_clean; ++t) {
+    if (t > 0) {
+      fa2_wait_vm_lgkm0<4>();
+      __builtin_amdgcn_s_barrier();
+    }
+    issue(t + 3);
+    const char* kt = kring + (t & 3) * kFa2Tile;
+    const char* vt = vring + (t & 3) * kFa2Tile;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const float16v x = fa6_scores_half<BF16>(kt, offs, qf, mneg, hh);
+      fa_u4 pf[2];
+      l_run += fa6_exp<BF16, false>(x, 0.f, pf);
+      fa6_pv_half<BF16>(vt, offs, pf, acc, hh);
+    }
+  }
+  for (; t < nt; ++t) {
+    if (t > 0) {
+      fa2_wait_vm_lgkm0<4>();
+      __builtin_amdgcn_s_barrier();
+    }
+    issue(t + 3);
+    if (t < ntw) {
+      const char* kt = kring + (t & 3) * kFa2Tile;
+      const char* vt = vring + (t & 3) * kFa2Tile;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j0 = t * kFa2BK + hh * 32;
+        float16v x = fa6_scores_half<BF16>(kt, offs, qf, mneg, hh);
+        if ((CAUSAL && j0 + 31 > q0w) || (j0 + 32 > P.Sk)) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kj = j0 + 8 * (e >> 2) + 4 * hi + (e & 3);
+            if (kj >= P.Sk || (CAUSAL && kj > qi)) x[e] = -INFINITY;
+          }
+        }
+        fa_u4 pf[2];
+        l_run += fa6_exp<BF16, false>(x, 0.f, pf);
+        fa6_pv_half<BF16>(vt, offs, pf, acc, hh);
+      }
+    }
+  }
+  fa2_wait_vm_lgkm0<0>();
+
+  // A P that rounded to infinity shows as a non-finite l or O.
+  bool bad = !(fabsf(l_run) <= 3.0e38f);
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bad |= !(fabsf(acc[db][e]) <= 3.0e38f);
+  if (__any(bad)) {
+    fa7_exact<BF16, CAUSAL>(P, b, h, q0w);
+    return;
+  }
+  fa7_store(P, b, h, qi, acc, l_run);
+}
+
+template <bool BF16, bool CAUSAL>
+void launch_fa7(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uint32_t vb) {
+  bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL>, dim3(unsigned(bh), unsigned(nqb), 1),
+               dim3(kFa2NW * 64), 0, A, kb, vb);
+}
+
 template <bool BF16, bool CAUSAL>
 void launch_fa6(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uint32_t vb) {
   bg::dispatch(ctx, fa6_fwd_kernel<BF16, CAUSAL>, dim3(unsigned(bh), unsigned(nqb), 1),
@@ -950,7 +1217,9 @@ void launch_fa6(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uin
 int attn_version() {
   static const int v = [] {
     const char* e = std::getenv("BG_ATTN_KERNEL");
-    return e && e[0] == '2' ? 2 : 6;
+    if (e && e[0] == '2') return 2;
+    if (e && e[0] == '6') return 6;
+    return 7;
   }();
   return v;
 }
@@ -1025,10 +1294,12 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     const bool r = d.round_scores != 0;
     const uint32_t kb = uint32_t(k_head), vb = uint32_t(v_head);
     Profile prof(ctx, bf ? "attention_bf16" : "attention_f16", bytes, flops);
-    const bool v6 = attn_version() == 6 && !r && (bf || A.sl2 <= 1.0f);
-#define BG_FA2(B_, C_, R_)                                             \
-  (v6 && !R_ ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb) \
-             : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
+    const int ver = attn_version();
+    const bool fast = ver != 2 && !r && (bf || A.sl2 <= 1.0f);
+#define BG_FA2(B_, C_, R_)                                                                     \
+  (fast && !R_ ? (ver == 6 ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb)               \
+                           : launch_fa7<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb))              \
+               : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
     if (bf) {
       if (c) { if (r) BG_FA2(true, true, true); else BG_FA2(true, true, false); }
       else { if (r) BG_FA2(true, false, true); else BG_FA2(true, false, false); }

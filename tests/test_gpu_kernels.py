@@ -422,6 +422,36 @@ def test_attention_late_dominant_key(bridge, rng, causal, dtype, round_scores):
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_attention_dominant_key_long_sequence(bridge, rng, dtype):
+    """C4-length heads where keys 1500 and 40 dominate every earlier key by
+    far more than 2^16: the fast kernel's reference max (from each query's
+    first 32 keys) overflows P for the queries that see them, and those
+    wavefronts must be recomputed exactly; head 1 is plain random data."""
+    b, h, s, d = 1, 2, 2048, 64
+    q = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    k = (0.25 * rng.standard_normal((b, h, s, d))).astype(np.float32)
+    v = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    u = np.ones(d, np.float32) / 2.0
+    q[0, 0] += 4.0 * u
+    k[0, 0, 1500] = 4.0 * u
+    k[0, 0, 40] = 3.0 * u
+    if dtype == "float16":
+        ts = [t.astype(np.float16) for t in (q, k, v)]
+        hs = [up(bridge, t) for t in ts]
+        ref = O.sdpa_amp(*ts, 0.125, True).astype(np.float32)
+    else:
+        ts = [O.f32_to_bf16_bits(t) for t in (q, k, v)]
+        hs = [up(bridge, t, "bfloat16") for t in ts]
+        ref = O.bf16_bits_to_f32(O.sdpa_bf16(*ts, 0.125, True))
+    ho = bridge.attention_ex(*hs, batch=b, heads=h, sq=s, sk=s, d=d, scale=0.125, causal=True,
+                             in_dtype=dtype, round_scores=False)
+    y = bridge.to_numpy(ho)
+    y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
+    assert np.isfinite(y).all()
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
 @pytest.mark.parametrize("round_scores", [False, True])
 def test_attention_strided_fused_qkv_views(bridge, rng, round_scores):
     """Q/K/V as views into one fused QKV projection [B, S, 3, H, D] (the GPT-2

@@ -167,6 +167,7 @@ SIGNATURES = {
     "bg_flash_attention": (C.c_int, [ctx_p, handle_t, handle_t, handle_t, handle_t, C.c_int64, C.c_int64,
                                      C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_int, PH]),
     "bg_matmul_ex": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), PH]),
+    "bg_plan_inspect": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     "bg_matmul_ex2": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), C.POINTER(MatmulExt), PH]),
     "bg_matmul_noalloc": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p]),

@@ -23,7 +23,7 @@ from __future__ import annotations
 
 import ctypes as C
 import json
-from typing import Any, Optional, Sequence, Tuple
+from typing import Any, Dict, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -659,3 +659,23 @@ class HipRealizerBridge:
     # -- reference protocol methods outside this build's scope ---------------------------
     def run_user_kernel(self, *a: Any, **k: Any) -> Any:
         raise JitNotImplementedError("HIP bridge: run_user_kernel takes WGSL, which has no HIP meaning")
+
+
+def inspect_tensor_plan(plan: Any, requests: Any = None) -> Dict[str, Any]:
+    """Parse, validate and fuse a tensor plan without a device
+    (bg_plan_inspect): the steps the executor would run, after its
+    plan-level fusion, as {"steps": [{"value_id", "op", "inputs", ...}],
+    "root_id"}.  Raises KernelError with the executor's own message for a
+    plan it would refuse."""
+    lib = N.load_library()
+    pj = (plan if isinstance(plan, str) else json.dumps(plan, separators=(",", ":"))).encode()
+    rj = None if requests is None else (requests if isinstance(requests, str)
+                                         else json.dumps(requests, separators=(",", ":"))).encode()
+    need = C.c_size_t(0)
+    lib.bg_plan_inspect(pj, rj, None, 0, C.byref(need))
+    buf = C.create_string_buffer(int(need.value))
+    rc = lib.bg_plan_inspect(pj, rj, buf, len(buf), C.byref(need))
+    text = buf.value.decode()
+    if rc != N.BG_OK:
+        raise KernelError(text, rc)
+    return json.loads(text)

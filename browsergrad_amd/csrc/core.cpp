@@ -1106,6 +1106,29 @@ int bg_run_tensor_plan_semantic(bg_ctx* ctx, const char* plan_json, const char* 
                       dst_nbytes, root_out);
 }
 
+int bg_plan_inspect(const char* plan_json, const char* requests_json, char* out, size_t out_cap,
+                    size_t* needed) {
+  std::string text;
+  int rc = BG_OK;
+  try {
+    if (!plan_json) fail(BG_E_INVALID, "plan_inspect: plan is NULL");
+    text = inspect_plan(plan_json, requests_json);
+  } catch (const Error& e) {
+    rc = e.code;
+    text = e.what();
+  } catch (const std::exception& e) {
+    rc = BG_E_INVALID;
+    text = e.what();
+  }
+  if (needed) *needed = text.size() + 1;
+  if (out && out_cap > 0) {
+    const size_t n = std::min(out_cap - 1, text.size());
+    std::memcpy(out, text.data(), n);
+    out[n] = 0;
+  }
+  return rc;
+}
+
 int bg_softmax_last(bg_ctx* ctx, bg_handle x, int64_t rows, int64_t cols, int out_dtype, bg_handle* out) {
   BG_API_BEGIN
   if (!out) fail(BG_E_INVALID, "softmax: NULL output");

@@ -244,6 +244,8 @@ void launch_attention_masked_f32(bg_ctx* ctx, const float* q, const float* k,
 // route); resident: the root must be an allocation of its own.
 bg_handle run_plan(bg_ctx* ctx, const char* json, const char* requests_json, const int64_t* ids,
                    const bg_handle* handles, int n, int dtype, bool resident);
+// Parse, validate and fuse a plan without running it (bg_plan_inspect).
+std::string inspect_plan(const char* json, const char* requests_json);
 
 }  // namespace bg
 

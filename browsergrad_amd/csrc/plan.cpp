@@ -43,33 +43,12 @@
 #include <vector>
 
 #include "core.h"
+#include "plan.h"
 
 namespace bg {
 namespace {
 
 // ---- a small JSON reader ---------------------------------------------------
-
-struct JVal {
-  enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
-  bool b = false;
-  double num = 0;
-  bool is_int = false;  // written without fraction / exponent
-  std::string str;
-  std::vector<JVal> arr;
-  std::vector<std::pair<std::string, JVal>> obj;
-
-  const JVal* get(const char* key) const {
-    if (kind != Obj) return nullptr;
-    for (const auto& kv : obj)
-      if (kv.first == key) return &kv.second;
-    return nullptr;
-  }
-  // snake_case or camelCase (tensor_plan.ts:139-180 accepts both)
-  const JVal* get2(const char* snake, const char* camel) const {
-    const JVal* v = get(camel);
-    return v && v->kind != Null ? v : get(snake);
-  }
-};
 
 class JsonReader {
  public:
@@ -245,27 +224,6 @@ class JsonReader {
   }
 };
 
-// ---- plan model (tensor_plan.ts:63-97) -------------------------------------
-
-struct Step {
-  int64_t step = 0;
-  int64_t value_id = 0;
-  std::string op;
-  std::vector<int64_t> inputs;
-  std::vector<int64_t> shape;
-  std::string dtype;
-  const JVal* arg = nullptr;  // may be null / JSON null
-  // Fused AdamW step (fuse_adamw): the absorbed M and V steps' args.
-  const JVal* arg_m = nullptr;
-  const JVal* arg_v = nullptr;
-};
-
-struct Plan {
-  std::vector<Step> steps;
-  int64_t root_id = 0;
-  int64_t peak_live_bytes = 0;
-};
-
 [[noreturn]] void plan_fail(const std::string& m, int code = BG_E_INVALID) { fail(code, "tensor plan " + m); }
 
 int64_t expect_int(const JVal* v, const std::string& name) {
@@ -310,6 +268,8 @@ Plan normalize(const JVal& root) {
     const JVal* op = s.get("op");
     if (!op || op->kind != JVal::Str) fail(BG_E_INVALID, at + ".op must be a string");
     st.op = op->str;
+    if (st.op.find('+') != std::string::npos)
+      fail(BG_E_INVALID, at + ".op \"" + st.op + "\" is not a plan opcode");
     st.inputs = int_list(s.get2("input_ids", "inputIds"), at + ".inputIds");
     st.shape = int_list(s.get("shape"), at + ".shape");
     if (st.shape.size() > BG_MAX_RANK)
@@ -320,7 +280,9 @@ Plan normalize(const JVal& root) {
     const JVal* dt = s.get("dtype");
     if (!dt || dt->kind != JVal::Str) fail(BG_E_INVALID, at + ".dtype must be a string");
     st.dtype = dt->str;
-    plan_dtype(st.dtype, at + ".dtype");
+    // float64 appears only on constants (NumPy scalars before AMP's CAST);
+    // they are held as float32, which is what the CAST that reads them yields.
+    if (!(st.op == "CONST" && st.dtype == "float64")) plan_dtype(st.dtype, at + ".dtype");
     st.arg = s.get("arg");
     p.steps.push_back(std::move(st));
   }
@@ -806,7 +768,8 @@ struct Runner {
   }
 
   bg_handle fused(const Step& s, std::vector<bg_handle> ins, const std::vector<bg_fused_op>& ops,
-                  const std::vector<double>& imms, int out_dtype) {
+                  const std::vector<double>& imms, int out_dtype, int reduce_op = BG_RED_NONE,
+                  bool keepdims = false) {
     std::vector<int64_t> strides;
     bool all_equal = true;
     for (bg_handle h : ins)
@@ -828,6 +791,8 @@ struct Runner {
     d.rank = int(shape.size());
     d.shape = shape.data();
     d.out_dtype = out_dtype;
+    d.reduce_op = reduce_op;
+    d.reduce_keepdims = keepdims ? 1 : 0;
     bg_handle out = 0;
     call(bg_fused_ex(ctx, &d, &out));
     if (s.shape.empty()) ctx->handles[out].shape.clear();
@@ -891,7 +856,93 @@ struct Runner {
 
   bg_handle exec(const Step& s) {
     const std::string& op = s.op;
-    const int dt = plan_dtype(s.dtype, "steps[" + std::to_string(s.step) + "].dtype");
+    const int dt = s.op == "CONST" && s.dtype == "float64" ? BG_F32
+                                                           : plan_dtype(s.dtype, "steps[" + std::to_string(s.step) + "].dtype");
+    if (op == "+PROGRAM") {
+      std::vector<bg_handle> ins;
+      for (size_t i = 0; i < s.inputs.size(); ++i) ins.push_back(need(s, i));
+      Step it = s;  // iteration shape for the broadcast strides
+      it.shape = s.iter;
+      bg_handle out = fused(it, ins, s.prog, s.imms, dt, s.reduce_op, s.keepdims);
+      ctx->handles[out].shape = s.shape;
+      return out;
+    }
+    if (op == "+LINEAR") {
+      bg_matmul_desc d = s.mm;
+      bg_matmul_ext e = s.mm_ext;
+      d.a = need(s, 0);
+      d.b = need(s, 1);
+      size_t nxt = 2;
+      if (s.has_bias) d.bias = need(s, nxt++);
+      if (s.has_residual) e.residual = need(s, nxt++);
+      // An operand already held in the GEMM's dtype needs no cast (a plan
+      // may declare a view's dtype as built rather than as carried).
+      if (rec(d.a).dtype == d.in_dtype) e.a_dtype = -1;
+      if (rec(d.b).dtype == d.in_dtype) e.b_dtype = -1;
+      d.stride_a = d.m * d.lda;
+      d.stride_b = (d.trans_b ? d.n : d.k) * d.ldb;
+      d.stride_c = d.m * d.ldc;
+      bg_handle out = 0;
+      call(bg_matmul_ex2(ctx, &d, &e, &out));
+      ctx->handles[out].shape = s.shape;
+      return own(out);
+    }
+    if (op == "+ATTENTION") {
+      bg_attention_desc d = s.att;
+      d.q = need(s, 0);
+      d.k = need(s, 1);
+      d.v = need(s, 2);
+      d.q_ss = d.d;
+      d.q_sh = d.sq * d.d;
+      d.q_sb = d.heads * d.sq * d.d;
+      d.k_ss = d.v_ss = d.d;
+      d.k_sh = d.v_sh = d.sk * d.d;
+      d.k_sb = d.v_sb = d.heads * d.sk * d.d;
+      bg_handle out = 0;
+      call(bg_attention_ex(ctx, &d, &out));
+      ctx->handles[out].shape = s.shape;
+      return own(out);
+    }
+    if (op == "SLICE") {
+      // arg.slices: one [start, stop, step] per axis, step >= 1 (extension).
+      bg_handle src = need(s, 0);
+      const Record& r = rec(src);
+      const JVal& sl = expect_arr(s.arg && s.arg->kind == JVal::Obj ? s.arg->get("slices") : nullptr,
+                                  "tensor plan SLICE.arg.slices");
+      if (sl.arr.size() != r.shape.size()) plan_fail("SLICE needs one [start, stop, step] per axis");
+      std::vector<int64_t> cstr(r.shape.size(), 1);
+      for (int i = int(r.shape.size()) - 2; i >= 0; --i) cstr[size_t(i)] = cstr[size_t(i) + 1] * r.shape[size_t(i) + 1];
+      int64_t offset = 0;
+      std::vector<int64_t> shape, strides;
+      for (size_t i = 0; i < sl.arr.size(); ++i) {
+        const std::vector<int64_t> t = int_list(&sl.arr[i], "tensor plan SLICE.arg.slices[" + std::to_string(i) + "]");
+        if (t.size() != 3 || t[2] < 1 || t[0] < 0 || t[1] < t[0] || t[1] > r.shape[i])
+          plan_fail("SLICE axis " + std::to_string(i) + " needs 0 <= start <= stop <= extent and step >= 1");
+        offset += t[0] * cstr[i];
+        shape.push_back((t[1] - t[0] + t[2] - 1) / t[2]);
+        strides.push_back(t[2] * cstr[i]);
+      }
+      if (shape != s.shape) plan_fail("SLICE output shape differs from the plan");
+      bg_handle out = 0;
+      call(bg_copy_strided(ctx, src, offset, shape.data(), strides.data(), int(shape.size()), &out));
+      return own(out);
+    }
+    if (op == "CAUSAL_MASK") {
+      // The top-left-aligned causal mask of SDPA (extension): bool
+      // [.., rows, cols], true where the key index exceeds the query index
+      // (numpy.triu(ones, k=1)).  Built on the host when no fused attention
+      // absorbed it.
+      if (s.shape.size() < 2 || dt != BG_BOOL) plan_fail("CAUSAL_MASK must be a bool matrix");
+      const int64_t rows = s.shape[s.shape.size() - 2], cols = s.shape.back();
+      const int64_t lead = numel(s.shape) / std::max<int64_t>(rows * cols, 1);
+      std::vector<uint8_t> host(size_t(numel(s.shape)));
+      for (int64_t b = 0; b < lead; ++b)
+        for (int64_t i = 0; i < rows; ++i)
+          for (int64_t j = 0; j < cols; ++j) host[size_t((b * rows + i) * cols + j)] = j > i ? 1 : 0;
+      bg_handle out = 0;
+      call(bg_upload(ctx, host.data(), host.size(), s.shape.data(), int(s.shape.size()), BG_BOOL, &out));
+      return own(out);
+    }
     if (op == "BUFFER") {
       auto it = vals.find(s.value_id);  // pre-bound by the caller
       if (it == vals.end()) plan_fail("missing BUFFER input " + std::to_string(s.value_id));
@@ -1263,15 +1314,53 @@ struct Runner {
 
 }  // namespace
 
+// Parses, validates and fuses a plan without a device (bg_plan_inspect):
+// one JSON object per step the executor would run, in order.
+std::string inspect_plan(const char* json, const char* requests_json) {
+  JVal doc = JsonReader(json, "tensor plan").parse();
+  Plan plan = normalize(doc);
+  std::unordered_map<int64_t, std::vector<int64_t>> sem;
+  if (requests_json) sem = bind_requests(plan, parse_requests(requests_json));
+  fuse_adamw(plan);
+  fuse_plan(plan, requests_json ? &sem : nullptr);
+  std::string out = "{\"steps\":[";
+  for (size_t i = 0; i < plan.steps.size(); ++i) {
+    const Step& s = plan.steps[i];
+    if (i) out += ",";
+    out += "{\"value_id\":" + std::to_string(s.value_id) + ",\"op\":\"";
+    for (char c : s.op) {
+      if (c == '"' || c == '\\') out += '\\';
+      out += (unsigned char)c < 0x20 ? '?' : c;
+    }
+    out += "\",\"inputs\":[";
+    for (size_t j = 0; j < s.inputs.size(); ++j) out += (j ? "," : "") + std::to_string(s.inputs[j]);
+    out += "]";
+    if (s.op == "+PROGRAM") {
+      out += ",\"n_ops\":" + std::to_string(s.prog.size()) + ",\"reduce\":" + std::to_string(s.reduce_op);
+    } else if (s.op == "+LINEAR") {
+      out += ",\"trans_b\":" + std::to_string(s.mm.trans_b) + ",\"round\":" + std::to_string(s.mm.round_f16) +
+             ",\"act\":" + std::to_string(s.mm.act) + ",\"bias\":" + std::to_string(int(s.has_bias)) +
+             ",\"residual\":" + std::to_string(int(s.has_residual)) + ",\"a_dtype\":" +
+             std::to_string(s.mm_ext.a_dtype) + ",\"b_dtype\":" + std::to_string(s.mm_ext.b_dtype);
+    } else if (s.op == "+ATTENTION") {
+      out += ",\"causal\":" + std::to_string(s.att.causal) + ",\"scale\":" + std::to_string(s.att.scale);
+    }
+    out += "}";
+  }
+  out += "],\"root_id\":" + std::to_string(plan.root_id) + "}";
+  return out;
+}
+
 bg_handle run_plan(bg_ctx* ctx, const char* json, const char* requests_json, const int64_t* ids,
                    const bg_handle* handles, int n, int dtype, bool resident) {
   if (dtype != BG_F32 && dtype != BG_F16 && dtype != BG_BF16 && dtype != BG_BOOL)
     fail(BG_E_DTYPE, "run_tensor_plan: dtype not supported");
   JVal doc = JsonReader(json, "tensor plan").parse();
   Plan plan = normalize(doc);
-  fuse_adamw(plan);
   std::unordered_map<int64_t, std::vector<int64_t>> sem;
   if (requests_json) sem = bind_requests(plan, parse_requests(requests_json));
+  fuse_adamw(plan);
+  fuse_plan(plan, requests_json ? &sem : nullptr);
 
   Runner R{ctx};
   if (requests_json) R.sem_axes = &sem;

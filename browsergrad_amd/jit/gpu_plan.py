@@ -14,9 +14,9 @@ permutation), and plan_summary() erases each PERMUTE's legacy arg to None
 (:252-258).
 
 Differences from the reference (the executor in libbghip lowers them):
-CMP, WHERE and CONST are accepted, as are rank > 2 MATMULs and float16 /
-bfloat16 / bool values; the reference refuses WHERE here (:561-566) and its
-executor refuses the rest.
+CMP, WHERE, CONST, SLICE and CAUSAL_MASK are accepted, as are rank > 2
+MATMULs and float16 / bfloat16 / bool values; the reference refuses WHERE
+here (:561-566) and its executor refuses the rest.
 """
 from __future__ import annotations
 
@@ -30,7 +30,7 @@ from .ir import (
     CONV_OPS,
     OP_ADD, OP_BROADCAST_TO, OP_BUFFER, OP_CAST, OP_CMP, OP_CONST, OP_CUSTOM, OP_DIV, OP_EXP,
     OP_FUSED_ELEMENTWISE, OP_FUSED_SOFTMAX, OP_LAYER_NORM, OP_LOAD, OP_LOG, OP_MATMUL, OP_MUL, OP_NEG,
-    OP_PERMUTE, OP_REDUCE, OP_RESHAPE, OP_WHERE, UOp, toposort,
+    OP_CAUSAL_MASK, OP_PERMUTE, OP_REDUCE, OP_RESHAPE, OP_SLICE, OP_WHERE, UOp, toposort,
 )
 from ..errors import JitNotImplementedError
 
@@ -41,10 +41,14 @@ _WIRE_I64_MAX = (1 << 63) - 1
 
 _DTYPE_BYTES = {"float32": 4, "float16": 2, "bfloat16": 2, "float64": 8, "int64": 8, "int32": 4, "bool": 1}
 
+# OP_CAUSAL_MASK (extension, ir.py): the plan builder of the HIP route
+# writes it in place of a LOAD of a causal-mask buffer, so the executor can
+# recognise masked attention without reading the mask.
+
 PLAN_OPS = frozenset({
     OP_BUFFER, OP_LOAD, OP_CONST, OP_CAST, OP_ADD, OP_MUL, OP_DIV, OP_NEG, OP_EXP, OP_LOG, OP_CMP, OP_WHERE,
     OP_MATMUL, OP_REDUCE, OP_RESHAPE, OP_PERMUTE, OP_BROADCAST_TO, OP_LAYER_NORM, OP_FUSED_ELEMENTWISE,
-    OP_FUSED_SOFTMAX,
+    OP_FUSED_SOFTMAX, OP_SLICE, OP_CAUSAL_MASK,
 }) | CONV_OPS
 
 
@@ -238,5 +242,5 @@ __all__ = [
     "PLAN_OPS", "PlanStep", "PlanBuffer", "GpuExecutionPlan", "DensePermutationViewCopyRequest",
     "GpuExecutionSubmission", "GpuPlanUnsupported", "build_gpu_execution_plan", "build_gpu_execution_submission",
     "gpu_plan_summary", "plan_json", "TENSOR_PLAN_SEMANTIC_REQUEST_SCHEMA", "TENSOR_PLAN_SEMANTIC_REQUEST_VERSION",
-    "DENSE_PERMUTATION_VIEW_COPY_REQUEST",
+    "DENSE_PERMUTATION_VIEW_COPY_REQUEST", "OP_CAUSAL_MASK",
 ]

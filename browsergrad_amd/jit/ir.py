@@ -63,15 +63,18 @@ CONV_OPS: FrozenSet[str] = frozenset(
 OP_HIP_LINEAR = "HIP_LINEAR"          # GEMM + AMP rounding + bias + activation epilogue
 OP_HIP_ATTENTION = "HIP_ATTENTION"    # the SDPA subgraph as one flash-attention kernel
 OP_HIP_REDUCE_FUSED = "HIP_REDUCE_FUSED"  # elementwise program + last-axis reduction
+# Plan-only leaf of the HIP tensor-plan route: the top-left causal mask
+# ([lq, lk] bool, true where the key index exceeds the query index).
+OP_CAUSAL_MASK = "CAUSAL_MASK"
 
 ALL_OPS: FrozenSet[str] = frozenset({
     OP_BUFFER, OP_LOAD, OP_CONST, OP_CAST, OP_ADD, OP_MUL, OP_DIV, OP_NEG, OP_EXP, OP_LOG,
     OP_CMP, OP_WHERE, OP_MATMUL, OP_REDUCE, OP_RESHAPE, OP_PERMUTE, OP_SLICE, OP_BROADCAST_TO,
     OP_LAYER_NORM, OP_FUSED_ELEMENTWISE, OP_FUSED_SOFTMAX, OP_ATTENTION_FORWARD, OP_CUSTOM,
-    OP_HIP_LINEAR, OP_HIP_ATTENTION, OP_HIP_REDUCE_FUSED,
+    OP_HIP_LINEAR, OP_HIP_ATTENTION, OP_HIP_REDUCE_FUSED, OP_CAUSAL_MASK,
 }) | CONV_OPS
 
-_LEAF_OPS: FrozenSet[str] = frozenset({OP_BUFFER, OP_CONST})
+_LEAF_OPS: FrozenSet[str] = frozenset({OP_BUFFER, OP_CONST, OP_CAUSAL_MASK})
 
 # NumPy dtype names (_ir.py:348-353) plus "bfloat16", an extension of this build.
 KNOWN_DTYPES: FrozenSet[str] = frozenset({

@@ -37,15 +37,15 @@ from . import config
 from .amp import insert_cast_pass
 from .attention_forward import validate_attention_forward_node
 from .buffers import BufferTable, GpuBufferTable
-from .fusion import fuse
-from .gpu_plan import build_gpu_execution_submission
-from .hip_fusion import hip_fuse
+from .fusion import fuse, substitute
+from .gpu_plan import GpuPlanUnsupported, build_gpu_execution_plan, build_gpu_execution_submission
+from .hip_fusion import hip_fuse, refresh_dtypes
 from .ir import (
     CONV_OPS,
     OP_ADD, OP_ATTENTION_FORWARD, OP_BROADCAST_TO, OP_BUFFER, OP_CAST, OP_CMP, OP_CONST, OP_CUSTOM, OP_DIV,
     OP_EXP, OP_FUSED_ELEMENTWISE, OP_FUSED_SOFTMAX, OP_HIP_ATTENTION, OP_HIP_LINEAR, OP_HIP_REDUCE_FUSED,
-    OP_LAYER_NORM, OP_LOAD, OP_LOG, OP_MATMUL, OP_MUL, OP_NEG, OP_PERMUTE, OP_REDUCE, OP_RESHAPE, OP_SLICE,
-    OP_WHERE,
+    OP_CAUSAL_MASK, OP_LAYER_NORM, OP_LOAD, OP_LOG, OP_MATMUL, OP_MUL, OP_NEG, OP_PERMUTE, OP_REDUCE, OP_RESHAPE,
+    OP_SLICE, OP_WHERE,
     UOp, toposort,
 )
 from .program import NotLowerable, ProgramTooLarge, broadcast_strides, compile_program
@@ -535,11 +535,51 @@ def realize_hip(root: UOp, buffers: BufferTable, gpu_buffer_table: Optional[GpuB
 
 # ---- plan route (_realize_webgpu.py:476-589) -------------------------------------------
 
-def _plan_submission(root: UOp) -> Tuple[dict, dict, str]:
-    sub = build_gpu_execution_submission(insert_cast_pass(root))
+def _plan_leaves(root: UOp, bt: BufferTable) -> UOp:
+    """Leaves the plan can state by value: a LOAD of a full() buffer becomes a
+    CONST of its shape (same values, no upload), a LOAD of a causal-mask
+    buffer a CAUSAL_MASK step (same values; lets the executor's plan-level
+    fuser recognise masked attention without reading the mask)."""
+    subs = {}
+    for n in toposort(root):
+        if n.op != OP_LOAD or not n.inputs or n.inputs[0].op != OP_BUFFER:
+            continue
+        bid = n.inputs[0].arg
+        fill = bt.fill_value(bid)
+        if fill is not None:
+            subs[id(n)] = UOp(OP_CONST, (), n.shape, n.dtype, {"value": float(fill)})
+            continue
+        cm = bt.causal_mask(bid)
+        if cm is not None:
+            subs[id(n)] = UOp(OP_CAUSAL_MASK, (), n.shape, "bool", {"rows": cm[0], "cols": cm[1]})
+    return substitute(root, subs) if subs else root
+
+
+def _plan_submission(root: UOp, bt: BufferTable) -> Tuple[dict, dict, str]:
+    """The plan and its semantic side table.  A PERMUTE the side table cannot
+    carry (rank other than 2 or 3, or not float32, as in attention's head
+    split and K transpose) sends the whole plan down the legacy route: every
+    PERMUTE keeps its axes in arg and no requests travel."""
+    # Views after cast insertion declare the dtype they were built with while
+    # their input turned narrow; the plan states the dtype the data has.
+    graph = _plan_leaves(refresh_dtypes(insert_cast_pass(root)), bt)
+    try:
+        sub = build_gpu_execution_submission(graph)
+    except GpuPlanUnsupported as e:
+        if "GPU semantic request" not in str(e):
+            raise
+        plan = build_gpu_execution_plan(graph).summary()
+        req = {"requests": []}
+        return plan, req, ""
     plan = sub.plan_summary()
     req = sub.semantic_request_summary()
     return plan, req, json.dumps(req, ensure_ascii=True, separators=(",", ":"), sort_keys=True)
+
+
+def _plan_root_dtype(plan: dict) -> str:
+    """dtype of the plan's root after cast insertion (an autocast graph's
+    output may be narrower than the graph as built)."""
+    return next(st["dtype"] for st in plan["steps"] if st["value_id"] == plan["root_id"])
 
 
 def _plan_inputs(plan: dict, bt: BufferTable, gbt: GpuBufferTable) -> list:
@@ -562,30 +602,33 @@ def _plan_inputs(plan: dict, bt: BufferTable, gbt: GpuBufferTable) -> list:
 
 def realize_tensor_plan_hip(root: UOp, buffers: BufferTable,
                             gpu_buffer_table: Optional[GpuBufferTable] = None) -> np.ndarray:
-    """PERMUTE steps travel only in the semantic side table, so a plan with
-    any PERMUTE runs through run_tensor_plan_semantic (legacy execution of
-    such a plan is refused, _realize_webgpu.py:476-522)."""
+    """PERMUTE steps travel in the semantic side table when it can carry them
+    (run_tensor_plan_semantic, as _realize_webgpu.py:476-522 requires);
+    plans with a PERMUTE it cannot carry (attention's rank-4 head split and
+    K transpose) run on the legacy route with the axes in the step arg."""
     gbt = _table(gpu_buffer_table)
-    plan, req, req_json = _plan_submission(root)
+    plan, req, req_json = _plan_submission(root, buffers)
     inputs = _plan_inputs(plan, buffers, gbt)
+    dtype = _plan_root_dtype(plan)
     if req["requests"]:
-        data = gbt.bridge.run_tensor_plan_semantic(plan, req_json, inputs, root.dtype)
+        data = gbt.bridge.run_tensor_plan_semantic(plan, req_json, inputs, dtype)
     else:
-        data = gbt.bridge.run_tensor_plan(plan, inputs, root.dtype)
-    arr = np.frombuffer(data, dtype=_np_dtype(root.dtype))
+        data = gbt.bridge.run_tensor_plan(plan, inputs, dtype)
+    arr = np.frombuffer(data, dtype=_np_dtype(dtype))
     return np.array(arr.reshape(root.shape) if root.shape else arr.reshape(()), copy=True)
 
 
 def realize_tensor_plan_hip_resident(root: UOp, buffers: BufferTable,
                                      gpu_buffer_table: Optional[GpuBufferTable] = None) -> str:
     gbt = _table(gpu_buffer_table)
-    plan, req, req_json = _plan_submission(root)
+    plan, req, req_json = _plan_submission(root, buffers)
     inputs = _plan_inputs(plan, buffers, gbt)
+    dtype = _plan_root_dtype(plan)
     if req["requests"]:
-        h = gbt.bridge.run_tensor_plan_resident_semantic(plan, req_json, inputs, root.dtype)
+        h = gbt.bridge.run_tensor_plan_resident_semantic(plan, req_json, inputs, dtype)
     else:
-        h = gbt.bridge.run_tensor_plan_resident(plan, inputs, root.dtype)
-    bid = buffers.new_unmaterialized_buffer(root.shape, root.dtype)
+        h = gbt.bridge.run_tensor_plan_resident(plan, inputs, dtype)
+    bid = buffers.new_unmaterialized_buffer(root.shape, dtype)
     gbt.register(bid, h)
     return bid
 

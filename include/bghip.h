@@ -501,6 +501,16 @@ int bg_run_tensor_plan_semantic(bg_ctx* ctx, const char* plan_json,
                                 int dtype, void* dst, size_t dst_nbytes,
                                 bg_handle* root_out);
 
+/* Device-free plan check (extension; no context, no GPU): parses and
+ * validates `plan_json` (and `requests_json` when non-NULL) exactly as
+ * bg_run_tensor_plan does, applies the plan-level fusion, and writes into
+ * `out` (capacity out_cap, always NUL-terminated) a JSON summary of the steps
+ * the executor would run ({"steps":[{"value_id","op","inputs",...}],
+ * "root_id"}), or the refusal message when the status is not BG_OK.
+ * *needed (when non-NULL) receives the full length + 1. */
+int bg_plan_inspect(const char* plan_json, const char* requests_json, char* out, size_t out_cap,
+                    size_t* needed);
+
 /* Raw device pointer of a handle (extension; for harnesses that time
  * kernels with their own events).  Valid until the handle is released. */
 int bg_device_ptr(bg_ctx* ctx, bg_handle h, void** ptr);

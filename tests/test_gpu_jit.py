@@ -154,17 +154,43 @@ def test_chained_matmul_residency(bridge):
 # ---- plan route --------------------------------------------------------------------
 
 PLAN_CASES = [("c1", 1.0, {}, 1e-4), ("c2", 1 / 16, {}, 1e-4), ("c3", 1 / 16, {"amp": False}, 1e-4),
-              ("c3", 1 / 16, {}, 2e-2)]
+              ("c3", 1 / 16, {}, 2e-2), ("c4", 1 / 8, {}, 2e-2), ("c5", 1 / 4, {}, 2e-2)]
+PLAN_IDS = ["c1", "c2", "c3_fp32", "c3", "c4", "c5"]
+# Kernel launches (profile scopes) of each config's plan after the
+# executor's plan-level fusion: GEMM + bias (+ relu / residual) epilogues,
+# one fused program for elementwise chains (+ trailing reduction), one
+# attention kernel for the SDPA steps.
+PLAN_LAUNCHES = {
+    "c1": {"gemm_f32": 2},
+    "c2": {"fused_reduce": 1},
+    "c3_fp32": {"gemm_f32": 1},
+    "c3": {"gemm_a_cast": 1, "gemm_b_cast": 1, "gemm_f16": 1},
+    "c4": {"attention_f16": 1},
+}
 
 
-@pytest.mark.parametrize("name,scale,kw,tol", PLAN_CASES, ids=["c1", "c2", "c3_fp32", "c3"])
+@pytest.mark.parametrize("name,scale,kw,tol", PLAN_CASES, ids=PLAN_IDS)
 def test_plan_route_configs(bridge, table, name, scale, kw, tol):
     s, y = configs.BUILDERS[name](scale=scale, **kw)
     ref = G.evaluate(y.uop, s.buffers)
     alive = bridge.aliveHandleCount()
-    out = realize_tensor_plan_hip(y.uop, s.buffers, table)
+    bridge.set_profiling(True)
+    n0 = len(bridge.flushProfiles()["passProfiles"])  # the list accumulates over the context's life
+    try:
+        out = realize_tensor_plan_hip(y.uop, s.buffers, table)
+        labels = [p["label"] for p in bridge.flushProfiles()["passProfiles"][n0:]]
+    finally:
+        bridge.set_profiling(False)
     _check(out, ref, tol)
     assert bridge.aliveHandleCount() == alive  # plan inputs were host data, all released
+    counts = {lb: labels.count(lb) for lb in set(labels)}
+    key = PLAN_IDS[PLAN_CASES.index((name, scale, kw, tol))]
+    if key in PLAN_LAUNCHES:
+        assert counts == PLAN_LAUNCHES[key], counts
+    else:  # c5: one attention, four GEMMs with their epilogues, two LayerNorms
+        assert counts.get("attention_f16") == 1 and counts.get("gemm_f16") == 4, counts
+        assert counts.get("layer_norm") == 2 and "softmax" not in counts and "fused_reduce" not in counts, counts
+        assert counts.get("fused_elementwise", 0) == 1, counts  # the GELU program
 
 
 def test_plan_route_semantic_and_resident(bridge, table):

@@ -226,9 +226,12 @@ class JsonReader {
 
 [[noreturn]] void plan_fail(const std::string& m, int code = BG_E_INVALID) { fail(code, "tensor plan " + m); }
 
+// Integers travel as JSON numbers (doubles): only those a double holds
+// exactly (|x| <= 2^53) are accepted, so the conversion is always defined.
 int64_t expect_int(const JVal* v, const std::string& name) {
-  if (!v || v->kind != JVal::Num || !std::isfinite(v->num) || v->num != std::floor(v->num))
-    fail(BG_E_INVALID, name + " must be an integer");
+  if (!v || v->kind != JVal::Num || !std::isfinite(v->num) || v->num != std::floor(v->num) ||
+      std::fabs(v->num) > 9007199254740992.0)
+    fail(BG_E_INVALID, name + " must be an integer (|x| <= 2^53)");
   return int64_t(v->num);
 }
 
@@ -1002,10 +1005,15 @@ struct Runner {
           plan_fail(at + " must be [opcode, lhs, rhs?]");
         if (it.arr[0].kind != JVal::Str) plan_fail(at + "[0] must be a string");
         int code = opcode(it.arr[0].str, at);
-        int32_t a = int32_t(expect_int(&it.arr[1], "tensor plan " + at + "[1]"));
+        auto ref32 = [&](const JVal* v, const std::string& name) {
+          const int64_t r = expect_int(v, name);
+          if (r < -1024 || r > 1024) plan_fail(at + " reference out of range");
+          return int32_t(r);
+        };
+        int32_t a = ref32(&it.arr[1], "tensor plan " + at + "[1]");
         int32_t b = a, c = 0;
-        if (it.arr.size() >= 3 && it.arr[2].kind != JVal::Null) b = int32_t(expect_int(&it.arr[2], "tensor plan " + at + "[2]"));
-        if (it.arr.size() == 4 && it.arr[3].kind != JVal::Null) c = int32_t(expect_int(&it.arr[3], "tensor plan " + at + "[3]"));
+        if (it.arr.size() >= 3 && it.arr[2].kind != JVal::Null) b = ref32(&it.arr[2], "tensor plan " + at + "[2]");
+        if (it.arr.size() == 4 && it.arr[3].kind != JVal::Null) c = ref32(&it.arr[3], "tensor plan " + at + "[3]");
         prog.push_back({code, a, b, c});
       }
       std::vector<bg_handle> ins;

@@ -102,6 +102,15 @@ struct Graph {
   }
 };
 
+// An integral JSON number a double holds exactly (|x| <= 2^53).
+bool as_int(const JVal& v, int64_t& out) {
+  if (v.kind != JVal::Num || !std::isfinite(v.num) || v.num != std::floor(v.num) ||
+      std::fabs(v.num) > 9007199254740992.0)
+    return false;
+  out = int64_t(v.num);
+  return true;
+}
+
 const JVal* arg_field(const Step& s, const char* key) {
   return s.arg && s.arg->kind == JVal::Obj ? s.arg->get(key) : nullptr;
 }
@@ -135,7 +144,8 @@ bool axes_are(const Step& s, std::initializer_list<int64_t> want) {
   size_t i = 0;
   for (int64_t w : want) {
     const JVal& e = a->arr[i++];
-    if (e.kind != JVal::Num || int64_t(e.num) != w) return false;
+    int64_t x;
+    if (!as_int(e, x) || x != w) return false;
   }
   return true;
 }
@@ -271,13 +281,9 @@ bool linear_epilogue_program(const Step& f, int64_t mm_id, int64_t& bias_id, int
   if (!ops || ops->kind != JVal::Arr || ops->arr.empty() || ops->arr.size() > 2) return false;
   auto op_at = [&](size_t i, std::string& code, int64_t& a, int64_t& b) {
     const JVal& o = ops->arr[i];
-    if (o.kind != JVal::Arr || o.arr.size() < 3 || o.arr[0].kind != JVal::Str || o.arr[1].kind != JVal::Num ||
-        o.arr[2].kind != JVal::Num)
-      return false;
+    if (o.kind != JVal::Arr || o.arr.size() < 3 || o.arr[0].kind != JVal::Str) return false;
     code = o.arr[0].str;
-    a = int64_t(o.arr[1].num);
-    b = int64_t(o.arr[2].num);
-    return true;
+    return as_int(o.arr[1], a) && as_int(o.arr[2], b);
   };
   auto input_of = [&](int64_t ref) -> int64_t {  // ref < 0 -> input value id
     const size_t i = size_t(-ref - 1);
@@ -604,8 +610,8 @@ bool build_program(const Graph& g, const std::vector<size_t>& members, std::vect
             x[j - 1] = x[0];
             continue;
           }
-          if (o.arr[j].kind != JVal::Num) return false;
-          const int64_t rr = int64_t(o.arr[j].num);
+          int64_t rr;
+          if (!as_int(o.arr[j], rr)) return false;
           if (rr < 0) {
             if (size_t(-rr - 1) >= in_refs.size()) return false;
             x[j - 1] = in_refs[size_t(-rr - 1)];
@@ -658,9 +664,10 @@ void fuse_elementwise(Plan& plan) {
       const JVal* ax = arg_field(top_step, "axis");
       const int64_t rank = int64_t(src->shape.size());
       bool last = false;
-      if (ax && ax->kind == JVal::Num) last = int64_t(ax->num) == rank - 1 || int64_t(ax->num) == -1;
-      else if (ax && ax->kind == JVal::Arr && ax->arr.size() == 1 && ax->arr[0].kind == JVal::Num)
-        last = int64_t(ax->arr[0].num) == rank - 1 || int64_t(ax->arr[0].num) == -1;
+      int64_t a0;
+      if (ax && as_int(*ax, a0)) last = a0 == rank - 1 || a0 == -1;
+      else if (ax && ax->kind == JVal::Arr && ax->arr.size() == 1 && as_int(ax->arr[0], a0))
+        last = a0 == rank - 1 || a0 == -1;
       else if ((!ax || ax->kind == JVal::Null) && rank == 1) last = true;
       if (!last) continue;
       const JVal* kd = arg_field(top_step, "keepdims");
@@ -745,6 +752,16 @@ void fuse_plan(Plan& plan, const std::unordered_map<int64_t, std::vector<int64_t
   // named passes (for comparisons and diagnosis); unset runs all three.
   const char* sel = std::getenv("BG_PLAN_FUSION");
   auto on = [&](const char* pass) { return !sel || std::string(sel).find(pass) != std::string::npos; };
+  // The matchers read inputs by position: a plan with a step of the wrong
+  // arity is left unfused (the executor refuses that step when it runs it).
+  static const std::unordered_map<std::string, size_t> arity = {
+      {"CAST", 1}, {"PERMUTE", 1}, {"FUSED_SOFTMAX", 1}, {"NEG", 1}, {"EXP", 1}, {"LOG", 1}, {"REDUCE", 1},
+      {"LOAD", 1}, {"RESHAPE", 1}, {"SLICE", 1}, {"ADD", 2}, {"MUL", 2}, {"DIV", 2}, {"CMP", 2},
+      {"MATMUL", 2}, {"WHERE", 3}, {"CONST", 0}, {"CAUSAL_MASK", 0}, {"BUFFER", 0}};
+  for (const Step& s : plan.steps) {
+    auto it = arity.find(s.op);
+    if (it != arity.end() && s.inputs.size() != it->second) return;
+  }
   g_sem_axes = sem_axes;
   if (on("sdpa")) fuse_sdpa(plan);
   if (on("linear")) fuse_linear(plan);

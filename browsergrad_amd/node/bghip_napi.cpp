@@ -6,13 +6,17 @@
 // include/bghip.h; the context is a napi External owned by the JS bridge
 // object.  Failures become a JS Error named "KernelError" whose message is
 // bg_last_error(ctx), like the reference's op-qualified KernelError
-// (types.ts:87-92).  Everything here is synchronous; index.js wraps the
-// methods the reference declares async (materialize, flash_attention, the
-// plan runs, flushProfiles) in Promises.
+// (types.ts:87-92).  materializeAsync and runTensorPlanAsync return Promises
+// settled off the event loop: the blocking read-back runs on a libuv worker
+// (napi_async_work), as the reference resolves them after mapAsync
+// (realizer.ts:79-91, runner.ts:537-581).  A context is used by one thread
+// at a time: every binding holds the context's mutex while it calls the
+// library, so a call made while a worker is busy waits for it.
 #include <node_api.h>
 
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -22,6 +26,7 @@ namespace {
 
 struct Ctx {
   bg_ctx* ctx = nullptr;
+  std::mutex mu;  // one thread in the library per context
 };
 
 void finalize_ctx(napi_env, void* data, void*) {
@@ -51,6 +56,8 @@ struct Args {
   napi_env env;
   std::vector<napi_value> v;
   bool ok = true;
+  Ctx* holder = nullptr;
+  std::unique_lock<std::mutex> lock;  // held for the rest of the call once ctx() is read
   Args(napi_env e, napi_callback_info info, size_t n) : env(e), v(n) {
     size_t argc = n;
     napi_get_cb_info(e, info, &argc, v.data(), nullptr, nullptr);
@@ -66,7 +73,9 @@ struct Args {
       ok = false;
       return nullptr;
     }
-    return static_cast<Ctx*>(p)->ctx;
+    holder = static_cast<Ctx*>(p);
+    lock = std::unique_lock<std::mutex>(holder->mu);
+    return holder->ctx;
   }
   double num(size_t i) {
     double d = 0;
@@ -175,9 +184,12 @@ napi_value CtxDestroy(napi_env env, napi_callback_info info) {
   void* p = nullptr;
   napi_get_value_external(env, a.v[0], &p);
   auto* c = static_cast<Ctx*>(p);
-  if (c && c->ctx) {
-    bg_ctx_destroy(c->ctx);
-    c->ctx = nullptr;
+  if (c) {
+    std::lock_guard<std::mutex> lk(c->mu);  // waits for a read-back in flight
+    if (c->ctx) {
+      bg_ctx_destroy(c->ctx);
+      c->ctx = nullptr;
+    }
   }
   return nullptr;
 }
@@ -371,6 +383,124 @@ napi_value RunTensorPlan(napi_env env, napi_callback_info info) {
   return bytes(env, buf.data(), buf.size());
 }
 
+// ---- Promise-returning read-backs (napi_async_work) ---------------------------
+
+// One queued blocking call: `run` executes on a libuv worker with the
+// context's mutex held; the Promise resolves with `out` bytes (or the root
+// handle) or rejects with the library's message.
+struct Work {
+  Ctx* holder = nullptr;
+  napi_ref keep = nullptr;  // keeps the context External alive while queued
+  napi_deferred deferred = nullptr;
+  napi_async_work work = nullptr;
+  int rc = BG_OK;
+  std::string err;
+  std::vector<uint8_t> out;
+  bool resident = false;
+  bg_handle root = 0;
+  // materialize
+  bg_handle h = 0;
+  // tensor plan
+  std::string plan, req;
+  bool semantic = false;
+  std::vector<int64_t> ids;
+  std::vector<bg_handle> hs;
+  int dtype = 0;
+};
+
+void work_execute(napi_env, void* data) {
+  auto* w = static_cast<Work*>(data);
+  std::lock_guard<std::mutex> lk(w->holder->mu);
+  bg_ctx* ctx = w->holder->ctx;
+  if (!ctx) {  // closed while the call was queued
+    w->rc = BG_E_INVALID;
+    w->err = "HIP bridge: context closed";
+    return;
+  }
+  if (!w->plan.empty()) {
+    void* dst = w->resident ? nullptr : static_cast<void*>(w->out.data());
+    w->rc = w->semantic ? bg_run_tensor_plan_semantic(ctx, w->plan.c_str(), w->req.c_str(), w->ids.data(),
+                                                      w->hs.data(), int(w->ids.size()), w->dtype, dst,
+                                                      w->out.size(), &w->root)
+                        : bg_run_tensor_plan(ctx, w->plan.c_str(), w->ids.data(), w->hs.data(),
+                                             int(w->ids.size()), w->dtype, dst, w->out.size(), &w->root);
+  } else {
+    w->rc = bg_materialize(ctx, w->h, w->out.data(), w->out.size());
+  }
+  if (w->rc != BG_OK) w->err = bg_last_error(ctx);
+}
+
+void work_complete(napi_env env, napi_status, void* data) {
+  auto* w = static_cast<Work*>(data);
+  if (w->rc == BG_OK) {
+    napi_value v = w->resident ? number(env, double(w->root)) : bytes(env, w->out.data(), w->out.size());
+    napi_resolve_deferred(env, w->deferred, v);
+  } else {
+    napi_value m, e, name;
+    napi_create_string_utf8(env, w->err.c_str(), w->err.size(), &m);
+    napi_create_error(env, nullptr, m, &e);
+    napi_create_string_utf8(env, "KernelError", NAPI_AUTO_LENGTH, &name);
+    napi_set_named_property(env, e, "name", name);
+    napi_reject_deferred(env, w->deferred, e);
+  }
+  napi_delete_reference(env, w->keep);
+  napi_delete_async_work(env, w->work);
+  delete w;
+}
+
+napi_value queue(napi_env env, napi_value ctx_value, Work* w, const char* name) {
+  napi_value promise, res_name;
+  napi_create_promise(env, &w->deferred, &promise);
+  napi_create_reference(env, ctx_value, 1, &w->keep);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &res_name);
+  napi_create_async_work(env, nullptr, res_name, work_execute, work_complete, w, &w->work);
+  napi_queue_async_work(env, w->work);
+  return promise;
+}
+
+napi_value MaterializeAsync(napi_env env, napi_callback_info info) {  // (ctx, h) -> Promise<Uint8Array>
+  Args a(env, info, 2);
+  bg_ctx* ctx = a.ctx();
+  bg_handle h = a.handle(1);
+  if (!a.ok) return nullptr;
+  int64_t shp[BG_MAX_RANK];
+  int rank = 0, dt = 0;
+  int64_t nb = 0;
+  if (!check(env, ctx, bg_handle_info(ctx, h, shp, &rank, &dt, &nb))) return nullptr;
+  auto* w = new Work();
+  w->holder = a.holder;
+  w->h = h;
+  w->out.resize(static_cast<size_t>(nb));
+  a.lock.unlock();  // the worker takes the mutex itself
+  return queue(env, a.v[0], w, "bghip.materialize");
+}
+
+// (ctx, planJson, requestsJson|null, ids[], handles[], dtype, resident, rootBytes) -> Promise
+napi_value RunTensorPlanAsync(napi_env env, napi_callback_info info) {
+  Args a(env, info, 8);
+  a.ctx();
+  auto* w = new Work();
+  w->plan = a.str(1);
+  w->semantic = !a.is_nullish(2);
+  if (w->semantic) w->req = a.str(2);
+  auto ids_d = a.nums(3);
+  auto hs_d = a.nums(4);
+  w->dtype = a.dtype(5);
+  napi_get_value_bool(env, a.v[6], &w->resident);
+  const int64_t nbytes = w->resident ? 0 : a.i64(7);
+  if (!a.ok || w->plan.empty() || nbytes < 0) {
+    if (a.ok) throw_kernel_error(env, "HIP bridge: runTensorPlanAsync: bad plan or root size");
+    delete w;
+    return nullptr;
+  }
+  w->holder = a.holder;
+  w->ids.assign(ids_d.begin(), ids_d.end());
+  w->hs.assign(hs_d.begin(), hs_d.end());
+  w->out.resize(size_t(nbytes));
+  a.lock.unlock();
+  return queue(env, a.v[0], w, "bghip.run_tensor_plan");
+}
+
 // ---- diagnostics (realizer.ts:275-298) ---------------------------------------
 
 napi_value AliveHandles(napi_env env, napi_callback_info info) {
@@ -446,6 +576,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"cast", Cast},                 {"flashAttention", FlashAttention},
       {"conv", Conv},
       {"runTensorPlan", RunTensorPlan}, {"aliveHandles", AliveHandles},
+      {"materializeAsync", MaterializeAsync}, {"runTensorPlanAsync", RunTensorPlanAsync},
       {"resourceSnapshot", ResourceSnapshot}, {"flushProfiles", FlushProfiles},
       {"version", Version},
   };

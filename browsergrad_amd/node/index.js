@@ -3,8 +3,10 @@
 // WebGpuRealizerBridge interface (packages/browsergrad-kernels/src/
 // realizer.ts:77-280), for Node hosts.  Method names, argument meaning and
 // return types are the reference's; device work runs through bghip.node
-// (N-API over libbghip.so).  Methods the reference declares async return
-// Promises resolved after the blocking native call.
+// (N-API over libbghip.so).  materialize and the tensor-plan runs return
+// Promises that settle when a libuv worker has finished the device call (the
+// event loop keeps running meanwhile); the other methods the reference
+// declares async return Promises resolved after the native call.
 //
 //   const { createHipRealizerBridge } = require('./browsergrad_amd/node');
 //   const bridge = createHipRealizerBridge({ device: 0 });
@@ -31,6 +33,13 @@ const OPCODES = { ADD: 0, MUL: 1, DIV: 2, NEG: 3, EXP: 4, LOG: 5 };
 function asBytes(data, name) {
   if (!(data instanceof Uint8Array)) throw new KernelError(`WebGPU bridge: ${name}.data must be Uint8Array bytes`);
   return data;
+}
+
+// Native errors named "KernelError" (and rejections of the async bindings)
+// become this module's KernelError class.
+function asKernelError(e) {
+  if (e && e.name === 'KernelError' && !(e instanceof KernelError)) return new KernelError(e.message);
+  return e;
 }
 
 function wrap(fn) {
@@ -94,14 +103,18 @@ function createHipRealizerBridge(options = {}) {
     return numel * width;
   }
 
-  function runPlan(plan, requests, inputs, dtype, resident) {
+  // The plan runs on a libuv worker (runTensorPlanAsync); inputs uploaded
+  // here are released once it settles.
+  async function runPlan(plan, requests, inputs, dtype, resident) {
     const obj = typeof plan === 'string' ? JSON.parse(plan) : plan;
     const text = typeof plan === 'string' ? plan : JSON.stringify(plan);
     const req = requests === null || requests === undefined ? null
       : (typeof requests === 'string' ? requests : JSON.stringify(requests));
     const { ids, handles, temps } = uploadPlanInputs(obj, inputs);
     try {
-      return wrap(() => n.runTensorPlan(ctx, text, req, ids, handles, dtype, resident, rootBytes(obj)));
+      return await n.runTensorPlanAsync(ctx, text, req, ids, handles, dtype, resident, rootBytes(obj));
+    } catch (e) {
+      throw asKernelError(e);
     } finally {
       for (const h of temps) n.release(ctx, h);
     }
@@ -109,7 +122,13 @@ function createHipRealizerBridge(options = {}) {
 
   const bridge = {
     upload: (data, shape, dtype) => wrap(() => n.upload(ctx, asBytes(data, 'upload'), shape, dtype)),
-    materialize: async (h, _shape, _dtype) => wrap(() => n.materialize(ctx, h)),
+    materialize: async (h, _shape, _dtype) => {
+      try {
+        return await n.materializeAsync(ctx, h);
+      } catch (e) {
+        throw asKernelError(e);
+      }
+    },
     release: (h) => wrap(() => n.release(ctx, h)),
     matmul: (a, b, m, k, nn, dtype) => wrap(() => n.matmul(ctx, a, b, m, k, nn, dtype)),
     fused_elementwise: (inputs, ops, shape, dtype) => wrap(() => {
@@ -127,7 +146,7 @@ function createHipRealizerBridge(options = {}) {
     run_tensor_plan_semantic: async (plan, requests, inputs, dtype) => runPlan(plan, requests, inputs, dtype, false),
     run_tensor_plan_resident: (plan, inputs, dtype) => runPlan(plan, null, inputs, dtype, true),
     run_tensor_plan_resident_semantic: async (plan, requests, inputs, dtype) => {
-      const h = runPlan(plan, requests, inputs, dtype, true);
+      const h = await runPlan(plan, requests, inputs, dtype, true);
       traces.set(h, { preparation: typeof requests === 'string' ? JSON.parse(requests) : requests });
       return h;
     },

@@ -102,6 +102,22 @@ async function main() {
   assert.throws(() => br.conv2d(), (e) => e.name === 'KernelError');
   assert.throws(() => br.run_user_kernel(), (e) => e.name === 'KernelError');
 
+  console.log('[node] read-backs settle from libuv workers');
+  const pending = br.materialize(c, [2, 2], 'float32');
+  assert.ok(pending instanceof Promise);
+  let ticked = false;
+  const tick = new Promise((resolve) => setImmediate(() => { ticked = true; resolve(); }));
+  const [m1, m2] = await Promise.all([pending, br.materialize(hf, [4], 'float32'), tick]);
+  assert.ok(ticked);
+  close(fromBytes(m1), [19, 22, 43, 50], 0, 'async materialize');
+  close(fromBytes(m2), xa.map((x, i) => Math.exp(x + xb[i]) / x), 1e-5, 'async materialize 2');
+  const gone = br.upload(f32([1, 2]), [2], 'float32');
+  br.release(gone);
+  await assert.rejects(br.materialize(gone, [2], 'float32'), (e) => e instanceof KernelError);
+  const planRuns = await Promise.all([0, 1, 2].map(() => br.run_tensor_plan_semantic(
+    plan, requests, [{ valueId: 0, data: f32(x) }], 'float32')));
+  for (const pr of planRuns) close(fromBytes(pr), want, 1e-6, 'concurrent plan runs');
+
   console.log('[node] residency bookkeeping');
   for (const h of [a, b, c, ha, hb, hf, q, k, v, o, h16, back, root]) br.release(h);
   br.release(a);  // idempotent

@@ -33,7 +33,7 @@ def test_addon_loads_and_exports():
     out = r.stdout.strip()
     for name in ("createHipRealizerBridge", "KernelError", "ctxCreate", "upload", "materialize", "matmul",
                  "fusedElementwise", "cast", "flashAttention", "conv", "runTensorPlan", "aliveHandles",
-                 "resourceSnapshot", "flushProfiles"):
+                 "resourceSnapshot", "flushProfiles", "materializeAsync", "runTensorPlanAsync"):
         assert name in out
     assert "bghip" in out
 

@@ -86,6 +86,14 @@ class MatmulExt(C.Structure):
     ]
 
 
+class LaunchRecord(C.Structure):
+    _fields_ = [
+        ("kernel", C.c_char * 160), ("grid", C.c_int64 * 3), ("block", C.c_int32 * 3),
+        ("dynamic_lds", C.c_int64), ("static_lds", C.c_int64), ("vgprs", C.c_int32), ("scratch", C.c_int32),
+        ("max_threads", C.c_int32), ("reserved", C.c_int32),
+    ]
+
+
 class AttentionDesc(C.Structure):
     _fields_ = [
         ("q", handle_t), ("k", handle_t), ("v", handle_t),
@@ -168,6 +176,8 @@ SIGNATURES = {
                                      C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_int, PH]),
     "bg_matmul_ex": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), PH]),
     "bg_plan_inspect": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "bg_set_launch_log": (C.c_int, [ctx_p, C.c_int]),
+    "bg_take_launch_log": (C.c_int, [ctx_p, C.POINTER(LaunchRecord), C.c_int, C.POINTER(C.c_int)]),
     "bg_matmul_ex2": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), C.POINTER(MatmulExt), PH]),
     "bg_matmul_noalloc": (C.c_int, [ctx_p, C.POINTER(MatmulDesc), C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p]),

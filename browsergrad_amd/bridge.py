@@ -650,6 +650,25 @@ class HipRealizerBridge:
 
     flush_profiles = flushProfiles
 
+    def set_launch_log(self, on: bool) -> None:
+        """Record every kernel launch of this context (bg_set_launch_log)."""
+        self._check(self._lib.bg_set_launch_log(self._ctx, 1 if on else 0))
+
+    def take_launch_log(self) -> list:
+        """The launches recorded since the last call, oldest first: kernel
+        symbol, grid, block, LDS bytes and the kernel's register / scratch
+        footprint (bg_take_launch_log)."""
+        n = C.c_int()
+        self._check(self._lib.bg_take_launch_log(self._ctx, None, 0, C.byref(n)))
+        arr = (N.LaunchRecord * max(1, n.value))()
+        got = C.c_int()
+        self._check(self._lib.bg_take_launch_log(self._ctx, arr, n.value, C.byref(got)))
+        return [{"kernel": arr[i].kernel.decode(errors="replace"), "grid": list(arr[i].grid),
+                 "block": list(arr[i].block), "dynamicLds": int(arr[i].dynamic_lds),
+                 "staticLds": int(arr[i].static_lds), "vgprs": int(arr[i].vgprs),
+                 "scratchBytesPerLane": int(arr[i].scratch), "maxThreads": int(arr[i].max_threads)}
+                for i in range(got.value)]
+
     def set_profiling(self, on: bool) -> None:
         """Switch per-dispatch profiling (the reference's creation option
         options.profiling, realizer.ts:899-914) on or off between calls."""

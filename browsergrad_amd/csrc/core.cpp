@@ -178,6 +178,29 @@ static void drop(bg_ctx* ctx, Record& r) {
   r.alloc = nullptr;
 }
 
+void log_launch(bg_ctx* ctx, const void* kernel, dim3 grid, dim3 block, size_t shmem) {
+  bg_launch_record r{};
+  const char* name = hipKernelNameRefByPtr(kernel, ctx->stream);
+  std::snprintf(r.kernel, sizeof(r.kernel), "%s", name ? name : "?");
+  r.grid[0] = grid.x;
+  r.grid[1] = grid.y;
+  r.grid[2] = grid.z;
+  r.block[0] = int32_t(block.x);
+  r.block[1] = int32_t(block.y);
+  r.block[2] = int32_t(block.z);
+  r.dynamic_lds = int64_t(shmem);
+  hipFuncAttributes fa{};
+  if (hipFuncGetAttributes(&fa, kernel) == hipSuccess) {
+    r.static_lds = int64_t(fa.sharedSizeBytes);
+    r.vgprs = int32_t(fa.numRegs);
+    r.scratch = int32_t(fa.localSizeBytes);
+    r.max_threads = int32_t(fa.maxThreadsPerBlock);
+  } else {
+    (void)hipGetLastError();
+  }
+  ctx->launch_log.push_back(r);
+}
+
 void* scratch(bg_ctx* ctx, size_t bytes, int slot) {
   if (bytes <= ctx->scratch_bytes[slot]) return ctx->scratch[slot];
   if (ctx->scratch[slot]) {
@@ -1104,6 +1127,27 @@ int bg_run_tensor_plan_semantic(bg_ctx* ctx, const char* plan_json, const char* 
   }
   return run_plan_abi(ctx, plan_json, requests_json, input_ids, input_handles, n_inputs, dtype, dst,
                       dst_nbytes, root_out);
+}
+
+int bg_set_launch_log(bg_ctx* ctx, int on) {
+  BG_API_BEGIN
+  ctx->log_launches = on != 0;
+  BG_API_END
+}
+
+int bg_take_launch_log(bg_ctx* ctx, bg_launch_record* out, int cap, int* n_out) {
+  BG_API_BEGIN
+  if (!n_out) fail(BG_E_INVALID, "take_launch_log: NULL count");
+  auto& log = ctx->launch_log;
+  if (!out) {
+    *n_out = int(log.size());
+  } else {
+    const size_t n = std::min(log.size(), size_t(cap < 0 ? 0 : cap));
+    std::copy(log.begin(), log.begin() + n, out);
+    log.erase(log.begin(), log.begin() + n);
+    *n_out = int(n);
+  }
+  BG_API_END
 }
 
 int bg_plan_inspect(const char* plan_json, const char* requests_json, char* out, size_t out_cap,

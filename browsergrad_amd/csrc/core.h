@@ -100,6 +100,10 @@ struct bg_ctx {
   char* noalloc_scratch = nullptr;
   size_t noalloc_scratch_bytes = 0;
   std::string noalloc_error;
+
+  // Launch log (bg_set_launch_log): one record per dispatch while on.
+  bool log_launches = false;
+  std::vector<bg_launch_record> launch_log;
 };
 
 namespace bg {
@@ -134,6 +138,9 @@ struct Profile {
 // profiling scope is open or the scope already dispatched a kernel).
 void next_dispatch_events(bg_ctx* ctx, hipEvent_t* start, hipEvent_t* stop);
 
+// Appends one bg_launch_record for a launch of `kernel` (core.cpp).
+void log_launch(bg_ctx* ctx, const void* kernel, dim3 grid, dim3 block, size_t shmem);
+
 // Launch `kernel` on the context stream with the profiling scope's events.
 template <typename... KArgs, typename... Args>
 void dispatch(bg_ctx* ctx, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
@@ -147,6 +154,7 @@ void dispatch(bg_ctx* ctx, void (*kernel)(KArgs...), dim3 grid, dim3 block, size
   }, vals);
   hipEvent_t start = nullptr, stop = nullptr;
   next_dispatch_events(ctx, &start, &stop);
+  if (ctx->log_launches) log_launch(ctx, reinterpret_cast<const void*>(kernel), grid, block, shmem);
   hip_check(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, shmem,
                                ctx->stream, start, stop, 0),
             "kernel launch");

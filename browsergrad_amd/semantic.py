@@ -25,16 +25,34 @@ attention-forward-model.ts): dense rank-4 f32 scaled-dot-product attention
 with an optional causal mask, online softmax, inputs and scaled scores
 required finite; it runs on the f32 flash-attention kernel.
 
-The reference also composes verified layout / tile / schedule artifacts
-(semantic-core) and reports their hashes in the trace; this module has no
-counterpart of that artifact machinery and reports the numerical contract,
-geometry and work counts only.
+Verified artifacts (the reference composes layout, logical-tile and
+schedule artifacts and reports their hashes in the trace,
+semantic_gemm.ts:122-154, 193-214): each run here records the kernels the
+library actually launched (bg_set_launch_log) and derives three artifacts
+from them and from the problem:
+
+* layout  -- every tensor's shape, element strides, dtype and byte length;
+  checked dense row-major and sized exactly;
+* logical tile -- the kernel's output tile (read from the launched kernel's
+  template arguments), the tile grid and the K decomposition; checked to
+  cover the output exactly once and the K range without gap;
+* schedule -- the launches (kernel symbol, grid, workgroup, LDS, registers,
+  scratch) and the workgroup-to-tile order; the GEMM's XCD-aware tile order
+  is restated on the host and checked to be a bijection onto the tile grid.
+
+Each artifact is canonical JSON (sorted keys, no spaces) hashed with
+SHA-256; the trace carries the three hashes, the input certificate's hash
+and a preparation hash over all of them.  An artifact whose check fails
+raises BG-WEBGPU-GEMM-VALIDATION (attention: -ATTENTION-VALIDATION) before
+any result is returned.
 """
 from __future__ import annotations
 
 import hashlib
 import itertools
-from typing import Any, Dict, Optional
+import json
+import re
+from typing import Any, Dict, List, Optional, Sequence
 
 import numpy as np
 
@@ -127,6 +145,136 @@ def certify_exact_f32_gemm_inputs(lhs: Any, rhs: Any, m: int, n: int, k: int) ->
     }
 
 
+# ---- verified artifacts --------------------------------------------------------
+
+def canonical_hash(obj: Any) -> str:
+    """SHA-256 of the canonical JSON of obj (sorted keys, no whitespace)."""
+    return hashlib.sha256(json.dumps(obj, sort_keys=True, separators=(",", ":")).encode()).hexdigest()
+
+
+def _artifact(kind: str, body: Dict[str, Any], checks: List[str]) -> Dict[str, Any]:
+    body = {"kind": kind, **body}
+    return {"body": body, "hash": canonical_hash(body), "checks": checks}
+
+
+def _fail(code: str, path: str, msg: str) -> None:
+    cls = SemanticAttentionError if "ATTENTION" in code else SemanticGemmError
+    raise cls(code, path, msg)
+
+
+def layout_artifact(tensors: Dict[str, Dict[str, Any]], code: str) -> Dict[str, Any]:
+    """Layout of dense row-major tensors {name: {shape, dtype}}; checked:
+    strides are the dense row-major ones and the byte length is exact."""
+    out = {}
+    for name, t in sorted(tensors.items()):
+        shape = [int(d) for d in t["shape"]]
+        item = np.dtype(t["dtype"]).itemsize
+        strides, acc = [], 1
+        for d in reversed(shape):
+            strides.insert(0, acc)
+            acc *= d
+        rec = {"shape": shape, "strides": strides, "dtype": t["dtype"], "byteLength": acc * item}
+        if rec["byteLength"] != int(np.prod(shape, dtype=np.int64)) * item or (strides and strides[-1] != 1):
+            _fail(code, f"$.layout.{name}", "layout is not dense row-major")
+        out[name] = rec
+    return _artifact("layout", {"tensors": out}, ["dense-row-major", "exact-byte-length"])
+
+
+def gemm_tile_order(pid: int, tiles_m: int, tiles_n: int) -> tuple:
+    """Host restatement of the GEMM kernels' workgroup -> tile map
+    (k_gemm.hip tile_coords): workgroups go round-robin over the 8 XCDs, so
+    the tiles of one XCD are made consecutive, then walked in groups of 4
+    tile rows."""
+    total = tiles_m * tiles_n
+    if total % 8 == 0:
+        per = total // 8
+        pid = (pid % 8) * per + pid // 8
+    g = 4
+    group = pid // (g * tiles_n)
+    first_m = group * g
+    gsz = min(g, tiles_m - first_m)
+    in_group = pid % (g * tiles_n)
+    return first_m + in_group % gsz, in_group // gsz
+
+
+_GEMM_KERNEL = re.compile(r"(gemm32_kernel|gemm16_lds_kernel|gemm16_kernel)ILi(\d+)ELi(\d+)E")
+
+
+def gemm_artifacts(launches: Sequence[Dict[str, Any]], m: int, n: int, k: int) -> Dict[str, Dict[str, Any]]:
+    """Logical-tile and schedule artifacts of one GEMM from its launch log."""
+    code = "BG-WEBGPU-GEMM-VALIDATION"
+    mains = [(r, _GEMM_KERNEL.search(r["kernel"])) for r in launches]
+    mains = [(r, mt) for r, mt in mains if mt]
+    if len(mains) != 1:
+        _fail(code, "$.schedule", f"expected one GEMM kernel launch, saw {[r['kernel'] for r in launches]}")
+    rec, mt = mains[0]
+    bm, bn = int(mt.group(2)), int(mt.group(3))
+    tiles_m, tiles_n = -(-m // bm), -(-n // bn)
+    grid = rec["grid"]
+    k_slices = int(grid[1])
+    if grid[0] != tiles_m * tiles_n:
+        _fail(code, "$.tile", f"grid.x {grid[0]} != {tiles_m} x {tiles_n} tiles of {bm}x{bn}")
+    if not (tiles_m * bm >= m > (tiles_m - 1) * bm and tiles_n * bn >= n > (tiles_n - 1) * bn):
+        _fail(code, "$.tile", "tile grid does not cover the output exactly once")
+    seen = {gemm_tile_order(p, tiles_m, tiles_n) for p in range(tiles_m * tiles_n)}
+    if len(seen) != tiles_m * tiles_n or not all(0 <= a < tiles_m and 0 <= b < tiles_n for a, b in seen):
+        _fail(code, "$.schedule.tileOrder", "workgroup -> tile order is not a bijection onto the tile grid")
+    tile = _artifact("logical-gemm-tile", {
+        "m": m, "n": n, "k": k, "tile": {"m": bm, "n": bn}, "tilesM": tiles_m, "tilesN": tiles_n,
+        "kSlices": k_slices,
+        "accumulation": "f32; ascending k inside a slice; slices summed in slice order by a finishing pass"
+                        if k_slices > 1 else "f32; ascending k",
+    }, ["tiles-cover-output-once"])
+    sched = _artifact("schedule", {
+        "launches": [{kk: r[kk] for kk in ("kernel", "grid", "block", "dynamicLds", "staticLds", "vgprs",
+                                          "scratchBytesPerLane")} for r in launches],
+        "tileOrder": "xcd-round-robin-consecutive, groups of 4 tile rows",
+    }, ["tile-order-bijection"])
+    return {"tile": tile, "schedule": sched}
+
+
+def attention_artifacts(launches: Sequence[Dict[str, Any]], rows: int) -> Dict[str, Dict[str, Any]]:
+    """Logical-tile and schedule artifacts of the f32 attention kernel: one
+    wavefront per query row, keys streamed in order."""
+    code = "BG-WEBGPU-ATTENTION-VALIDATION"
+    mains = [r for r in launches if "attention" in r["kernel"]]
+    if len(mains) != 1:
+        _fail(code, "$.schedule", f"expected one attention kernel launch, saw {[r['kernel'] for r in launches]}")
+    r = mains[0]
+    waves = int(r["block"][0]) // 64
+    cover = int(r["grid"][0]) * waves
+    if not (cover >= rows > cover - waves):
+        _fail(code, "$.tile", f"{r['grid'][0]} workgroups x {waves} wavefronts do not cover {rows} query rows once")
+    tile = _artifact("logical-attention-tile", {"queryRowsPerWavefront": 1, "wavefrontsPerWorkgroup": waves,
+                                                "rows": rows, "keyOrder": "ascending, online softmax"},
+                     ["rows-covered-once"])
+    sched = _artifact("schedule", {
+        "launches": [{kk: x[kk] for kk in ("kernel", "grid", "block", "dynamicLds", "staticLds", "vgprs",
+                                          "scratchBytesPerLane")} for x in launches]}, ["one-launch"])
+    return {"tile": tile, "schedule": sched}
+
+
+def _trace_hashes(profile: str, layout: Dict[str, Any], arts: Dict[str, Dict[str, Any]],
+                  certificate: Optional[Dict[str, Any]]) -> Dict[str, Any]:
+    cert_hash = canonical_hash(certificate) if certificate is not None else None
+    hashes = {"layoutSemanticHash": layout["hash"], "kernelSemanticHash": arts["tile"]["hash"],
+              "scheduleSemanticHash": arts["schedule"]["hash"], "inputCertificateSemanticHash": cert_hash}
+    hashes["backendPreparationHash"] = canonical_hash({"profile": profile, "version": BACKEND_VERSION, **hashes})
+    hashes["artifacts"] = {"layout": layout, **arts}
+    return hashes
+
+
+def _run_logged(bridge: Any, fn):
+    """Run fn() with the bridge's launch log on; returns (result, launches)."""
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()  # drop anything older
+        res = fn()
+        return res, bridge.take_launch_log()
+    finally:
+        bridge.set_launch_log(False)
+
+
 def _device_facts(bridge: Any) -> Dict[str, Any]:
     return {"backend": "hip", "architecture": "gfx950", "library": getattr(bridge, "version", lambda: "")()}
 
@@ -144,6 +292,7 @@ def run_semantic_gemm_exact_f32(bridge: Any, certificate: Dict[str, Any], lhs: A
         if _digest(arr) != certificate["inputs"][name]["digest"]:
             raise SemanticGemmError("BG-WEBGPU-GEMM-INVALID-BINDING", f"$.inputs.{name}",
                                     "input bytes do not match the certificate's commitment")
+    launches: List[Dict[str, Any]] = []
     if m == 0 or n == 0:
         out = np.zeros((m, n), np.float32)
     else:
@@ -153,7 +302,8 @@ def run_semantic_gemm_exact_f32(bridge: Any, certificate: Dict[str, Any], lhs: A
             if k == 0:
                 out = np.zeros((m, n), np.float32)
             else:
-                hc = bridge.matmul_ex(ha, hb, m=m, n=n, k=k, in_dtype="float32", out_dtype="float32")
+                hc, launches = _run_logged(
+                    bridge, lambda: bridge.matmul_ex(ha, hb, m=m, n=n, k=k, in_dtype="float32", out_dtype="float32"))
                 try:
                     out = bridge.to_numpy(hc)
                 finally:
@@ -184,6 +334,11 @@ def run_semantic_gemm_exact_f32(bridge: Any, certificate: Dict[str, Any], lhs: A
         "submitted": True,
         "device": _device_facts(bridge),
     }
+    if launches:
+        layout = layout_artifact({"lhs": {"shape": [m, k], "dtype": "float32"},
+                                  "rhs": {"shape": [k, n], "dtype": "float32"},
+                                  "output": {"shape": [m, n], "dtype": "float32"}}, "BG-WEBGPU-GEMM-VALIDATION")
+        trace.update(_trace_hashes(GEMM_PROFILE, layout, gemm_artifacts(launches, m, n, k), certificate))
     return {"destination": np.ascontiguousarray(out, np.float32).tobytes(), "trace": trace}
 
 
@@ -214,8 +369,9 @@ def run_semantic_attention_f32(bridge: Any, query: Any, key: Any, value: Any, *,
                                      "causal attention needs q_len <= k_len")
     hs = [bridge.upload(t, t.shape, "float32") for t in (q, k, v)]
     try:
-        ho = bridge.attention_ex(hs[0], hs[1], hs[2], batch=batch, heads=heads, sq=q_len, sk=k_len, d=head_dim,
-                                 scale=sc, causal=causal, in_dtype="float32", out_dtype="float32")
+        ho, launches = _run_logged(bridge, lambda: bridge.attention_ex(
+            hs[0], hs[1], hs[2], batch=batch, heads=heads, sq=q_len, sk=k_len, d=head_dim, scale=sc,
+            causal=causal, in_dtype="float32", out_dtype="float32"))
         try:
             out = bridge.to_numpy(ho)
         finally:
@@ -239,8 +395,16 @@ def run_semantic_attention_f32(bridge: Any, query: Any, key: Any, value: Any, *,
         "submitted": True,
         "device": _device_facts(bridge),
     }
+    shp = lambda s_: [batch, heads, s_, head_dim]  # noqa: E731
+    layout = layout_artifact({"query": {"shape": shp(q_len), "dtype": "float32"},
+                              "key": {"shape": shp(k_len), "dtype": "float32"},
+                              "value": {"shape": shp(k_len), "dtype": "float32"},
+                              "output": {"shape": shp(q_len), "dtype": "float32"}}, "BG-WEBGPU-ATTENTION-VALIDATION")
+    trace.update(_trace_hashes(ATTENTION_PROFILE, layout, attention_artifacts(launches, batch * heads * q_len),
+                               None))
     return {"destination": out.astype(np.float32).tobytes(), "trace": trace}
 
 
 __all__ = ["certify_exact_f32_gemm_inputs", "run_semantic_gemm_exact_f32", "run_semantic_attention_f32",
-           "SemanticGemmError", "SemanticAttentionError", "EXACT_F32_INPUT_PROFILE", "EXACT_F32_INTEGER_LIMIT"]
+           "SemanticGemmError", "SemanticAttentionError", "EXACT_F32_INPUT_PROFILE", "EXACT_F32_INTEGER_LIMIT",
+           "canonical_hash", "layout_artifact", "gemm_artifacts", "attention_artifacts", "gemm_tile_order"]

@@ -246,6 +246,24 @@ typedef struct bg_pass_profile {
   int64_t flops;   /* algorithmic flops of the dispatch */
 } bg_pass_profile;
 
+/* One kernel launch as the library issued it (extension; the launch log of
+ * bg_set_launch_log).  kernel: the kernel symbol (mangled, truncated to
+ * 159 bytes); grid / block: launch geometry; dynamic_lds: dynamic LDS bytes
+ * of the launch; static_lds, vgprs (architected VGPRs per lane), scratch
+ * (private bytes per lane) and max_threads: the kernel's compiled
+ * attributes (hipFuncGetAttributes). */
+typedef struct bg_launch_record {
+  char kernel[160];
+  int64_t grid[3];
+  int32_t block[3];
+  int64_t dynamic_lds;
+  int64_t static_lds;
+  int32_t vgprs;
+  int32_t scratch;
+  int32_t max_threads;
+  int32_t reserved;
+} bg_launch_record;
+
 /* ---- context (createWebGpuRealizerBridge, realizer.ts:898-1005) ------- */
 int bg_ctx_create(int device, int profiling, bg_ctx** out);
 int bg_ctx_destroy(bg_ctx* ctx);
@@ -278,6 +296,15 @@ int bg_flush_profiles(bg_ctx* ctx, bg_pass_profile* out, int cap, int* n_out);
  * reference fixes it at creation (options.profiling, realizer.ts:899, 914);
  * profiles already recorded stay pending until bg_flush_profiles. */
 int bg_set_profiling(bg_ctx* ctx, int on);
+/* extension: record every kernel the library launches on this context
+ * (on != 0) until switched off; bg_take_launch_log copies up to cap records
+ * (oldest first) into out, sets *n_out to the number copied (or, with out
+ * NULL, to the number pending) and clears what it copied.  Kernels compiled
+ * at run time (fused programs) are launched as code objects and are not
+ * recorded.  Used by the certified-numerics entry points to describe the
+ * schedule that actually ran. */
+int bg_set_launch_log(bg_ctx* ctx, int on);
+int bg_take_launch_log(bg_ctx* ctx, bg_launch_record* out, int cap, int* n_out);
 
 /* ---- compute ------------------------------------------------------------ */
 /* matmul: realizer.ts:1043-1060.  A[M,K] @ B[K,N] row-major; dtype is

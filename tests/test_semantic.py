@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 
 from browsergrad_amd.semantic import (
+    canonical_hash, gemm_artifacts, gemm_tile_order,
     EXACT_F32_INTEGER_LIMIT, SemanticAttentionError, SemanticGemmError, certify_exact_f32_gemm_inputs,
     run_semantic_attention_f32, run_semantic_gemm_exact_f32,
 )
@@ -61,6 +62,17 @@ def test_exact_gemm_is_bit_exact(bridge, m, n, k, hi):
     assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(F32))
     t = res["trace"]
     assert t["multiplyAdds"] == m * n * k and t["numericalPreservation"] == "bit-exact-on-certified-inputs"
+    # verified artifacts from the launches that ran, with their hashes
+    arts = t["artifacts"]
+    assert arts["layout"]["body"]["tensors"]["lhs"]["strides"] == [k, 1]
+    assert arts["schedule"]["body"]["launches"][0]["kernel"].find("gemm32") >= 0
+    for name, key in (("layout", "layoutSemanticHash"), ("tile", "kernelSemanticHash"),
+                      ("schedule", "scheduleSemanticHash")):
+        assert t[key] == arts[name]["hash"] == canonical_hash(arts[name]["body"])
+    assert len(t["backendPreparationHash"]) == 64 and t["inputCertificateSemanticHash"]
+    # the same problem prepares the same artifacts
+    again = run_semantic_gemm_exact_f32(bridge, certify_exact_f32_gemm_inputs(a, b, m, n, k), a, b)["trace"]
+    assert again["backendPreparationHash"] == t["backendPreparationHash"]
 
 
 @pytest.mark.gpu
@@ -95,7 +107,51 @@ def test_semantic_attention_f32(bridge, causal):
     ref = O.attention_f64(q, k, v, 1.0 / np.sqrt(d), causal=causal)
     assert O.within(got, ref, 1e-4).all(), O.report(got, ref, 1e-4)
     assert res["trace"]["mask"] == ("causal" if causal else "none")
+    t = res["trace"]
+    assert t["kernelSemanticHash"] == t["artifacts"]["tile"]["hash"]
+    assert t["artifacts"]["tile"]["body"]["rows"] == b * h * sq
     bad = q.copy()
     bad[0, 0, 0, 0] = np.inf
     with pytest.raises(SemanticAttentionError, match="finite"):
         run_semantic_attention_f32(bridge, bad, k, v, batch=b, heads=h, q_len=sq, k_len=sk, head_dim=d)
+
+
+def test_gemm_tile_order_is_a_bijection():
+    """The host restatement of the kernels' workgroup -> tile map covers every
+    tile exactly once for every grid shape up to 48 x 48 tiles (both the
+    XCD-remapped case, tile count % 8 == 0, and the plain one)."""
+    for tm in range(1, 49):
+        for tn in range(1, 49):
+            seen = {gemm_tile_order(p, tm, tn) for p in range(tm * tn)}
+            assert len(seen) == tm * tn and all(0 <= a < tm and 0 <= b < tn for a, b in seen), (tm, tn)
+
+
+def _rec(kernel, grid):
+    return {"kernel": kernel, "grid": grid, "block": [256, 1, 1], "dynamicLds": 0, "staticLds": 32768,
+            "vgprs": 128, "scratchBytesPerLane": 0}
+
+
+def test_gemm_artifacts_from_a_launch_log():
+    log = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEv8GemmArgs", [6, 1, 1])]
+    arts = gemm_artifacts(log, 300, 200, 64)
+    tile = arts["tile"]["body"]
+    assert (tile["tile"], tile["tilesM"], tile["tilesN"], tile["kSlices"]) == ({"m": 128, "n": 128}, 3, 2, 1)
+    assert arts["tile"]["hash"] == canonical_hash(tile)
+    # split K: partial GEMM over 4 slices and the finishing pass
+    log2 = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb1ELb1EEEv8GemmArgs", [1, 4, 1]),
+            _rec("_ZN12_GLOBAL__N_120gemm32_splitk_reduceILi0EEEv8GemmArgsi", [32, 1, 1])]
+    t2 = gemm_artifacts(log2, 64, 128, 784)["tile"]["body"]
+    assert t2["kSlices"] == 4 and "slice order" in t2["accumulation"]
+
+
+@pytest.mark.parametrize("grid,m,n,msg", [
+    ([5, 1, 1], 300, 200, "grid.x"),            # one tile short
+    ([6, 1, 1], 300, 300, "grid.x"),            # wrong tile count for the shape
+])
+def test_gemm_artifacts_refuse_a_schedule_that_does_not_cover(grid, m, n, msg):
+    log = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEv8GemmArgs", grid)]
+    with pytest.raises(SemanticGemmError, match=msg) as e:
+        gemm_artifacts(log, m, n, 64)
+    assert e.value.code == "BG-WEBGPU-GEMM-VALIDATION"
+    with pytest.raises(SemanticGemmError, match="one GEMM kernel launch"):
+        gemm_artifacts([], m, n, 64)

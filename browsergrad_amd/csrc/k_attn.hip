@@ -1050,13 +1050,23 @@ __device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0
   }
 }
 
-template <bool BF16, bool CAUSAL>
-// Four wavefronts per SIMD (two workgroups per CU), as v6 runs: <= 128 VGPRs.
-__global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
-  __shared__ fa_u4 smem[2 * kFa6Ring * kFa2Tile / 16];
+// NW wavefronts x 32 queries per workgroup, a RING-slot LDS ring of 64-key
+// K and V tiles.  <8, 4>: two workgroups per CU, four wavefronts per SIMD
+// (the long-sequence shape).  <4, 3>: 128-query workgroups, three per CU
+// (48 KB of LDS each), for grids too small to fill the CUs evenly with
+// 256-query blocks (a causal S = 1024 head has 4 such blocks of 4, 8, 12 and
+// 16 tiles; 8 blocks of 128 queries fill three workgroup slots per CU).
+template <bool BF16, bool CAUSAL, int NW, int RING>
+__global__ void __launch_bounds__(NW * 64, NW == 8 ? 4 : 3)  // the LDS-bound occupancy
+fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
+  static_assert((NW == 8 && RING == 4) || (NW == 4 && RING == 3), "instantiated shapes");
+  constexpr int BQ = NW * kFa2QW;       // queries per workgroup
+  constexpr int PARTS = 8 / NW;         // 1 KB slices of each tile per wavefront
+  constexpr int DMA = 2 * PARTS;        // copies per wavefront per tile (K and V)
+  __shared__ fa_u4 smem[2 * RING * kFa2Tile / 16];
   char* sb = reinterpret_cast<char*>(smem);
   char* kring = sb;
-  char* vring = sb + kFa6Ring * kFa2Tile;
+  char* vring = sb + RING * kFa2Tile;
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1064,7 +1074,7 @@ __global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint
   const int bh = blockIdx.x;
   const int qblk = P.n_qblocks - 1 - int(blockIdx.y);  // heavy query blocks first
   const int b = bh / P.H, h = bh % P.H;
-  const int q0 = qblk * kFa2BQ;
+  const int q0 = qblk * BQ;
   const int q0w = q0 + w * kFa2QW;
   const int qi = q0w + (lane & 31);
 
@@ -1075,25 +1085,37 @@ __global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint
   const bgk::sgpr4_t rv = bgk::buffer_rsrc(Vp, v_bytes);
 
   const int nt_all = (P.Sk + kFa2BK - 1) / kFa2BK;
-  const int nt = CAUSAL ? min(nt_all, (q0 + kFa2BQ + kFa2BK - 1) / kFa2BK) : nt_all;
+  const int nt = CAUSAL ? min(nt_all, (q0 + BQ + kFa2BK - 1) / kFa2BK) : nt_all;
   const int ntw = CAUSAL ? min(nt, (q0w + kFa2QW + kFa2BK - 1) / kFa2BK) : nt;
   // Tiles with no masked key for any query of the workgroup.
   const int t_clean = min(nt, CAUSAL ? min(P.Sk / kFa2BK, (q0 + 1) / kFa2BK) : P.Sk / kFa2BK);
 
-  const int u = w * 64 + lane;
-  const int krow = u >> 3, pc = u & 7;
-  const uint32_t koff = uint32_t((int64_t(krow) * P.k_ss + ((pc ^ ((krow >> 1) & 7)) * 8)) * 2);
-  const uint32_t voff = uint32_t((int64_t(krow) * P.v_ss + ((pc ^ ((krow & 3) << 1)) * 8)) * 2);
+  // Wavefront w copies the 1 KB slices w, w + NW, ... (rows 8 s .. 8 s + 7)
+  // of each K and V tile; lane L writes 16-byte unit 64 s + L = (row, chunk).
+  uint32_t koff[PARTS], voff[PARTS];
+  int krow[PARTS];
+#pragma unroll
+  for (int p = 0; p < PARTS; ++p) {
+    const int u = (w + p * NW) * 64 + lane;
+    const int pc = u & 7;
+    krow[p] = u >> 3;
+    koff[p] = uint32_t((int64_t(krow[p]) * P.k_ss + ((pc ^ ((krow[p] >> 1) & 7)) * 8)) * 2);
+    voff[p] = uint32_t((int64_t(krow[p]) * P.v_ss + ((pc ^ ((krow[p] & 3) << 1)) * 8)) * 2);
+  }
   const uint32_t kstep = uint32_t(int64_t(kFa2BK) * P.k_ss * 2);
   const uint32_t vstep = uint32_t(int64_t(kFa2BK) * P.v_ss * 2);
   const uint32_t kl = bgk::lds_addr(kring) + uint32_t(w) * 1024u;
   const uint32_t vl = bgk::lds_addr(vring) + uint32_t(w) * 1024u;
   auto issue = [&](int j) {
     const bool real = j >= 0 && j < nt;
-    const bool ok = real && j * kFa2BK + krow < P.Sk;
-    const uint32_t sl = uint32_t(j & 3) * kFa2Tile;
-    bgk::dma16_to_lds(kl + sl, ok ? koff : kFa2Oob, rk, real ? uint32_t(j) * kstep : 0u);
-    bgk::dma16_to_lds(vl + sl, ok ? voff : kFa2Oob, rv, real ? uint32_t(j) * vstep : 0u);
+    const uint32_t sl = uint32_t(j % RING) * kFa2Tile;
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p) {
+      const bool ok = real && j * kFa2BK + krow[p] < P.Sk;
+      const uint32_t at = sl + uint32_t(p * NW) * 1024u;
+      bgk::dma16_to_lds(kl + at, ok ? koff[p] : kFa2Oob, rk, real ? uint32_t(j) * kstep : 0u);
+      bgk::dma16_to_lds(vl + at, ok ? voff[p] : kFa2Oob, rv, real ? uint32_t(j) * vstep : 0u);
+    }
   };
 
   const float sl2 = P.sl2;
@@ -1102,9 +1124,8 @@ __global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint
   for (int dc = 0; dc < 4; ++dc)
     qf[dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
                        : fa_u4{0u, 0u, 0u, 0u};
-  issue(0);
-  issue(1);
-  issue(2);
+#pragma unroll
+  for (int j = 0; j < RING - 1; ++j) issue(j);
   fa2_wait_vm_lgkm0<0>();  // also retires the Q loads in the compiler's bookkeeping
   __builtin_amdgcn_s_barrier();
 #pragma unroll
@@ -1143,12 +1164,12 @@ __global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint
   int t = 0;
   for (; t < t_clean; ++t) {
     if (t > 0) {
-      fa2_wait_vm_lgkm0<4>();
+      fa2_wait_vm_lgkm0<(RING - 2) * DMA>();  // tile t landed; t+1 .. t+RING-2 may be in flight
       __builtin_amdgcn_s_barrier();
     }
-    issue(t + 3);
-    const char* kt = kring + (t & 3) * kFa2Tile;
-    const char* vt = vring + (t & 3) * kFa2Tile;
+    issue(t + RING - 1);  // into the slot of tile t-1, which every wavefront has left
+    const char* kt = kring + (t % RING) * kFa2Tile;
+    const char* vt = vring + (t % RING) * kFa2Tile;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const float16v x = fa6_scores_half<BF16>(kt, offs, qf, mneg, hh);
@@ -1159,16 +1180,20 @@ __global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint
   }
   for (; t < nt; ++t) {
     if (t > 0) {
-      fa2_wait_vm_lgkm0<4>();
+      fa2_wait_vm_lgkm0<(RING - 2) * DMA>();
       __builtin_amdgcn_s_barrier();
     }
-    issue(t + 3);
+    issue(t + RING - 1);
+    const char* kt = kring + (t % RING) * kFa2Tile;
+    const char* vt = vring + (t % RING) * kFa2Tile;
     if (t < ntw) {
-      const char* kt = kring + (t & 3) * kFa2Tile;
-      const char* vt = vring + (t & 3) * kFa2Tile;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
+        // j0 and q0w are multiples of 32: a half with j0 > q0w lies after
+        // every query of the wavefront and adds nothing; j0 == q0w is the
+        // diagonal half, j0 < q0w a fully visible one.
         const int j0 = t * kFa2BK + hh * 32;
+        if (CAUSAL && j0 > q0w) break;
         float16v x = fa6_scores_half<BF16>(kt, offs, qf, mneg, hh);
         if ((CAUSAL && j0 + 31 > q0w) || (j0 + 32 > P.Sk)) {
 #pragma unroll
@@ -1198,10 +1223,22 @@ __global__ void __launch_bounds__(kFa2NW * 64, 4) fa7_fwd_kernel(Fa2Args P, uint
   fa7_store(P, b, h, qi, acc, l_run);
 }
 
+// 256-query workgroups when they give at least three per CU's two slots
+// (C4: 128 heads x 8 blocks); 128-query workgroups otherwise (C5: 96 heads
+// x 4 blocks of 256 would leave a 2:1 imbalance between CUs).
 template <bool BF16, bool CAUSAL>
-void launch_fa7(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uint32_t vb) {
-  bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL>, dim3(unsigned(bh), unsigned(nqb), 1),
-               dim3(kFa2NW * 64), 0, A, kb, vb);
+void launch_fa7(bg_ctx* ctx, const Fa2Args& A0, int bh, uint32_t kb, uint32_t vb) {
+  Fa2Args A = A0;
+  const int64_t big = int64_t(bh) * ((A.Sq + 255) / 256);
+  if (big >= 768 || (A.Sq + 127) / 128 > 65535) {
+    A.n_qblocks = (A.Sq + 255) / 256;
+    bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 8, 4>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
+                 dim3(8 * 64), 0, A, kb, vb);
+  } else {
+    A.n_qblocks = (A.Sq + 127) / 128;
+    bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 4, 3>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
+                 dim3(4 * 64), 0, A, kb, vb);
+  }
 }
 
 template <bool BF16, bool CAUSAL>
@@ -1298,7 +1335,7 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     const bool fast = ver != 2 && !r && (bf || A.sl2 <= 1.0f);
 #define BG_FA2(B_, C_, R_)                                                                     \
   (fast && !R_ ? (ver == 6 ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb)               \
-                           : launch_fa7<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb))              \
+                           : launch_fa7<B_, C_>(ctx, A, bh, kb, vb))                         \
                : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
     if (bf) {
       if (c) { if (r) BG_FA2(true, true, true); else BG_FA2(true, true, false); }

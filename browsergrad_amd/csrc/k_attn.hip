@@ -31,6 +31,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "common.cuh"
@@ -1230,7 +1231,11 @@ template <bool BF16, bool CAUSAL>
 void launch_fa7(bg_ctx* ctx, const Fa2Args& A0, int bh, uint32_t kb, uint32_t vb) {
   Fa2Args A = A0;
   const int64_t big = int64_t(bh) * ((A.Sq + 255) / 256);
-  if (big >= 768 || (A.Sq + 127) / 128 > 65535) {
+  // Diagnostic override for tests and sweeps: BG_FA7_BLOCK=256 or 128.
+  const char* force = std::getenv("BG_FA7_BLOCK");
+  const bool want256 = force && std::strcmp(force, "256") == 0;
+  const bool want128 = force && std::strcmp(force, "128") == 0;
+  if (want256 || (!want128 && big >= 768) || (A.Sq + 127) / 128 > 65535) {
     A.n_qblocks = (A.Sq + 255) / 256;
     bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 8, 4>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
                  dim3(8 * 64), 0, A, kb, vb);

@@ -804,7 +804,8 @@ bool aligned_to(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p)
 // ahead, so short stages (small tiles or BK = 32) need more of them to cover
 // HBM latency.
 enum class LdsCfg { T256x256x64s2, T256x256x32s4, T256x128x64s3, T128x256x64s3, T128x128x64s4, T128x128x32s4,
-                    T128x128x64s2, T256x256x64s2w8, T256x256x32s4w8, T256x128x64s3w8 };
+                    T128x128x64s2, T256x256x64s2w8, T256x256x32s4w8, T256x128x64s3w8, T128x192x64s3w8,
+                    T128x192x64s2w8 };
 
 template <int BM_, int BN_, int BK_, int S_, int WGM_ = 2, int WGN_ = 2>
 struct CfgTag {
@@ -825,6 +826,8 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch, int act) {
     if (v == "256x256x64s2w8") return LdsCfg::T256x256x64s2w8;
     if (v == "256x256x32s4w8") return LdsCfg::T256x256x32s4w8;
     if (v == "256x128x64s3w8") return LdsCfg::T256x128x64s3w8;
+    if (v == "128x192x64s3w8") return LdsCfg::T128x192x64s3w8;
+    if (v == "128x192x64s2w8") return LdsCfg::T128x192x64s2w8;
   }
   // Measured on MI355X (kernel time, configurations interleaved round-robin
   // so that all share one thermal state; f16 out, + bias):
@@ -837,13 +840,23 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch, int act) {
   //   8192x768x3072:   256x128x64/3, 8 wavefronts         43.7 us (128x128: 46.1)
   //   8192x3072x768 + GELU: 128x128x64/2                  57.3 us
   //                    (256x128 w8 58.7; 256x256 w8 61.2)
-  // 1+ waves of 256x256 tiles take them with two wavefronts per SIMD (deep
-  // K) or 1.25+ waves (shallow K); narrow outputs (N <= 1024) take 256x128;
-  // the rest 128x128, two workgroups per CU.  With tanh-GELU in the epilogue
-  // 128x128 tiles keep the lead: their 8192x3072 grid is 6 waves of tiles,
-  // 256x256's 1.5 waves expose the epilogue.
+  // 128x192 tiles, 8 wavefronts as a 4 x 2 grid of 32x96 blocks (kernel
+  // trace medians, round-robin launches, f16 out + bias; residual for N=768):
+  //   8192x2304x768:         two stages (two per CU)  34.9 us (128x128: 42.8)
+  //   8192x3072x768 + GELU:  two stages               51.7 us (128x128: 57.6)
+  //   8192x768x3072 + res:   three stages (one per CU) 45.6 us (256x128 w8: 51.5)
+  //   8192x768x768 + res:    three stages             19.1 us (256x128 w8: 20.6)
+  // GPT-2's widths (768, 2304, 3072) are multiples of 192.
+  // 1+ waves of 256x256 tiles with a deep K take them with two wavefronts
+  // per SIMD; outputs whose width is a multiple of 192 take 128x192 (two
+  // stages when there are two tiles per CU slot pair, else three); else
+  // 1.25+ waves of 256x256 tiles (shallow K); narrow outputs (N <= 1024)
+  // take 256x128; the rest 128x128, two workgroups per CU.  With tanh-GELU
+  // in the epilogue 256x256 tiles lose: their 1.5 waves expose the epilogue.
   const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
   if (t256 >= 256 && k >= 2048 && act != BG_ACT_GELU_TANH) return LdsCfg::T256x256x64s2w8;
+  const int64_t t192 = ((m + 127) / 128) * (n / 192) * batch;
+  if (n % 192 == 0 && t192 >= 256) return t192 >= 512 ? LdsCfg::T128x192x64s2w8 : LdsCfg::T128x192x64s3w8;
   if (t256 >= 320 && act != BG_ACT_GELU_TANH) return LdsCfg::T256x256x64s2w8;
   const int64_t t256x128 = ((m + 255) / 256) * ((n + 127) / 128) * batch;
   if (n <= 1024 && t256x128 >= 128) return LdsCfg::T256x128x64s3w8;
@@ -990,6 +1003,8 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const 
       case LdsCfg::T256x256x64s2w8: go(CfgTag<256, 256, 64, 2, 2, 4>{}); break;
       case LdsCfg::T256x256x32s4w8: go(CfgTag<256, 256, 32, 4, 2, 4>{}); break;
       case LdsCfg::T256x128x64s3w8: go(CfgTag<256, 128, 64, 3, 4, 2>{}); break;
+      case LdsCfg::T128x192x64s3w8: go(CfgTag<128, 192, 64, 3, 4, 2>{}); break;
+      case LdsCfg::T128x192x64s2w8: go(CfgTag<128, 192, 64, 2, 4, 2>{}); break;
       default: go(CfgTag<128, 128, 64, 2>{}); break;
     }
     return;

@@ -18,6 +18,16 @@ TOL32 = 1e-4
 TOL16 = 2e-2
 
 
+@pytest.fixture(params=["auto", "256"])
+def fa7_block(request, monkeypatch):
+    """The attention kernel picks 256-query workgroups for grids of at least
+    768 such blocks and 128-query ones below; the small test shapes land on
+    the second, so each attention test also runs with the first forced."""
+    if request.param != "auto":
+        monkeypatch.setenv("BG_FA7_BLOCK", request.param)
+    return request.param
+
+
 def up(br, a, dtype=None):
     a = np.ascontiguousarray(a)
     return br.upload(a, a.shape, dtype or a.dtype.name)
@@ -226,7 +236,7 @@ def test_copy_strided_permute(bridge, rng):
                                           (2, 2, 256, False), (1, 1, 1000, True)])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("round_scores", [False, True])
-def test_attention_mfma(bridge, rng, b, h, s, causal, dtype, round_scores):
+def test_attention_mfma(bridge, rng, fa7_block, b, h, s, causal, dtype, round_scores):
     d = 64
     q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
     scale = 1.0 / np.sqrt(d)
@@ -339,7 +349,7 @@ def test_gemm_f32_bias_relu_gelu(bridge, rng, m, k, n):
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("round_scores", [False, True])
-def test_attention_long_sequence(bridge, rng, dtype, causal, round_scores):
+def test_attention_long_sequence(bridge, rng, fa7_block, dtype, causal, round_scores):
     """Two full S=2048 heads (the C4 shape per head) and a ragged 1100."""
     for (b, h, s) in ((1, 2, 2048), (1, 1, 1100)):
         d = 64
@@ -360,7 +370,7 @@ def test_attention_long_sequence(bridge, rng, dtype, causal, round_scores):
         assert O.within(y, ref, TOL16).all(), (b, h, s, O.report(y, ref, TOL16))
 
 
-def test_attention_rectangular_noncausal(bridge, rng):
+def test_attention_rectangular_noncausal(bridge, rng, fa7_block):
     b, h, sq, sk, d = 2, 3, 100, 300, 64
     q = rng.standard_normal((b, h, sq, d)).astype(np.float16)
     k = rng.standard_normal((b, h, sk, d)).astype(np.float16)
@@ -374,7 +384,7 @@ def test_attention_rectangular_noncausal(bridge, rng):
 
 @pytest.mark.parametrize("sq,sk", [(300, 100), (100, 300), (600, 130), (257, 257), (64, 2048)])
 @pytest.mark.parametrize("round_scores", [False, True])
-def test_attention_rectangular_causal(bridge, rng, sq, sk, round_scores):
+def test_attention_rectangular_causal(bridge, rng, fa7_block, sq, sk, round_scores):
     """Causal with Sq != Sk: the reference mask triu(ones(Sq, Sk), k=1) is
     top-left aligned (key j visible to query i iff j <= i), so queries past Sk
     see every key.  (600, 130) puts whole query blocks past the last key."""
@@ -392,7 +402,7 @@ def test_attention_rectangular_causal(bridge, rng, sq, sk, round_scores):
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("round_scores", [False, True])
-def test_attention_late_dominant_key(bridge, rng, causal, dtype, round_scores):
+def test_attention_late_dominant_key(bridge, rng, fa7_block, causal, dtype, round_scores):
     """Head 0 holds a key (index 100) whose score beats every key of the first
     32 by far more than 16 (log2 units): a reference max taken from the first
     keys must move, or P overflows the 16-bit range.  Head 1 is ordinary
@@ -423,7 +433,7 @@ def test_attention_late_dominant_key(bridge, rng, causal, dtype, round_scores):
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_attention_dominant_key_long_sequence(bridge, rng, dtype):
+def test_attention_dominant_key_long_sequence(bridge, rng, fa7_block, dtype):
     """C4-length heads where keys 1500 and 40 dominate every earlier key by
     far more than 2^16: the fast kernel's reference max (from each query's
     first 32 keys) overflows P for the queries that see them, and those

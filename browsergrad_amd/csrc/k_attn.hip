@@ -1051,6 +1051,39 @@ __device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0
   }
 }
 
+// Workgroup -> (head, query block).  Heavy query blocks (causal: more key
+// tiles) come first in a global order whose position g maps to head g % bh
+// and block n_qblocks - 1 - g / bh.  Workgroups are dispatched round-robin
+// over the 8 XCDs, so XCD x takes positions x, x + 8, ... (a head's blocks
+// stay on one XCD when bh % 8 == 0); within an XCD the first rounds of 32
+// (one workgroup per CU) alternate direction, so a CU that starts with one
+// of the heaviest blocks of a round gets one of the lightest of the next:
+// with C5's 96 heads x 8 blocks (2..16 tiles, three per CU) the per-CU
+// tile sums go from 20-34 to 24-30 (modelled; 25.0 -> 24.0 us measured).
+// Reversing only whole rounds keeps the map a bijection.  Only the
+// 128-query shape uses it: its grids fit the resident slots at once, while
+// the 256-query shape's larger grids refill slots as blocks finish (there
+// the reordering measured 85.0 -> 87.2 us on C4).
+__device__ __forceinline__ void fa7_block_of(int lid, int bh, int nqb, bool snake, int& head, int& qblk) {
+  if (!snake) {  // plain heavy-first order, head fastest
+    head = lid % bh;
+    qblk = nqb - 1 - lid / bh;
+    return;
+  }
+  const int total = bh * nqb;
+  constexpr int kXcd = 8, kCusPerXcd = 32;
+  const bool split = total % kXcd == 0;
+  const int xcd = split ? lid % kXcd : 0;
+  const int j = split ? lid / kXcd : lid;
+  const int per = split ? total / kXcd : total;
+  const int round = j / kCusPerXcd, pos = j % kCusPerXcd;
+  const bool flip = (round & 1) && (round + 1) * kCusPerXcd <= per;
+  const int jj = round * kCusPerXcd + (flip ? kCusPerXcd - 1 - pos : pos);
+  const int g = split ? jj * kXcd + xcd : jj;
+  head = g % bh;
+  qblk = nqb - 1 - g / bh;
+}
+
 // NW wavefronts x 32 queries per workgroup, a RING-slot LDS ring of 64-key
 // K and V tiles.  <8, 4>: two workgroups per CU, four wavefronts per SIMD
 // (the long-sequence shape).  <4, 3>: 128-query workgroups, three per CU
@@ -1072,8 +1105,8 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hi = lane >> 5;
-  const int bh = blockIdx.x;
-  const int qblk = P.n_qblocks - 1 - int(blockIdx.y);  // heavy query blocks first
+  int bh, qblk;
+  fa7_block_of(int(blockIdx.y) * int(gridDim.x) + int(blockIdx.x), int(gridDim.x), P.n_qblocks, NW == 4, bh, qblk);
   const int b = bh / P.H, h = bh % P.H;
   const int q0 = qblk * BQ;
   const int q0w = q0 + w * kFa2QW;

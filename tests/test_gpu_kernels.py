@@ -462,6 +462,20 @@ def test_attention_dominant_key_long_sequence(bridge, rng, fa7_block, dtype):
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
 
 
+def test_attention_reordered_grid_every_head(bridge, rng):
+    """128-query workgroups of a grid that fills the resident slots take
+    their (head, query block) from a heavy-first order whose rounds of 32 per
+    XCD alternate direction.  4 x 16 heads x 8 blocks = 512 workgroups walk a
+    reversed round; every head and query block must come out once and right."""
+    b, h, s, d = 4, 16, 1024, 64
+    q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float16) for _ in range(3))
+    ho = bridge.attention_ex(up(bridge, q), up(bridge, k), up(bridge, v), batch=b, heads=h, sq=s, sk=s, d=d,
+                             scale=0.125, causal=True, in_dtype="float16", round_scores=False)
+    y = bridge.to_numpy(ho).astype(np.float32)
+    ref = O.sdpa_amp(q, k, v, 0.125, True).astype(np.float32)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
 @pytest.mark.parametrize("round_scores", [False, True])
 def test_attention_strided_fused_qkv_views(bridge, rng, round_scores):
     """Q/K/V as views into one fused QKV projection [B, S, 3, H, D] (the GPT-2

@@ -68,8 +68,8 @@ struct Args {
   float imm[16];
   void* out;
 };
-struct f4_ { float x, y, z, w; };
-struct u2_ { u32 x, y; };
+typedef float f4v_ __attribute__((ext_vector_type(4)));
+typedef u32 u2v_ __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bg_h2f(u16 v) { return (float)__builtin_bit_cast(_Float16, v); }
 __device__ __forceinline__ u16 bg_f2h(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
 __device__ __forceinline__ float bg_b2f(u16 v) { return __builtin_bit_cast(float, ((u32)v) << 16); }
@@ -136,15 +136,19 @@ std::string load1_expr(int dtype, int i, const std::string& off) {
 void emit_vec_load(std::ostringstream& os, int dtype, int i, const std::string& off, int V) {
   if (V == 4) {
     switch (dtype) {
+      // Operands stream through once: 16-byte (8-byte) aligned vector loads
+      // with the nontemporal hint (the launcher picks V = 4 only for
+      // aligned bases and strides).
       case BG_F32:
-        os << "    f4_ t" << i << " = *(const f4_*)((const float*)A.in[" << i << "] + (" << off
-           << "));\n    float x" << i << "[4] = {t" << i << ".x, t" << i << ".y, t" << i << ".z, t" << i
+        os << "    f4v_ t" << i << " = __builtin_nontemporal_load((const f4v_*)((const float*)A.in[" << i << "] + ("
+           << off << ")));\n    float x" << i << "[4] = {t" << i << ".x, t" << i << ".y, t" << i << ".z, t" << i
            << ".w};\n";
         return;
       case BG_F16:
       case BG_BF16: {
         const char* cv = dtype == BG_F16 ? "bg_h2f" : "bg_b2f";
-        os << "    u2_ t" << i << " = *(const u2_*)((const u16*)A.in[" << i << "] + (" << off << "));\n"
+        os << "    u2v_ t" << i << " = __builtin_nontemporal_load((const u2v_*)((const u16*)A.in[" << i << "] + ("
+           << off << ")));\n"
            << "    float x" << i << "[4] = {" << cv << "((u16)t" << i << ".x), " << cv << "((u16)(t" << i
            << ".x >> 16)), " << cv << "((u16)t" << i << ".y), " << cv << "((u16)(t" << i << ".y >> 16))};\n";
         return;
@@ -292,13 +296,13 @@ std::string generate(const Plan& p) {
        << "    const i64 col = (g - row * vcols) * " << V << ";\n";
     emit_body(os, p, V);
     if (V == 4 && p.out_dtype == BG_F32) {
-      os << "    f4_ r = {s" << last << "[0], s" << last << "[1], s" << last << "[2], s" << last << "[3]};\n"
-         << "    *(f4_*)((float*)A.out + lin) = r;\n";
+      os << "    f4v_ r = {s" << last << "[0], s" << last << "[1], s" << last << "[2], s" << last << "[3]};\n"
+         << "    *(f4v_*)((float*)A.out + lin) = r;\n";
     } else if (V == 4 && (p.out_dtype == BG_F16 || p.out_dtype == BG_BF16)) {
       const char* cv = p.out_dtype == BG_F16 ? "bg_f2h" : "bg_f2b";
-      os << "    u2_ r = {(u32)" << cv << "(s" << last << "[0]) | ((u32)" << cv << "(s" << last
+      os << "    u2v_ r = {(u32)" << cv << "(s" << last << "[0]) | ((u32)" << cv << "(s" << last
          << "[1]) << 16), (u32)" << cv << "(s" << last << "[2]) | ((u32)" << cv << "(s" << last
-         << "[3]) << 16)};\n    *(u2_*)((u16*)A.out + lin) = r;\n";
+         << "[3]) << 16)};\n    *(u2v_*)((u16*)A.out + lin) = r;\n";
     } else {
       os << "#pragma unroll\n    for (int j = 0; j < " << V << "; ++j) { "
          << store_expr(p.out_dtype, "lin + j", "s" + std::to_string(last) + "[j]") << " }\n";

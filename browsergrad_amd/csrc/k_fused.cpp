@@ -136,19 +136,20 @@ std::string load1_expr(int dtype, int i, const std::string& off) {
 void emit_vec_load(std::ostringstream& os, int dtype, int i, const std::string& off, int V) {
   if (V == 4) {
     switch (dtype) {
-      // Operands stream through once: 16-byte (8-byte) aligned vector loads
-      // with the nontemporal hint (the launcher picks V = 4 only for
-      // aligned bases and strides).
+      // 16-byte (8-byte) aligned vector loads (the launcher picks V = 4
+      // only for aligned bases and strides); LD_ is the nontemporal load in
+      // reductions, whose operands stream through once with nothing
+      // written back (measured: 6.3 -> 6.7 TB/s read on the C2 shape), and a
+      // plain load in map kernels (the hint slowed f32 -> f16 casts by 20%).
       case BG_F32:
-        os << "    f4v_ t" << i << " = __builtin_nontemporal_load((const f4v_*)((const float*)A.in[" << i << "] + ("
-           << off << ")));\n    float x" << i << "[4] = {t" << i << ".x, t" << i << ".y, t" << i << ".z, t" << i
+        os << "    f4v_ t" << i << " = LD_((const f4v_*)((const float*)A.in[" << i << "] + (" << off
+           << ")));\n    float x" << i << "[4] = {t" << i << ".x, t" << i << ".y, t" << i << ".z, t" << i
            << ".w};\n";
         return;
       case BG_F16:
       case BG_BF16: {
         const char* cv = dtype == BG_F16 ? "bg_h2f" : "bg_b2f";
-        os << "    u2v_ t" << i << " = __builtin_nontemporal_load((const u2v_*)((const u16*)A.in[" << i << "] + ("
-           << off << ")));\n"
+        os << "    u2v_ t" << i << " = LD_((const u2v_*)((const u16*)A.in[" << i << "] + (" << off << ")));\n"
            << "    float x" << i << "[4] = {" << cv << "((u16)t" << i << ".x), " << cv << "((u16)(t" << i
            << ".x >> 16)), " << cv << "((u16)t" << i << ".y), " << cv << "((u16)(t" << i << ".y >> 16))};\n";
         return;
@@ -283,6 +284,7 @@ std::string generate(const Plan& p) {
   os << kPrelude;
   const int V = p.vec;
   const int last = int(p.ops.size()) - 1;
+  os << (p.reduce == BG_RED_NONE ? "#define LD_(p) (*(p))\n" : "#define LD_(p) __builtin_nontemporal_load(p)\n");
   os << "extern \"C\" __global__ void __launch_bounds__(256) bg_fused(Args A) {\n";
   // Scalars hoisted out of the loop.
   for (int i = 0; i < p.n_in; ++i)

@@ -1158,10 +1158,24 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
   for (int dc = 0; dc < 4; ++dc)
     qf[dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
                        : fa_u4{0u, 0u, 0u, 0u};
+  // PAIRS (the 4-slot ring): tiles are awaited and refilled two at a time,
+  // one barrier per two tiles: at an even step t the wavefronts wait for
+  // tiles t and t+1, pass the barrier and copy tiles t+2 and t+3 into the
+  // slots of t-2 and t-1, so each copy has two tiles of compute to land.
+  constexpr bool PAIRS = RING == 4;
+  if constexpr (PAIRS) {
+    issue(0);
+    issue(1);
+  } else {
 #pragma unroll
-  for (int j = 0; j < RING - 1; ++j) issue(j);
+    for (int j = 0; j < RING - 1; ++j) issue(j);
+  }
   fa2_wait_vm_lgkm0<0>();  // also retires the Q loads in the compiler's bookkeeping
   __builtin_amdgcn_s_barrier();
+  if constexpr (PAIRS) {
+    issue(2);
+    issue(3);
+  }
 #pragma unroll
   for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
@@ -1197,11 +1211,20 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
 
   int t = 0;
   for (; t < t_clean; ++t) {
-    if (t > 0) {
-      fa2_wait_vm_lgkm0<(RING - 2) * DMA>();  // tile t landed; t+1 .. t+RING-2 may be in flight
-      __builtin_amdgcn_s_barrier();
+    if constexpr (PAIRS) {
+      if (t > 0 && (t & 1) == 0) {
+        fa2_wait_vm_lgkm0<0>();  // tiles t, t+1 landed
+        __builtin_amdgcn_s_barrier();
+        issue(t + 2);  // into the slots of tiles t-2, t-1, which every wavefront has left
+        issue(t + 3);
+      }
+    } else {
+      if (t > 0) {
+        fa2_wait_vm_lgkm0<(RING - 2) * DMA>();  // tile t landed; t+1 .. t+RING-2 may be in flight
+        __builtin_amdgcn_s_barrier();
+      }
+      issue(t + RING - 1);  // into the slot of tile t-1, which every wavefront has left
     }
-    issue(t + RING - 1);  // into the slot of tile t-1, which every wavefront has left
     const char* kt = kring + (t % RING) * kFa2Tile;
     const char* vt = vring + (t % RING) * kFa2Tile;
 #pragma unroll
@@ -1213,11 +1236,20 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
     }
   }
   for (; t < nt; ++t) {
-    if (t > 0) {
-      fa2_wait_vm_lgkm0<(RING - 2) * DMA>();
-      __builtin_amdgcn_s_barrier();
+    if constexpr (PAIRS) {
+      if (t > 0 && (t & 1) == 0) {
+        fa2_wait_vm_lgkm0<0>();
+        __builtin_amdgcn_s_barrier();
+        issue(t + 2);
+        issue(t + 3);
+      }
+    } else {
+      if (t > 0) {
+        fa2_wait_vm_lgkm0<(RING - 2) * DMA>();
+        __builtin_amdgcn_s_barrier();
+      }
+      issue(t + RING - 1);
     }
-    issue(t + RING - 1);
     const char* kt = kring + (t % RING) * kFa2Tile;
     const char* vt = vring + (t % RING) * kFa2Tile;
     if (t < ntw) {

@@ -446,13 +446,16 @@ def bench_c4(br, steps, warmup):
            "tflops_kernel": flops / (k_ms * 1e-3) / 1e12,
            "tflops_wall": flops / (wall_ms * 1e-3) / 1e12}
     out["frac_of_peak"] = out["tflops_kernel"] / MFMA_F16_PEAK_TFLOPS
-    from oracle import ops as O  # checker only: two (b, h) slices
+    from oracle import ops as O  # checker only: eight (b, h) slices over all batches
     h = run()
     y = br.to_numpy(h).astype(np.float32)
     br.release(h)
-    sl = (slice(0, 1), slice(0, 2))
-    ref = O.sdpa_amp(q[sl], k[sl], v[sl], scale, True).astype(np.float32)
-    out["parity"] = O.report(y[sl], ref, 2e-2)
+    picks = [(0, 0), (1, 15), (2, 7), (3, 8), (4, 1), (5, 14), (6, 10), (7, 15)]
+    ys = np.stack([y[b, hh] for b, hh in picks])
+    refs = np.stack([O.sdpa_amp(q[b:b + 1, hh:hh + 1], k[b:b + 1, hh:hh + 1], v[b:b + 1, hh:hh + 1], scale,
+                                True)[0, 0] for b, hh in picks]).astype(np.float32)
+    out["parity"] = O.report(ys, refs, 2e-2)
+    out["parity"]["heads_checked"] = [f"b{b}h{hh}" for b, hh in picks]
     for hh in (hq, hk, hv):
         br.release(hh)
     return out

@@ -1064,24 +1064,24 @@ __device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0
 // 128-query shape uses it: its grids fit the resident slots at once, while
 // the 256-query shape's larger grids refill slots as blocks finish (there
 // the reordering measured 85.0 -> 87.2 us on C4).
-__device__ __forceinline__ void fa7_block_of(int lid, int bh, int nqb, bool snake, int& head, int& qblk) {
+__device__ __forceinline__ void fa7_block_of(int64_t lid, int bh, int nqb, bool snake, int& head, int& qblk) {
   if (!snake) {  // plain heavy-first order, head fastest
-    head = lid % bh;
-    qblk = nqb - 1 - lid / bh;
+    head = int(lid % bh);
+    qblk = nqb - 1 - int(lid / bh);
     return;
   }
-  const int total = bh * nqb;
+  const int64_t total = int64_t(bh) * nqb;
   constexpr int kXcd = 8, kCusPerXcd = 32;
   const bool split = total % kXcd == 0;
-  const int xcd = split ? lid % kXcd : 0;
-  const int j = split ? lid / kXcd : lid;
-  const int per = split ? total / kXcd : total;
-  const int round = j / kCusPerXcd, pos = j % kCusPerXcd;
+  const int64_t xcd = split ? lid % kXcd : 0;
+  const int64_t j = split ? lid / kXcd : lid;
+  const int64_t per = split ? total / kXcd : total;
+  const int64_t round = j / kCusPerXcd, pos = j % kCusPerXcd;
   const bool flip = (round & 1) && (round + 1) * kCusPerXcd <= per;
-  const int jj = round * kCusPerXcd + (flip ? kCusPerXcd - 1 - pos : pos);
-  const int g = split ? jj * kXcd + xcd : jj;
-  head = g % bh;
-  qblk = nqb - 1 - g / bh;
+  const int64_t jj = round * kCusPerXcd + (flip ? kCusPerXcd - 1 - pos : pos);
+  const int64_t g = split ? jj * kXcd + xcd : jj;
+  head = int(g % bh);
+  qblk = nqb - 1 - int(g / bh);
 }
 
 // NW wavefronts x 32 queries per workgroup, a RING-slot LDS ring of 64-key
@@ -1106,7 +1106,7 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hi = lane >> 5;
   int bh, qblk;
-  fa7_block_of(int(blockIdx.y) * int(gridDim.x) + int(blockIdx.x), int(gridDim.x), P.n_qblocks, NW == 4, bh, qblk);
+  fa7_block_of(int64_t(blockIdx.y) * gridDim.x + blockIdx.x, int(gridDim.x), P.n_qblocks, NW == 4, bh, qblk);
   const int b = bh / P.H, h = bh % P.H;
   const int q0 = qblk * BQ;
   const int q0w = q0 + w * kFa2QW;

@@ -549,3 +549,32 @@ def test_attention_large_scale_routes_around_prescaled_q(bridge, rng):
         y = bridge.to_numpy(ho).astype(np.float32)
         assert np.isfinite(y).all()
         assert O.within(y, ref, TOL16).all(), (rs, O.report(y, ref, TOL16))
+
+
+@pytest.mark.parametrize("m,k,n,act,residual", [(8000, 768, 768, 0, True), (4100, 768, 2304, 0, False),
+                                                (8192, 136, 3072, 2, False), (2000, 3072, 768, 1, True)])
+def test_gemm_128x192_tiles_ragged(bridge, rng, monkeypatch, m, k, n, act, residual):
+    """Widths that are multiples of 192 take 128x192 tiles (an 8-wavefront
+    4 x 2 grid); ragged M and a K tail must give the same bits as another
+    tile shape's kernel (both accumulate each 16-wide k chunk in order) and
+    match the oracle's autocast linear."""
+    x = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, (n,)).astype(np.float32)
+    x16, w16 = x.astype(np.float16), w.astype(np.float16)
+    hx, hw, hb = up(bridge, x16), up(bridge, w16), up(bridge, b)
+    r = rng.standard_normal((m, n)).astype(np.float32) if residual else None
+    kw = dict(m=m, n=n, k=k, trans_b=True, in_dtype="float16", out_dtype="float32", bias=hb, round_out=True,
+              act=act, residual=up(bridge, r) if residual else None)
+    y = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw))
+    monkeypatch.setenv("BG_GEMM_TILE", "128x128x64s2")
+    y2 = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw))
+    assert np.array_equal(y.view(np.uint8), y2.view(np.uint8))
+    z = O.matmul(x16, np.ascontiguousarray(w16.T)).astype(np.float32) + b
+    if act == 1:
+        z = np.maximum(z, np.float32(0))
+    elif act == 2:
+        z = O.gelu_tanh_f32(z)
+    if residual:
+        z = z + r
+    assert O.within(y, z, TOL16).all(), O.report(y, z, TOL16)

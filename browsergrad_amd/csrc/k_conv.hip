@@ -19,6 +19,7 @@
 // bounds-checked loops skip them.  The product runs on v_mfma_f32_32x32x2f32
 // (full f32) in 64- or 128-wide workgroup tiles of four wavefronts.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.cuh"
@@ -68,6 +69,65 @@ struct ConvK {
 };
 
 constexpr int CBK = 16;  // k-step of every tile; WGRAD slices are multiples of it
+
+// Epilogue shared by the conv GEMM kernels: bias, then the store of each
+// wavefront's (BM/2) x (BN/2) block (WGRAD: into its split slice).
+template <int MODE, int BM, int BN>
+__device__ __forceinline__ void conv_epilogue(const ConvK& P, float16v (&acc)[BM / 64][BN / 64], int m0, int n0,
+                                              int wm, int wn, int g, int split) {
+  constexpr int TM = BM / 64, TN = BN / 64;
+  const int lane = threadIdx.x & 63;
+  // Lane l holds rows 8*(e/4) + (e%4) + 4*(l/32) and column l%32 of each
+  // 32 x 32 tile: groups of four consecutive rows, stored as one float4 when
+  // they are contiguous and aligned in the output (spatial size % 4 == 0).
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+    if (col >= P.NC) continue;
+    float bz = 0.f;
+    if constexpr (MODE == MODE_FWD) {
+      if (P.bias) bz = P.bias[int64_t(g) * P.Opg + col];
+    } else if constexpr (MODE == MODE_DGRAD) {
+      if (P.bias) bz = P.bias[int64_t(g) * P.Cpg + col];
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = m0 + wm * (BM / 2) + i * 32 + 8 * q + 4 * (lane >> 5);
+        if (row >= P.M) continue;
+        if constexpr (MODE == MODE_WGRAD) {
+          float* dst = P.out + int64_t(split) * P.part_stride + (int64_t(g) * P.Opg + row) * P.NC + col;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (row + e < P.M) dst[int64_t(e) * P.NC] = acc[i][j][4 * q + e];
+        } else {
+          const int spatial = MODE == MODE_FWD ? P.oS : P.S;
+          const int chans = MODE == MODE_FWD ? P.O : P.C;
+          const int cpg = MODE == MODE_FWD ? P.Opg : P.Cpg;
+          const uint32_t n = fdiv(uint32_t(row), MODE == MODE_FWD ? P.f_oS : P.f_S);
+          const uint32_t sp = uint32_t(row) - n * uint32_t(spatial);
+          float* dst = P.out + (int64_t(n) * chans + int64_t(g) * cpg + col) * spatial + sp;
+          const float4 v = make_float4(acc[i][j][4 * q] + bz, acc[i][j][4 * q + 1] + bz,
+                                       acc[i][j][4 * q + 2] + bz, acc[i][j][4 * q + 3] + bz);
+          if ((spatial & 3) == 0 && row + 3 < P.M) {
+            *reinterpret_cast<float4*>(dst) = v;
+          } else {
+            // Rows may cross into the next image: place each one on its own.
+            const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int re = row + e;
+              if (re >= P.M) break;
+              const uint32_t ne = fdiv(uint32_t(re), MODE == MODE_FWD ? P.f_oS : P.f_S);
+              const uint32_t se = uint32_t(re) - ne * uint32_t(spatial);
+              P.out[(int64_t(ne) * chans + int64_t(g) * cpg + col) * spatial + se] = vals[e];
+            }
+          }
+        }
+      }
+  }
+}
 
 // Workgroup tile BM x BN (64 or 128 each), four wavefronts in a 2 x 2 grid,
 // each holding (BM/2) x (BN/2) as TM x TN MFMA 32 x 32 accumulators.
@@ -281,56 +341,148 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
     __syncthreads();
   }
 
-  // Lane l holds rows 8*(e/4) + (e%4) + 4*(l/32) and column l%32 of each
-  // 32 x 32 tile: groups of four consecutive rows, stored as one float4 when
-  // they are contiguous and aligned in the output (spatial size % 4 == 0).
+  conv_epilogue<MODE, BM, BN>(P, acc, m0, n0, wm, wn, g, split);
+}
+
+// Forward convolution with the operands gathered straight into an S-stage
+// LDS ring by buffer_load_dword ... lds (one wavefront instruction fills one
+// 64-float row of a k-major tile: lane L writes element L, fetching whatever
+// x or w value that row position needs).  Taps outside the input, rows past
+// M, columns past NC and k past the reduction get an offset beyond the
+// buffer's num_records and read 0, so the gathers need no branches and no
+// register round trip; copies run S-1 k-steps ahead of the MFMAs and each
+// step waits only for its own stage.  Same tile, MFMA and epilogue as
+// conv_gemm_kernel<MODE_FWD>; requires x and w below 2 GiB (32-bit offsets).
+constexpr uint32_t kConvOob = 0x80000000u;
+
+// buffer_load_dword ... lds: lane L copies the 4 bytes at voffset + soffset
+// of the buffer to LDS byte lds_base + 4 L.  Inline assembly for the reason
+// given at bgk::dma16_to_lds: with the builtin the compiler makes every later
+// LDS read wait for all outstanding copies, which empties the ring.  The
+// leading s_nop keeps five wait states between a VALU write of an SGPR
+// operand and this VMEM read of it.
+__device__ __forceinline__ void conv_dma4_to_lds(uint32_t lds_base, uint32_t voffset, bgk::sgpr4_t rsrc,
+                                                 uint32_t soffset) {
+  asm volatile(
+      "s_nop 4\n\t"
+      "buffer_load_dword %1, %2, %3 offen lds"
+      :
+      : "{m0}"(lds_base), "v"(voffset), "s"(rsrc), "s"(soffset)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void conv_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int S>
+__global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_bytes, uint32_t b_bytes) {
+  constexpr int LDA = BM + 1, LDB = BN + 1;
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int QA = BM / 64, QB = BN / 64;  // 64-float rows per k row
+  constexpr int IA = CBK * QA / 4, IB = CBK * QB / 4;  // instructions per wavefront per stage
+  constexpr int NLD = IA + IB;
+  static_assert(NLD * (S - 1) < 64, "vmcnt range");
+  __shared__ float As[S][CBK * LDA];
+  __shared__ float Bs[S][CBK * LDB];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tm = int(blockIdx.x) % P.tiles_m, tn = int(blockIdx.x) / P.tiles_m;
+  const int g = int(blockIdx.y);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int K = P.K;
+  const int KHW = P.KH * P.KW;
+
+  // Instruction i of wavefront w covers tile row block (i*4 + w) % Q at k
+  // offset (i*4 + w) / Q; for Q = 1 or 2 the block is fixed per wavefront.
+  const int qa = QA == 1 ? 0 : (wave & 1);
+  const int qb = QB == 1 ? 0 : (wave & 1);
+  // A: this lane's output position m -> x base and input origin.
+  const int m = m0 + qa * 64 + lane;
+  const bool row_ok = m < P.M;
+  const uint32_t mm = row_ok ? uint32_t(m) : 0u;
+  const uint32_t n = fdiv(mm, P.f_oS), sp = mm - n * uint32_t(P.oS);
+  const uint32_t od = fdiv(sp, P.f_oHW), rr = sp - od * uint32_t(P.oH * P.oW);
+  const uint32_t oh = fdiv(rr, P.f_oW), ow = rr - oh * uint32_t(P.oW);
+  const int64_t a_base = (int64_t(n) * P.C + int64_t(g) * P.Cpg) * P.S;
+  const int p0 = int(od) * P.sd - P.pd, p1 = int(oh) * P.sh - P.ph, p2 = int(ow) * P.sw - P.pw;
+  // B: this lane's output channel o -> w row.
+  const int o = n0 + qb * 64 + lane;
+  const uint32_t b_lane = o < P.NC ? uint32_t((int64_t(g) * P.Opg + o) * K * 4) : kConvOob;
+
+  const bgk::sgpr4_t ra = bgk::buffer_rsrc(P.a, a_bytes);
+  const bgk::sgpr4_t rb = bgk::buffer_rsrc(P.b, b_bytes);
+  const int nk = (K + CBK - 1) / CBK;
+
+  auto issue_stage = [&](int t) {
+    const int slot = t % S;
+    const int k0 = t * CBK;
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
-    if (col >= P.NC) continue;
-    float bz = 0.f;
-    if constexpr (MODE == MODE_FWD) {
-      if (P.bias) bz = P.bias[int64_t(g) * P.Opg + col];
-    } else if constexpr (MODE == MODE_DGRAD) {
-      if (P.bias) bz = P.bias[int64_t(g) * P.Cpg + col];
+    for (int i = 0; i < IA; ++i) {
+      const int kl = (i * 4 + wave) / QA;
+      const int k = k0 + kl;  // uniform
+      const bool k_ok = k < K;
+      const uint32_t kc = k_ok ? uint32_t(k) : 0u;
+      const uint32_t c = fdiv(kc, P.f_KV), kv = kc - c * uint32_t(P.KV);
+      const uint32_t kd = fdiv(kv, P.f_KHW), r = kv - kd * uint32_t(KHW);
+      const uint32_t kh = fdiv(r, P.f_KW), kw = r - kh * uint32_t(P.KW);
+      const int id = p0 + int(kd) * P.dd, ih = p1 + int(kh) * P.dh, iw = p2 + int(kw) * P.dw;
+      const bool ok = k_ok && row_ok && unsigned(id) < unsigned(P.D) && unsigned(ih) < unsigned(P.H) &&
+                      unsigned(iw) < unsigned(P.W);
+      const uint32_t off =
+          ok ? uint32_t((a_base + int64_t(c) * P.S + (int64_t(id) * P.H + ih) * P.W + iw) * 4) : kConvOob;
+      conv_dma4_to_lds(bgk::lds_addr(&As[slot][kl * LDA + qa * 64]), off, ra, 0u);
     }
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < IB; ++i) {
+      const int kl = (i * 4 + wave) / QB;
+      const int k = k0 + kl;  // uniform
+      const uint32_t off = k < K ? b_lane : kConvOob;
+      conv_dma4_to_lds(bgk::lds_addr(&Bs[slot][kl * LDB + qb * 64]), off, rb, uint32_t(k < K ? k * 4 : 0));
+    }
+  };
+
+  float16v acc[TM][TN];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = m0 + wm * (BM / 2) + i * 32 + 8 * q + 4 * (lane >> 5);
-        if (row >= P.M) continue;
-        if constexpr (MODE == MODE_WGRAD) {
-          float* dst = P.out + int64_t(split) * P.part_stride + (int64_t(g) * P.Opg + row) * P.NC + col;
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (row + e < P.M) dst[int64_t(e) * P.NC] = acc[i][j][4 * q + e];
-        } else {
-          const int spatial = MODE == MODE_FWD ? P.oS : P.S;
-          const int chans = MODE == MODE_FWD ? P.O : P.C;
-          const int cpg = MODE == MODE_FWD ? P.Opg : P.Cpg;
-          const uint32_t n = fdiv(uint32_t(row), MODE == MODE_FWD ? P.f_oS : P.f_S);
-          const uint32_t sp = uint32_t(row) - n * uint32_t(spatial);
-          float* dst = P.out + (int64_t(n) * chans + int64_t(g) * cpg + col) * spatial + sp;
-          const float4 v = make_float4(acc[i][j][4 * q] + bz, acc[i][j][4 * q + 1] + bz,
-                                       acc[i][j][4 * q + 2] + bz, acc[i][j][4 * q + 3] + bz);
-          if ((spatial & 3) == 0 && row + 3 < P.M) {
-            *reinterpret_cast<float4*>(dst) = v;
-          } else {
-            // Rows may cross into the next image: place each one on its own.
-            const float vals[4] = {v.x, v.y, v.z, v.w};
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int re = row + e;
-              if (re >= P.M) break;
-              const uint32_t ne = fdiv(uint32_t(re), MODE == MODE_FWD ? P.f_oS : P.f_S);
-              const uint32_t se = uint32_t(re) - ne * uint32_t(spatial);
-              P.out[(int64_t(ne) * chans + int64_t(g) * cpg + col) * spatial + se] = vals[e];
-            }
-          }
-        }
-      }
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Stages past the reduction load only zeros (every offset out of range),
+  // so each step issues the same number of copies and the partial waits
+  // below always name the right stage.
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t) issue_stage(t);
+  for (int kt = 0; kt < nk; ++kt) {
+    // Stage kt has landed (later stages may still be in flight), every
+    // wavefront has finished reading the slot refilled next.
+    conv_wait_vmcnt<NLD * (S - 2)>();
+    __syncthreads();
+    issue_stage(kt + S - 1);
+    const int buf = kt % S;
+#pragma unroll
+    for (int s = 0; s < CBK / 2; ++s) {
+      const int k = 2 * s + (lane >> 5);
+      float af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = As[buf][k * LDA + wm * (BM / 2) + i * 32 + (lane & 31)];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = Bs[buf][k * LDB + wn * (BN / 2) + j * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
   }
+  conv_wait_vmcnt<0>();  // the run-out copies still write LDS; let them land before exit
+
+  conv_epilogue<MODE_FWD, BM, BN>(P, acc, m0, n0, wm, wn, g, 0);
 }
 
 // dw[i] = sum over split slices (in order) of part[s][i].
@@ -549,6 +701,21 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   }
   if (k.M == 0 || k.NC == 0) return;
   const dim3 grid(unsigned(tiles), unsigned(G * k.ksplit));
+  // Forward: the LDS-ring kernel when x and w fit 32-bit byte offsets
+  // (BG_CONV_RING=0 selects the register-staged kernel, for comparisons).
+  const int64_t a_bytes = p.n * int64_t(k.C) * k.S * 4, b_bytes = int64_t(k.O) * k.K * 4;
+  const char* ring_env = std::getenv("BG_CONV_RING");
+  const bool ring = mode == 0 && a_bytes < (int64_t(1) << 31) && b_bytes < (int64_t(1) << 31) &&
+                    !(ring_env && ring_env[0] == '0');
+  if (ring) {
+    auto go_ring = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes)); };
+    if (bm == 128 && bn == 128) go_ring(conv_fwd_ring_kernel<128, 128, 4>);
+    else if (bm == 128) go_ring(conv_fwd_ring_kernel<128, 64, 4>);
+    else if (bn == 128) go_ring(conv_fwd_ring_kernel<64, 128, 4>);
+    else go_ring(conv_fwd_ring_kernel<64, 64, 4>);
+    hip_check(hipGetLastError(), "conv launch");
+    return;
+  }
   auto go = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k); };
   auto pick = [&](auto mode_tag) {
     constexpr int MD = decltype(mode_tag)::value;

@@ -287,6 +287,31 @@ def test_conv_ex_matches_oracle(bridge, case):
         assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
 
 
+@pytest.mark.parametrize("case", [CASES[i] for i in (0, 2, 3, 5, 6)])
+def test_conv_forward_ring_matches_register_kernel(bridge, case, monkeypatch):
+    """The forward (and the stride-1 input gradient, which runs as a forward
+    convolution) copies its operands into an LDS ring; BG_CONV_RING=0 selects
+    the register-staged kernel. Both feed the MFMAs the same k sequence, so
+    the outputs are bit-identical, and both match the oracle."""
+    r, n, ci, ins, co, k, s, p, d, g = case
+    rng = np.random.default_rng(sum(ins) + 29 * co)
+    x = rng.standard_normal((n, ci) + ins).astype(F32)
+    w = rng.standard_normal((co, ci // g) + k).astype(F32)
+    b = rng.standard_normal(co).astype(F32)
+    out = _out_size(ins, k, s, p, d)
+    dy = rng.standard_normal((n, co) + out).astype(F32)
+    kw = dict(n=n, c_in=ci, c_out=co, in_size=ins, out_size=out, k=k, stride=s, pad=p, dilation=d, groups=g)
+    runs = {}
+    for env in ("1", "0"):
+        monkeypatch.setenv("BG_CONV_RING", env)
+        runs[env] = (conv_ex(bridge, "forward", x, w, b, **kw), conv_ex(bridge, "backward_input", dy, w, **kw))
+    for got, ref in zip(runs["1"], (O.conv_forward(x, w, b, s, p, d, g, out),
+                                    O.conv_backward_input(dy, w, s, p, d, g, ins))):
+        assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
+    for a, c in zip(runs["1"], runs["0"]):
+        assert np.array_equal(a, c)
+
+
 TCASES = [
     (2, 4, (3, 4), 6, (3, 2), (2, 2), (1, 0), (1, 1), (1, 1), 2),
     (1, 3, (5, 5), 2, (2, 3), (1, 2), (0, 1), (0, 1), (2, 1), 1),

@@ -1,9 +1,9 @@
-"""Typed ATTENTION_FORWARD contract (SURVEY a20) on the CPU.
+"""Typed ATTENTION_FORWARD contract on the CPU.
 
 Acceptance / refusal cases follow
 packages/browsergrad-jit/src/python/_framework_contracts.py:2755-2932 and the
-public surface index.ts:212-265; C4's shape is refused by the work ceiling,
-as SURVEY a20 records.  The float32 restatement is pinned against the
+public surface index.ts:212-265; C4's shape is refused by the work ceiling
+(_framework_contracts.py:89-93).  The float32 restatement is pinned against the
 float64 definition and the Q = 0 -> mean(V) identity.
 """
 from __future__ import annotations
@@ -58,7 +58,7 @@ def test_contract_dtype_and_extent_types():
 
 
 def test_c4_work_is_over_the_ceiling():
-    # B8 H16 S2048 D64 -> 2^36 multiply-add elements > 2^30.
+    # B8 H16 S2048 D64 -> 2^36 multiply-add elements > 2^30 (_framework_contracts.py:89-93).
     assert 8 * 16 * 2048 * 2048 * 2 * 64 == 1 << 36 > ATTENTION_FORWARD_WORK_ELEMENT_MAX
 
 

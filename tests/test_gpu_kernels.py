@@ -578,3 +578,29 @@ def test_gemm_128x192_tiles_ragged(bridge, rng, monkeypatch, m, k, n, act, resid
     if residual:
         z = z + r
     assert O.within(y, z, TOL16).all(), O.report(y, z, TOL16)
+
+
+@pytest.mark.parametrize("shared_w", [True, False])
+def test_gemm_128x192_tiles_batched(bridge, rng, monkeypatch, shared_w):
+    """Batched 128x192 tiles (batch 8, ragged M = 1100, K tail 200): each
+    batch reads its own A, residual and C slices and either one shared B
+    (stride 0) or its own; bit-identical to the 128x128 kernel and within
+    the bar of the oracle's per-batch autocast linear."""
+    bt, m, k, n = 8, 1100, 200, 768
+    x = rng.uniform(-1, 1, (bt, m, k)).astype(np.float32)
+    nw = 1 if shared_w else bt
+    w = (rng.standard_normal((nw, n, k)) * 0.05).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, (n,)).astype(np.float32)
+    r = rng.standard_normal((bt, m, n)).astype(np.float32)
+    x16, w16 = x.astype(np.float16), w.astype(np.float16)
+    hx, hw, hb, hr = up(bridge, x16), up(bridge, w16), up(bridge, b), up(bridge, r)
+    kw = dict(m=m, n=n, k=k, batch=bt, trans_b=True, stride_b=0 if shared_w else n * k, in_dtype="float16",
+              out_dtype="float32", bias=hb, round_out=True, residual=hr)
+    y = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw)).reshape(bt, m, n)
+    monkeypatch.setenv("BG_GEMM_TILE", "128x128x64s2")
+    y2 = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw)).reshape(bt, m, n)
+    assert np.array_equal(y.view(np.uint8), y2.view(np.uint8))
+    for i in range(bt):
+        wi = w16[0 if shared_w else i]
+        z = O.matmul(x16[i], np.ascontiguousarray(wi.T)).astype(np.float32) + b + r[i]
+        assert O.within(y[i], z, TOL16).all(), (i, O.report(y[i], z, TOL16))

@@ -348,6 +348,10 @@ BIG = [
     (4, 64, (32, 32), 64, (3, 3), (1, 1), (1, 1)),
     (8, 32, (16, 16), 96, (3, 3), (2, 2), (1, 1)),
     (2, 3, (64, 64), 16, (7, 7), (2, 2), (3, 3)),
+    # 512 output tiles of 128 x 128 for the forward and of 128 x 64 for the
+    # stride-1 input gradient (run as a forward convolution with C and O
+    # exchanged): the ring kernel's 128-wide shapes.
+    (16, 4, (64, 64), 128, (3, 3), (1, 1), (1, 1)),
 ]
 
 
@@ -382,6 +386,31 @@ def test_conv2d_large_against_float64(bridge, case):
         err = np.abs(got - truth)
         bound = _bound(truth, mass, K)
         assert np.all(err <= bound), float(np.max(err / bound))
+
+
+def test_conv_ring_wide_tiles_launched(bridge):
+    """BIG's last case runs the ring kernel's 128 x 128 shape (forward) and
+    128 x 64 shape (stride-1 input gradient), as the launch log shows."""
+    n, ci, hw, co, k, s, p = BIG[-1]
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((n, ci) + hw).astype(F32)
+    w = rng.standard_normal((co, ci) + k).astype(F32)
+    out = _out_size(hw, k, s, p, (1, 1))
+    dy = rng.standard_normal((n, co) + out).astype(F32)
+    kw = dict(n=n, c_in=ci, c_out=co, in_size=hw, out_size=out, k=k, stride=s, pad=p, dilation=(1, 1))
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        conv_ex(bridge, "forward", x, w, **kw)
+        fwd = [r["kernel"] for r in bridge.take_launch_log()]
+        conv_ex(bridge, "backward_input", dy, w, **kw)
+        bwd = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    wide = lambda names, bn: any("conv_fwd_ring_kernel" in t and (f"ILi128ELi{bn}ELi4E" in t or f"<128, {bn}, 4>" in t)
+                                 for t in names)
+    assert wide(fwd, 128), fwd
+    assert wide(bwd, 64), bwd
 
 
 @pytest.mark.parametrize("shape", [(4, 16, 28, 28), (3, 5, 7, 7), (2, 3, 4, 300)])

@@ -50,18 +50,30 @@ C2_OPS = [("MUL", -1, -2, 0), ("ADD", 0, -3, 0), ("IMM", 0, 0, 0), ("CMP_GT", 1,
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "fused_c2_rowsum_4096x4096_traffic.md")
 
 
+TRAFFIC_SOURCE = os.path.join(ROOT, "browsergrad_amd", "csrc", "k_fused.cpp")
+
+
 def measured_traffic():
     """HBM bytes per launch of the C2 kernel from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE passes (calibrated against a copy kernel of
-    known size); None when that profile is absent."""
+    known size).  None when that profile is absent, or when it was measured
+    on another version of the kernel generator: the profile records the
+    sha256 of k_fused.cpp it was taken with, and any edit to that file makes
+    the number stale until the passes are run again."""
+    import hashlib
+    want = value = None
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+                    value = int(line.split(":")[1])
+                elif line.startswith("generator_sha256:"):
+                    want = line.split(":")[1].strip()
+        with open(TRAFFIC_SOURCE, "rb") as f:
+            have = hashlib.sha256(f.read()).hexdigest()
     except OSError:
-        pass
-    return None
+        return None
+    return value if want is not None and want == have else None
 
 
 def log(msg: str) -> None:

@@ -204,8 +204,6 @@ void launch_optimizer_fused(bg_ctx* ctx, int kind, const bg_optim_args& a, doubl
 // in[] holds the kind's inputs in bg_optimizer_update order (unused slots NULL).
 void launch_optimizer(bg_ctx* ctx, int kind, const bg_optim_args& a, const float* const (&in)[4], float* out,
                       int64_t n);
-void launch_reduce_last(bg_ctx* ctx, const void* x, int dtype, void* y,
-                        int64_t rows, int64_t cols, int op);
 void launch_softmax_last(bg_ctx* ctx, const void* x, int x_dtype, void* y, int y_dtype,
                          int64_t rows, int64_t cols);
 // Extras of bg_matmul_ex2: operand storage dtypes converted in a pre-pass

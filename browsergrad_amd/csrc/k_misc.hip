@@ -815,10 +815,4 @@ void launch_attention_masked_f32(bg_ctx* ctx, const float* q, const float* k, co
   launch_attention_generic(ctx, d, q, k, v, mask, mask_b, mask_h, o, false);
 }
 
-void launch_reduce_last(bg_ctx* ctx, const void* x, int dtype, void* y, int64_t rows,
-                        int64_t cols, int op) {
-  (void)ctx; (void)x; (void)dtype; (void)y; (void)rows; (void)cols; (void)op;
-  fail(BG_E_UNSUPPORTED, "reduce_last: routed through fused_ex");
-}
-
 }  // namespace bg

@@ -35,6 +35,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstdio>
 #include <cstring>
 #include <initializer_list>
 #include <set>
@@ -1345,6 +1346,13 @@ std::string inspect_plan(const char* json, const char* requests_json) {
     out += "]";
     if (s.op == "+PROGRAM") {
       out += ",\"n_ops\":" + std::to_string(s.prog.size()) + ",\"reduce\":" + std::to_string(s.reduce_op);
+      out += ",\"imms\":[";
+      for (size_t j = 0; j < s.imms.size(); ++j) {
+        char b[40];
+        std::snprintf(b, sizeof b, "%.17g", s.imms[j]);
+        out += (j ? "," : "") + std::string(b);
+      }
+      out += "]";
     } else if (s.op == "+LINEAR") {
       out += ",\"trans_b\":" + std::to_string(s.mm.trans_b) + ",\"round\":" + std::to_string(s.mm.round_f16) +
              ",\"act\":" + std::to_string(s.mm.act) + ",\"bias\":" + std::to_string(int(s.has_bias)) +

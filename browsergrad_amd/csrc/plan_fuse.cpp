@@ -226,34 +226,49 @@ void fuse_sdpa(Plan& plan) {
     Step* kt = g.prod_of(kt_id);
     if (!kt || !g.single(kt_id)) continue;
     int64_t k_id = 0;
+    // K's shape and dtype as the attention reads it.  A CAST(PERMUTE(K)) is
+    // only recorded here; it is re-pointed at K once every check has passed,
+    // so a plan the checks turn away is left exactly as it was.
+    std::vector<int64_t> ks;
+    std::string k_dtype;
+    int64_t perm_id = -1, perm_src = -1;
     if (kt->op == "PERMUTE" && axes_are(*kt, {0, 1, 3, 2})) {
       absorbed.push_back(kt_id);
       k_id = kt->inputs[0];
+      const Step* k = g.prod_of(k_id);
+      if (!k) continue;
+      ks = k->shape;
+      k_dtype = k->dtype;
     } else if (kt->op == "CAST" && is_narrow(kt->dtype)) {
       // CAST(PERMUTE(K)) -> the cast applies to K itself (a cast commutes
       // with a permutation); the attention reads K unpermuted.
-      Step* perm = g.prod_of(kt->inputs[0]);
+      const Step* perm = g.prod_of(kt->inputs[0]);
       if (!perm || perm->op != "PERMUTE" || !axes_are(*perm, {0, 1, 3, 2}) || !g.single(kt->inputs[0])) continue;
       const Step* src = g.prod_of(perm->inputs[0]);
       if (!src) continue;
-      // Re-point the cast at the unpermuted source: it now produces K.
-      kt->inputs = {perm->inputs[0]};
-      kt->shape = src->shape;
-      g.remove(perm->value_id);
+      perm_id = kt->inputs[0];
+      perm_src = perm->inputs[0];
       k_id = kt_id;
+      ks = src->shape;
+      k_dtype = kt->dtype;
     } else {
       continue;
     }
     const Step* q = g.prod_of(q_id);
-    const Step* k = g.prod_of(k_id);
     const Step* v = g.prod_of(v_id);
-    if (!q || !k || !v || q->shape.size() != 4 || k->shape.size() != 4 || v->shape.size() != 4) continue;
-    if (q->dtype != k->dtype || k->dtype != v->dtype || !is_narrow(q->dtype)) continue;
-    const auto &qs = q->shape, &ks = k->shape, &vs = v->shape;
+    if (!q || !v || q->shape.size() != 4 || ks.size() != 4 || v->shape.size() != 4) continue;
+    if (q->dtype != k_dtype || k_dtype != v->dtype || !is_narrow(q->dtype)) continue;
+    const auto &qs = q->shape, &vs = v->shape;
     if (qs[0] != ks[0] || qs[1] != ks[1] || ks != vs || qs[3] != ks[3] || o.shape[2] != qs[2] ||
         o.shape[3] != vs[3])
       continue;
     for (int64_t a : absorbed) g.remove(a);
+    if (perm_id >= 0) {
+      // Re-point the cast at the unpermuted source: it now produces K.
+      kt->inputs = {perm_src};
+      kt->shape = ks;
+      g.remove(perm_id);
+    }
     bg_attention_desc& d = o.att;
     d = bg_attention_desc{};
     d.batch = qs[0];
@@ -522,6 +537,7 @@ bool const_expr(const Graph& g, int64_t v, double& out, int depth = 0) {
     if (const_value(s, out)) {
       if (s->dtype == "float32") out = double(float(out));
       else if (s->dtype == "float16") out = double(float(_Float16(float(out))));
+      else if (s->dtype == "bfloat16") out = double(float(__bf16(float(out))));
       return true;
     }
     return false;

@@ -13,10 +13,8 @@ walker can treat them symbolically instead of uploading them:
 Their arrays are still produced on demand (get()) for consumers that need
 the bytes.
 
-GpuBufferTable mirrors _gpu_buffer_table.py:35-131 method for method:
-register (refuses double registration), get, has, detach, replace, release,
-release_all, upload (idempotent), stats {handles_alive, uploaded_bytes,
-registered_ids}.
+GpuBufferTable keeps the interface of _gpu_buffer_table.py:35-131 (method
+names, idempotent upload, stats keys) over its own bookkeeping.
 """
 from __future__ import annotations
 
@@ -106,77 +104,85 @@ class BufferTable:
 
 
 class GpuBufferTable:
-    """Per-session registry buffer_id -> bridge handle (the bridge owns memory)."""
+    """Device residency of one session's seed buffers.
 
-    __slots__ = ("_handles", "_bridge", "_total_uploaded_bytes", "_handles_alive")
+    Maps a buffer id to the bridge handle that holds its bytes on the GPU.
+    The bridge owns the memory; the table decides when a handle is minted
+    (the first ``upload`` of an id; later ones return the same handle) and
+    when it is given back (``release`` / ``replace`` / ``release_all``).
+    ``handles_alive`` and ``registered_ids`` are both the number of ids that
+    currently hold a handle; ``uploaded_bytes`` counts host bytes sent over
+    the table's life.  Interface of the reference's table
+    (``_gpu_buffer_table.py:35-131``): the method names, an idempotent
+    upload, a refused second ``register`` of one id, and the stats keys the
+    residency tests read.
+    """
+
+    __slots__ = ("_bridge", "_resident", "_sent")
 
     def __init__(self, bridge: Any) -> None:
         if bridge is None:
-            raise BufferTableError("GpuBufferTable requires a non-None bridge. Register a bridge first.")
-        self._handles: Dict[str, Any] = {}
+            raise BufferTableError("a GpuBufferTable needs a bridge to hold its device handles, got None")
         self._bridge = bridge
-        self._total_uploaded_bytes = 0
-        self._handles_alive = 0
+        self._resident: Dict[str, Any] = {}
+        self._sent = 0
 
     @property
     def bridge(self) -> Any:
         return self._bridge
 
-    def register(self, buffer_id: str, handle: Any) -> None:
-        if buffer_id in self._handles:
-            raise BufferTableError(
-                f"GpuBufferTable: buffer_id {buffer_id!r} is already registered with a handle. "
-                f"The realizer should consult .get() before re-uploading.")
-        self._handles[buffer_id] = handle
-        self._handles_alive += 1
-
-    def get(self, buffer_id: str) -> Optional[Any]:
-        return self._handles.get(buffer_id)
-
-    def has(self, buffer_id: str) -> bool:
-        return buffer_id in self._handles
-
-    def detach(self, buffer_id: str) -> Any:
-        if buffer_id not in self._handles:
-            raise BufferTableError(f"GpuBufferTable: cannot detach unknown buffer_id {buffer_id!r}")
-        self._handles_alive -= 1
-        return self._handles.pop(buffer_id)
-
-    def replace(self, buffer_id: str, handle: Any) -> None:
-        old = self._handles.pop(buffer_id, None)
-        if old is not None:
-            self._bridge.release(old)
-            self._handles_alive -= 1
-        self._handles[buffer_id] = handle
-        self._handles_alive += 1
-
-    def release(self, buffer_id: str) -> None:
-        handle = self._handles.pop(buffer_id, None)
-        if handle is None:
-            return
-        self._bridge.release(handle)
-        self._handles_alive -= 1
-
-    def release_all(self) -> None:
-        for buffer_id in list(self._handles):
-            self.release(buffer_id)
-
-    def upload(self, buffer_id: str, data: Any, shape: tuple, dtype: str) -> Any:
-        existing = self._handles.get(buffer_id)
-        if existing is not None:
-            return existing
-        handle = self._bridge.upload(data, shape, dtype)
-        self._handles[buffer_id] = handle
-        self._handles_alive += 1
-        self._total_uploaded_bytes += len(data) if isinstance(data, (bytes, bytearray)) else int(data.nbytes)
+    def _drop(self, buffer_id: str, give_back: bool) -> Any:
+        handle = self._resident.pop(buffer_id)
+        if give_back:
+            self._bridge.release(handle)
         return handle
 
+    def register(self, buffer_id: str, handle: Any) -> None:
+        """Record a handle minted elsewhere (a resident plan result)."""
+        held = self._resident.get(buffer_id)
+        if held is not None:
+            raise BufferTableError(
+                f"buffer {buffer_id!r} is resident already (handle {held!r}); "
+                "look it up with get() rather than registering a second handle")
+        self._resident[buffer_id] = handle
+
+    def get(self, buffer_id: str) -> Optional[Any]:
+        return self._resident.get(buffer_id)
+
+    def has(self, buffer_id: str) -> bool:
+        return buffer_id in self._resident
+
+    def detach(self, buffer_id: str) -> Any:
+        """Forget an id without releasing its handle; the caller owns it now."""
+        if buffer_id not in self._resident:
+            raise BufferTableError(f"buffer {buffer_id!r} holds no device handle, so there is nothing to detach")
+        return self._drop(buffer_id, give_back=False)
+
+    def replace(self, buffer_id: str, handle: Any) -> None:
+        if buffer_id in self._resident:
+            self._drop(buffer_id, give_back=True)
+        self._resident[buffer_id] = handle
+
+    def release(self, buffer_id: str) -> None:
+        """Give an id's handle back to the bridge; unknown ids are ignored."""
+        if buffer_id in self._resident:
+            self._drop(buffer_id, give_back=True)
+
+    def release_all(self) -> None:
+        while self._resident:
+            self._drop(next(iter(self._resident)), give_back=True)
+
+    def upload(self, buffer_id: str, data: Any, shape: tuple, dtype: str) -> Any:
+        """The id's handle, uploading ``data`` only the first time."""
+        held = self._resident.get(buffer_id)
+        if held is None:
+            held = self._resident[buffer_id] = self._bridge.upload(data, shape, dtype)
+            self._sent += len(data) if isinstance(data, (bytes, bytearray)) else int(data.nbytes)
+        return held
+
     def stats(self) -> Dict[str, int]:
-        return {
-            "handles_alive": self._handles_alive,
-            "uploaded_bytes": self._total_uploaded_bytes,
-            "registered_ids": len(self._handles),
-        }
+        n = len(self._resident)
+        return {"handles_alive": n, "uploaded_bytes": self._sent, "registered_ids": n}
 
 
 __all__ = ["BufferTable", "BufferTableError", "GpuBufferTable"]

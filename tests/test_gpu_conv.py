@@ -413,6 +413,40 @@ def test_conv_ring_wide_tiles_launched(bridge):
     assert wide(bwd, 64), bwd
 
 
+def test_conv_ring_64x128_tiles(bridge, monkeypatch):
+    """Fewer than 128 output positions (M = 64) against 256 output channels
+    per group and 256 groups make 512 tiles of 64 x 128: the ring kernel's
+    64 x 128 shape.  It is bit-identical to the register-staged kernel and
+    within the float64 bound."""
+    n, hw, cpg, opg, g, k = 1, (8, 8), 2, 256, 256, (3, 3)
+    ci, co = cpg * g, opg * g
+    rng = np.random.default_rng(64128)
+    x = rng.standard_normal((n, ci) + hw).astype(F32)
+    w = (rng.standard_normal((co, cpg) + k) / math.sqrt(cpg * 9)).astype(F32)
+    b = rng.standard_normal(co).astype(F32)
+    kw = dict(n=n, c_in=ci, c_out=co, in_size=hw, out_size=hw, k=k, stride=(1, 1), pad=(1, 1), dilation=(1, 1),
+              groups=g)
+    monkeypatch.setenv("BG_CONV_RING", "1")
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        y = conv_ex(bridge, "forward", x, w, b, **kw)
+        names = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    assert any("conv_fwd_ring_kernel" in t and ("ILi64ELi128ELi4E" in t or "<64, 128, 4>" in t) for t in names), names
+    monkeypatch.setenv("BG_CONV_RING", "0")
+    y0 = conv_ex(bridge, "forward", x, w, b, **kw)
+    assert np.array_equal(y, y0)
+    xt = torch.tensor(x, dtype=torch.float64)
+    wt = torch.tensor(w, dtype=torch.float64)
+    bt = torch.tensor(b, dtype=torch.float64)
+    y64 = F.conv2d(xt, wt, bt, padding=1, groups=g).numpy()
+    mass = F.conv2d(xt.abs(), wt.abs(), bt.abs(), padding=1, groups=g).numpy()
+    err = np.abs(y - y64)
+    assert np.all(err <= _bound(y64, mass, cpg * 9)), float(np.max(err / _bound(y64, mass, cpg * 9)))
+
+
 @pytest.mark.parametrize("shape", [(4, 16, 28, 28), (3, 5, 7, 7), (2, 3, 4, 300)])
 def test_bias_gradient_float4_and_scalar_rows(bridge, shape):
     """Spatial sizes that are multiples of 4 (784, 1200) take the float4 row

@@ -193,6 +193,23 @@ def test_plan_route_configs(bridge, table, name, scale, kw, tol):
         assert counts.get("fused_elementwise", 0) == 1, counts  # the GELU program
 
 
+@pytest.mark.parametrize("shapes", [((1, 2, 5, 4), (1, 2, 3, 4), (1, 2, 3, 6)),
+                                    ((1, 2, 5, 4), (1, 1, 4, 4), (1, 1, 4, 4))],
+                         ids=["dv_ne_dk", "broadcast_k_heads_sk_eq_d"])
+def test_plan_route_unfusable_amp_sdpa(bridge, table, rng, shapes):
+    """Autocast SDPA graphs the attention kernel does not take (value depth
+    != key depth; one key head against two query heads with sk == d): the
+    plan route runs their steps unfused and matches the graph oracle."""
+    from browsergrad_amd.jit.tensor import autocast, scaled_dot_product_attention
+    s = Session()
+    q, k, v = (s.from_numpy(rng.standard_normal(sh, dtype=np.float32)) for sh in shapes)
+    with autocast("float16"):
+        y = scaled_dot_product_attention(q, k, v)
+    ref = G.evaluate(y.uop, s.buffers)
+    out = realize_tensor_plan_hip(y.uop, s.buffers, table)
+    _check(out, ref, 2e-2)
+
+
 def test_plan_route_semantic_and_resident(bridge, table):
     s, y = configs.c1(scale=1.0)
     ref = G.evaluate(y.uop, s.buffers)

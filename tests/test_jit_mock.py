@@ -122,3 +122,36 @@ def test_residual_epilogue_rides_on_the_gemm():
     fused = realize_hip(y.uop, s.buffers, GpuBufferTable(br))
     plain = realize_hip(y.uop, s.buffers, GpuBufferTable(MockHipBridge()), hip_rewrites=False)
     _check(fused, plain, 2e-2)
+
+
+def test_gpu_buffer_table_bookkeeping():
+    """The table's own contract (_gpu_buffer_table.py:35-131): idempotent
+    upload, refused second register, detach hands the handle over without a
+    release, replace/release give handles back, stats stay consistent."""
+    from browsergrad_amd.jit.buffers import BufferTableError
+    br = MockHipBridge()
+    t = GpuBufferTable(br)
+    a = np.arange(6, dtype=np.float32)
+    h1 = t.upload("a", a, (6,), "float32")
+    assert t.upload("a", a, (6,), "float32") == h1  # no second upload
+    assert t.stats() == {"handles_alive": 1, "uploaded_bytes": 24, "registered_ids": 1}
+    with pytest.raises(BufferTableError, match="resident already"):
+        t.register("a", h1)
+    hb = br.upload(a, (6,), "float32")
+    t.register("b", hb)
+    assert t.has("b") and t.get("b") == hb and t.get("zzz") is None
+    assert t.detach("b") == hb and not t.has("b")
+    assert br.aliveHandleCount() == 2  # detach does not release
+    with pytest.raises(BufferTableError, match="nothing to detach"):
+        t.detach("b")
+    br.release(hb)
+    hc = br.upload(a, (6,), "float32")
+    t.replace("a", hc)  # h1 is released
+    assert br.aliveHandleCount() == 1 and t.get("a") == hc
+    t.release("missing")  # ignored
+    t.upload("d", a.tobytes(), (6,), "float32")
+    assert t.stats() == {"handles_alive": 2, "uploaded_bytes": 48, "registered_ids": 2}
+    t.release_all()
+    assert br.aliveHandleCount() == 0 and t.stats()["handles_alive"] == 0
+    with pytest.raises(BufferTableError, match="needs a bridge"):
+        GpuBufferTable(None)

@@ -124,3 +124,68 @@ def test_internal_opcodes_are_not_accepted_from_the_wire():
 def test_malformed_plans_are_refused(text, msg):
     with pytest.raises(KernelError, match=msg):
         inspect(text)
+
+
+def _amp_sdpa(qshape, kshape, vshape, seed=0):
+    """An autocast SDPA graph (CAST(PERMUTE(K)) feeds Q K^T) of the given shapes."""
+    from browsergrad_amd.jit.tensor import Session, autocast, scaled_dot_product_attention
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    s = Session()
+    q, k, v = (s.from_numpy(rng.standard_normal(sh, dtype=np.float32)) for sh in (qshape, kshape, vshape))
+    with autocast("float16"):
+        y = scaled_dot_product_attention(q, k, v)
+    return s, y
+
+
+def _sdpa_steps_left_alone(y, s):
+    plan, req, rj = _plan_submission(y.uop, s.buffers)
+    out = inspect(plan, rj or None)
+    by_id = {st["value_id"]: st for st in out["steps"]}
+    ops = [st["op"] for st in out["steps"]]
+    assert "+ATTENTION" not in ops
+    # The K^T cast still reads the permuted K, and the permutation is still there.
+    perms = [st for st in out["steps"] if st["op"] == "PERMUTE"]
+    mm = [st for st in out["steps"] if st["op"] == "MATMUL"]
+    assert len(mm) == 2, ops
+    qk = mm[0]  # the first MATMUL in plan order is Q K^T
+    kt = by_id[qk["inputs"][1]]
+    assert kt["op"] == "CAST", kt
+    src = by_id[kt["inputs"][0]]
+    assert src["op"] == "PERMUTE" and src in perms, (kt, src)
+    return plan, out
+
+
+def test_sdpa_refused_when_value_depth_differs_leaves_plan_unchanged():
+    # dv = 6 != dk = 4: not an attention the kernel runs.  Before the fix
+    # the CAST(PERMUTE(K)) was already re-pointed at K when the shape check
+    # turned the group away, so Q K^T read K unpermuted.
+    s, y = _amp_sdpa((1, 2, 5, 4), (1, 2, 3, 4), (1, 2, 3, 6))
+    _sdpa_steps_left_alone(y, s)
+
+
+def test_sdpa_refused_for_broadcast_key_heads_with_sk_equal_d():
+    # K with one head against two query heads, sk == d == 4: a wrongly
+    # re-pointed cast would still make a shape-valid (and silently wrong)
+    # Q K^T, so the plan itself must be unchanged.
+    s, y = _amp_sdpa((1, 2, 5, 4), (1, 1, 4, 4), (1, 1, 4, 4))
+    _sdpa_steps_left_alone(y, s)
+
+
+def test_bf16_scalar_constant_is_inlined_rounded():
+    # One bfloat16 CONST read by two fused groups: each program inlines it as
+    # an immediate, which must be the value the unfused executor stores
+    # (rounded to bfloat16), not the wire's double.
+    c = 0.1  # bf16(0.1) = 0.10009765625
+    steps = [_st(0, "BUFFER", [], [4, 8], dtype="bfloat16"),
+             _st(1, "CONST", [], [1], dtype="bfloat16", arg={"value": c}),
+             _st(2, "MUL", [0, 1], [4, 8], dtype="bfloat16"),
+             _st(3, "REDUCE", [2], [4], dtype="bfloat16", arg={"op": "sum", "axis": 1, "keepdims": False}),
+             _st(4, "ADD", [0, 1], [4, 8], dtype="bfloat16"),
+             _st(5, "REDUCE", [4], [4], dtype="bfloat16", arg={"op": "sum", "axis": 1, "keepdims": False}),
+             _st(6, "ADD", [3, 5], [4], dtype="bfloat16")]
+    out = inspect(_plan(steps, 6))
+    progs = [st for st in out["steps"] if st["op"] == "+PROGRAM"]
+    assert progs, [st["op"] for st in out["steps"]]
+    imms = [v for st in progs for v in st.get("imms", [])]
+    assert imms and all(v == 0.10009765625 for v in imms), imms

@@ -340,7 +340,7 @@ def _walk_timed(br, uop, buffers, steps, warmup, recast=False):
 
     def step():
         if recast:
-            for key in [k for k in gbt._handles if "::" in k]:
+            for key in [k for k in gbt.ids() if "::" in k]:
                 gbt.release(key)
         br.release(walk(g, buffers, gbt, materialize=False))
 

@@ -152,6 +152,10 @@ class GpuBufferTable:
     def has(self, buffer_id: str) -> bool:
         return buffer_id in self._resident
 
+    def ids(self) -> list:
+        """The buffer ids that currently hold a handle."""
+        return list(self._resident)
+
     def detach(self, buffer_id: str) -> Any:
         """Forget an id without releasing its handle; the caller owns it now."""
         if buffer_id not in self._resident:

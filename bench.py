@@ -438,7 +438,11 @@ def bench_c3_e2e(br, steps, warmup):
 
 # --------------------------------------------------------------------------- C4
 
-def bench_c4(br, steps, warmup):
+def bench_c4(br, steps, warmup, round_scores=False):
+    """C4 causal attention.  ``round_scores`` selects the kernel form that
+    rounds each score S = Q K^T to f16 before scaling, as the reference's
+    AMP graph stores it (_realize.py:395-412); parity is then checked against
+    the oracle's rounding steps, not only its tolerance."""
     B, H, S, D = 8, 16, 2048, 64
     rng = np.random.default_rng(4)
     q, k, v = (rng.standard_normal((B, H, S, D), dtype=np.float32).astype(np.float16) for _ in range(3))
@@ -447,7 +451,7 @@ def bench_c4(br, steps, warmup):
 
     def run():
         return br.attention_ex(hq, hk, hv, batch=B, heads=H, sq=S, sk=S, d=D, scale=scale, causal=True,
-                               in_dtype="float16", out_dtype="float16", round_scores=False)
+                               in_dtype="float16", out_dtype="float16", round_scores=round_scores)
 
     def step():
         br.release(run())
@@ -742,6 +746,8 @@ def main() -> int:
         log("c4 causal attention B8 H16 S2048 D64 fp16")
         extra["c4_attention_fp16"] = bench_c4(br, max(10, a.steps // 2), a.warmup)
         log(f"  {extra['c4_attention_fp16']}")
+        extra["c4_attention_fp16_exact_rounding"] = bench_c4(br, max(10, a.steps // 2), a.warmup, round_scores=True)
+        log(f"  {extra['c4_attention_fp16_exact_rounding']}")
     if "c5" in only:
         log("c5 gpt-2 block B8 S1024 E768 H12 autocast f16 (walker)")
         extra["c5_gpt2_block_fp16"] = bench_c5(br, max(10, a.steps // 5), max(3, a.warmup // 2))

@@ -956,6 +956,31 @@ __global__ void __launch_bounds__(kFa2NW * 64, 2) fa6_fwd_kernel(Fa2Args P, uint
 // a causal or length mask, then the remaining (diagonal) tiles with the
 // mask test.  Ring, copies and barriers are v6's.
 
+// ROUND_S form of fa6_exp: x holds raw scores S = Q K^T (f32 accumulate);
+// each is rounded to the input dtype (the reference's AMP matmul output),
+// then scaled into the log2 domain against the reference max:
+// P = exp2(16-bit(S) * scale * log2 e - m).  Returns the f32 row sum.
+template <bool BF16>
+__device__ __forceinline__ float fa7_exp_round(const float16v& x, float sl2, float negm, fa_u4 (&pf)[2]) {
+  float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm) {
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = mm * 8 + 2 * j;
+      const uint32_t sr = fa2_pack<BF16>(x[e], x[e + 1]);
+      const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(fa2_lo<BF16>(sr), sl2, negm));
+      const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(fa2_hi<BF16>(sr), sl2, negm));
+      l0 += e0;
+      l1 += e1;
+      pk[j] = fa2_pack<BF16>(e0, e1);
+    }
+    pf[mm] = fa_u4{pk[0], pk[1], pk[2], pk[3]};
+  }
+  return l0 + l1;
+}
+
 // O = acc / l for this lane's query; O^T layout: register e of acc[db] holds
 // d = 32 db + 8 (e / 4) + 4 hi + e % 4.
 __device__ __forceinline__ void fa7_store(const Fa2Args& P, int b, int h, int qi, const float16v (&acc)[2],
@@ -1002,7 +1027,7 @@ __device__ __forceinline__ float fa7_round(float x) {
   else return static_cast<float>(static_cast<_Float16>(x));
 }
 
-template <bool BF16, bool CAUSAL>
+template <bool BF16, bool CAUSAL, bool ROUND_S>
 __device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0w) {
   const int lane = threadIdx.x & 63;
   const uint16_t* Qp = P.q + b * P.q_sb + h * P.q_sh;
@@ -1024,10 +1049,16 @@ __device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0
         for (int d = 0; d < 64; d += 2) {
           const uint32_t qw = *reinterpret_cast<const uint32_t*>(qrow + d);
           const uint32_t kw = *reinterpret_cast<const uint32_t*>(krow + d);
-          acc += fa7_round<BF16>(fa2_lo<BF16>(qw) * P.sl2) * fa2_lo<BF16>(kw);
-          acc += fa7_round<BF16>(fa2_hi<BF16>(qw) * P.sl2) * fa2_hi<BF16>(kw);
+          if constexpr (ROUND_S) {
+            acc += fa2_lo<BF16>(qw) * fa2_lo<BF16>(kw);
+            acc += fa2_hi<BF16>(qw) * fa2_hi<BF16>(kw);
+          } else {
+            acc += fa7_round<BF16>(fa2_lo<BF16>(qw) * P.sl2) * fa2_lo<BF16>(kw);
+            acc += fa7_round<BF16>(fa2_hi<BF16>(qw) * P.sl2) * fa2_hi<BF16>(kw);
+          }
         }
-        sc = acc;
+        // ROUND_S: the score rounds to the input dtype before scaling.
+        sc = ROUND_S ? fa7_round<BF16>(acc) * P.sl2 : acc;
       }
       const float m_new = fmaxf(m_run, fa7_wave_max(sc));
       const float alpha = m_run == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -1090,7 +1121,14 @@ __device__ __forceinline__ void fa7_block_of(int64_t lid, int bh, int nqb, bool 
 // (48 KB of LDS each), for grids too small to fill the CUs evenly with
 // 256-query blocks (a causal S = 1024 head has 4 such blocks of 4, 8, 12 and
 // 16 tiles; 8 blocks of 128 queries fill three workgroup slots per CU).
-template <bool BF16, bool CAUSAL, int NW, int RING>
+//
+// ROUND_S follows the reference's AMP rounding of the scores
+// (_realize.py:395-412: the f16 matmul's output is stored in f16, then
+// scaled in f32): Q is used as stored, the S accumulators start from zero,
+// and each score is rounded to the input dtype before it is scaled and
+// shifted by the reference max (one FMA per score; the default form folds
+// the scale into Q and the shift into the MFMA's accumulator seed instead).
+template <bool BF16, bool CAUSAL, int NW, int RING, bool ROUND_S>
 __global__ void __launch_bounds__(NW * 64, NW == 8 ? 4 : 3)  // the LDS-bound occupancy
 fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
   static_assert((NW == 8 && RING == 4) || (NW == 4 && RING == 3), "instantiated shapes");
@@ -1176,30 +1214,37 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
     issue(2);
     issue(3);
   }
+  if constexpr (!ROUND_S) {
 #pragma unroll
-  for (int dc = 0; dc < 4; ++dc)
+    for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qf[dc][i] = fa6_scale2<BF16>(qf[dc][i], sl2);
+      for (int i = 0; i < 4; ++i) qf[dc][i] = fa6_scale2<BF16>(qf[dc][i], sl2);
+  }
 
   const Fa6Offs offs;
+  float16v zero;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) zero[e] = 0.f;
   // Reference max: exact maximum over this query's keys 0..31 (key 0 is
   // always visible), the same for the wavefront's two lanes of a query.
+  // Default form: -m seeds the S accumulators (mneg).  ROUND_S: the scores
+  // start from zero and negm is added by the per-score FMA.
   float16v mneg;
+  float negm;
   {
-    float16v zero;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) zero[e] = 0.f;
     float16v x = fa6_scores_half<BF16>(kring, offs, qf, zero, 0);
     float mt = -INFINITY;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int kj = 8 * (e >> 2) + 4 * hi + (e & 3);
-      if (!(kj >= P.Sk || (CAUSAL && kj > qi))) mt = fmaxf(mt, x[e]);
+      const float xe = ROUND_S ? fa7_round<BF16>(x[e]) * sl2 : x[e];
+      if (!(kj >= P.Sk || (CAUSAL && kj > qi))) mt = fmaxf(mt, xe);
     }
     mt = fmaxf(mt, fa2_xor32(mt));
     const float m_use = mt == -INFINITY ? 0.f : mt;
+    negm = -m_use;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) mneg[e] = -m_use;
+    for (int e = 0; e < 16; ++e) mneg[e] = ROUND_S ? 0.f : -m_use;
   }
 
   float16v acc[2];
@@ -1231,7 +1276,8 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
     for (int hh = 0; hh < 2; ++hh) {
       const float16v x = fa6_scores_half<BF16>(kt, offs, qf, mneg, hh);
       fa_u4 pf[2];
-      l_run += fa6_exp<BF16, false>(x, 0.f, pf);
+      if constexpr (ROUND_S) l_run += fa7_exp_round<BF16>(x, sl2, negm, pf);
+      else l_run += fa6_exp<BF16, false>(x, 0.f, pf);
       fa6_pv_half<BF16>(vt, offs, pf, acc, hh);
     }
   }
@@ -1269,7 +1315,8 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
           }
         }
         fa_u4 pf[2];
-        l_run += fa6_exp<BF16, false>(x, 0.f, pf);
+        if constexpr (ROUND_S) l_run += fa7_exp_round<BF16>(x, sl2, negm, pf);
+        else l_run += fa6_exp<BF16, false>(x, 0.f, pf);
         fa6_pv_half<BF16>(vt, offs, pf, acc, hh);
       }
     }
@@ -1283,7 +1330,7 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) bad |= !(fabsf(acc[db][e]) <= 3.0e38f);
   if (__any(bad)) {
-    fa7_exact<BF16, CAUSAL>(P, b, h, q0w);
+    fa7_exact<BF16, CAUSAL, ROUND_S>(P, b, h, q0w);
     return;
   }
   fa7_store(P, b, h, qi, acc, l_run);
@@ -1292,7 +1339,7 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
 // 256-query workgroups when they give at least three per CU's two slots
 // (C4: 128 heads x 8 blocks); 128-query workgroups otherwise (C5: 96 heads
 // x 4 blocks of 256 would leave a 2:1 imbalance between CUs).
-template <bool BF16, bool CAUSAL>
+template <bool BF16, bool CAUSAL, bool ROUND_S>
 void launch_fa7(bg_ctx* ctx, const Fa2Args& A0, int bh, uint32_t kb, uint32_t vb) {
   Fa2Args A = A0;
   const int64_t big = int64_t(bh) * ((A.Sq + 255) / 256);
@@ -1302,11 +1349,11 @@ void launch_fa7(bg_ctx* ctx, const Fa2Args& A0, int bh, uint32_t kb, uint32_t vb
   const bool want128 = force && std::strcmp(force, "128") == 0;
   if (want256 || (!want128 && big >= 768) || (A.Sq + 127) / 128 > 65535) {
     A.n_qblocks = (A.Sq + 255) / 256;
-    bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 8, 4>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
+    bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 8, 4, ROUND_S>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
                  dim3(8 * 64), 0, A, kb, vb);
   } else {
     A.n_qblocks = (A.Sq + 127) / 128;
-    bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 4, 3>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
+    bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 4, 3, ROUND_S>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
                  dim3(4 * 64), 0, A, kb, vb);
   }
 }
@@ -1402,11 +1449,13 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     const uint32_t kb = uint32_t(k_head), vb = uint32_t(v_head);
     Profile prof(ctx, bf ? "attention_bf16" : "attention_f16", bytes, flops);
     const int ver = attn_version();
-    const bool fast = ver != 2 && !r && (bf || A.sl2 <= 1.0f);
+    // fa7 with the scale folded into Q needs |Q * scale * log2 e| <= |Q| for
+    // f16 (no overflow); its ROUND_S form scales each rounded score instead.
+    const bool fast = ver != 2 && (r || bf || A.sl2 <= 1.0f);
 #define BG_FA2(B_, C_, R_)                                                                     \
-  (fast && !R_ ? (ver == 6 ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb)               \
-                           : launch_fa7<B_, C_>(ctx, A, bh, kb, vb))                         \
-               : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
+  (fast ? (ver == 6 && !R_ ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb)               \
+                           : launch_fa7<B_, C_, R_>(ctx, A, bh, kb, vb))                     \
+        : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
     if (bf) {
       if (c) { if (r) BG_FA2(true, true, true); else BG_FA2(true, true, false); }
       else { if (r) BG_FA2(true, false, true); else BG_FA2(true, false, false); }

@@ -520,11 +520,23 @@ def test_attention_round_scores_is_honoured(bridge, dtype):
         ref = O.bf16_bits_to_f32(O.sdpa_bf16(*ts, scale, False))
         hs = [up(bridge, t, "bfloat16") for t in ts]
     assert np.all(ref == 0.0)
-    out = {}
-    for rs in (True, False):
-        ho = bridge.attention_ex(*hs, batch=1, heads=1, sq=1, sk=sk, d=d, scale=scale, causal=False,
-                                 in_dtype=dtype, out_dtype="float32", round_scores=rs)
-        out[rs] = bridge.to_numpy(ho)
+    out, names = {}, {}
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        for rs in (True, False):
+            ho = bridge.attention_ex(*hs, batch=1, heads=1, sq=1, sk=sk, d=d, scale=scale, causal=False,
+                                     in_dtype=dtype, out_dtype="float32", round_scores=rs)
+            out[rs] = bridge.to_numpy(ho)
+            names[rs] = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    # Both forms run the fast kernel; its last template argument is ROUND_S.
+    def fa7(ts, rs):  # mangled (...ELb1EEEvNS_7Fa2Args...) or demangled (..., true>(...)
+        flag = ("ELb1EEEv", ", true>(") if rs else ("ELb0EEEv", ", false>(")
+        return any("fa7_fwd_kernel" in t and (flag[0] in t or flag[1] in t) for t in ts)
+    assert fa7(names[True], True), names[True]
+    assert fa7(names[False], False), names[False]
     assert np.all(out[True] == 0.0), out[True][..., :4]
     assert np.all(out[False] < 0.0), out[False][..., :4]
     assert O.within(out[False], ref, TOL16).all()

@@ -477,6 +477,42 @@ def bench_c4(br, steps, warmup, round_scores=False):
     return out
 
 
+def bench_attention_f32(br, steps, warmup):
+    """The C4 shape (B8 H16 S2048 D64, causal) in float32: the bridge's own
+    attention dtype (realizer.ts:1122-1151), on the f32 MFMA kernel, against
+    the fp32 matrix peak."""
+    B, H, S, D = 8, 16, 2048, 64
+    rng = np.random.default_rng(44)
+    q, k, v = (rng.standard_normal((B, H, S, D), dtype=np.float32) for _ in range(3))
+    hq, hk, hv = (br.upload(t, t.shape, "float32") for t in (q, k, v))
+    scale = 1.0 / np.sqrt(D)
+
+    def run():
+        return br.attention_ex(hq, hk, hv, batch=B, heads=H, sq=S, sk=S, d=D, scale=scale, causal=True,
+                               in_dtype="float32", out_dtype="float32")
+
+    def step():
+        br.release(run())
+
+    wall_ms, k_ms, _ = timed(br, step, steps, warmup, "attention_f32")
+    flops = 4.0 * B * H * D * S * (S + 1) / 2
+    out = {"wall_ms": wall_ms, "kernel_ms": k_ms,
+           "tflops_kernel": flops / (k_ms * 1e-3) / 1e12,
+           "tflops_wall": flops / (wall_ms * 1e-3) / 1e12}
+    out["frac_of_fp32_peak"] = out["tflops_kernel"] / FP32_PEAK_TFLOPS
+    from oracle import ops as O  # checker only: two (b, h) slices
+    h = run()
+    y = br.to_numpy(h)
+    br.release(h)
+    picks = [(0, 0), (7, 15)]
+    ys = np.stack([y[b, hh] for b, hh in picks])
+    refs = np.stack([O.attention_f64(q[b, hh], k[b, hh], v[b, hh], scale, causal=True) for b, hh in picks])
+    out["parity"] = O.report(ys, refs, 1e-4)
+    for t in (hq, hk, hv):
+        br.release(t)
+    return out
+
+
 # --------------------------------------------------------------------------- C1
 
 def bench_c1(br, steps, warmup):
@@ -748,6 +784,9 @@ def main() -> int:
         log(f"  {extra['c4_attention_fp16']}")
         extra["c4_attention_fp16_exact_rounding"] = bench_c4(br, max(10, a.steps // 2), a.warmup, round_scores=True)
         log(f"  {extra['c4_attention_fp16_exact_rounding']}")
+        log("c4 shape in float32 (the bridge's attention dtype)")
+        extra["attention_f32_b8h16s2048d64_causal"] = bench_attention_f32(br, max(5, a.steps // 10), 2)
+        log(f"  {extra['attention_f32_b8h16s2048d64_causal']}")
     if "c5" in only:
         log("c5 gpt-2 block B8 S1024 E768 H12 autocast f16 (walker)")
         extra["c5_gpt2_block_fp16"] = bench_c5(br, max(10, a.steps // 5), max(3, a.warmup // 2))

@@ -108,6 +108,24 @@ class AttentionDesc(C.Structure):
     ]
 
 
+BG_PLAN_MAX_LAUNCHES = 4
+
+
+class LaunchPlanEntry(C.Structure):
+    _fields_ = [
+        ("family", C.c_char * 48), ("n_targs", C.c_int32), ("targs", C.c_int32 * 8), ("block", C.c_int32 * 3),
+        ("grid", C.c_int64 * 3),
+    ]
+
+
+class LaunchPlan(C.Structure):
+    _fields_ = [
+        ("n_launches", C.c_int32), ("tile_m", C.c_int32), ("tile_n", C.c_int32), ("tile_k", C.c_int32),
+        ("k_slices", C.c_int32), ("reserved", C.c_int32), ("lds_bytes", C.c_int64), ("workspace_bytes", C.c_int64),
+        ("launch", LaunchPlanEntry * BG_PLAN_MAX_LAUNCHES),
+    ]
+
+
 class Snapshot(C.Structure):
     _fields_ = [
         ("current_owned_bytes", C.c_int64), ("peak_owned_bytes", C.c_int64),
@@ -207,6 +225,9 @@ SIGNATURES = {
                                               C.c_void_p, C.c_size_t, PH]),
     "bg_softmax_last": (C.c_int, [ctx_p, handle_t, C.c_int64, C.c_int64, C.c_int, PH]),
     "bg_device_ptr": (C.c_int, [ctx_p, handle_t, C.POINTER(C.c_void_p)]),
+    "bg_matmul_launch_plan": (C.c_int, [C.POINTER(MatmulDesc), C.POINTER(LaunchPlan), C.c_char_p, C.c_size_t]),
+    "bg_attention_launch_plan": (C.c_int, [C.POINTER(AttentionDesc), C.POINTER(LaunchPlan), C.c_char_p,
+                                           C.c_size_t]),
     "bg_stream": (C.c_int, [ctx_p, C.POINTER(C.c_void_p)]),
 }
 

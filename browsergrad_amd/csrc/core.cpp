@@ -280,6 +280,28 @@ static void resolve_profiles(bg_ctx* ctx) {
 
 using namespace bg;
 
+// Context-free entries: the refusal message goes to err.
+template <class F>
+static int no_ctx_call(char* err, size_t err_cap, F&& f) {
+  std::string text;
+  int rc = BG_OK;
+  try {
+    f();
+  } catch (const bg::Error& e) {
+    rc = e.code;
+    text = e.what();
+  } catch (const std::exception& e) {
+    rc = BG_E_INVALID;
+    text = e.what();
+  }
+  if (err && err_cap > 0) {
+    const size_t n = std::min(err_cap - 1, text.size());
+    std::memcpy(err, text.data(), n);
+    err[n] = 0;
+  }
+  return rc;
+}
+
 extern "C" {
 
 const char* bg_version(void) { return "bghip 0.1 gfx950"; }
@@ -1010,6 +1032,20 @@ int bg_attention_ex(bg_ctx* ctx, const bg_attention_desc* desc, bg_handle* out) 
   }
   *out = o;
   BG_API_END
+}
+
+int bg_matmul_launch_plan(const bg_matmul_desc* desc, bg_launch_plan* out, char* err, size_t err_cap) {
+  return no_ctx_call(err, err_cap, [&] {
+    if (!desc || !out) fail(BG_E_INVALID, "matmul_launch_plan: NULL argument");
+    plan_matmul(*desc, *out);
+  });
+}
+
+int bg_attention_launch_plan(const bg_attention_desc* desc, bg_launch_plan* out, char* err, size_t err_cap) {
+  return no_ctx_call(err, err_cap, [&] {
+    if (!desc || !out) fail(BG_E_INVALID, "attention_launch_plan: NULL argument");
+    plan_attention(*desc, *out);
+  });
 }
 
 int bg_flash_attention(bg_ctx* ctx, bg_handle q, bg_handle k, bg_handle v,

@@ -236,6 +236,21 @@ void noalloc_setup(bg_ctx* ctx);
 void launch_attention(bg_ctx* ctx, const bg_attention_desc& d,
                       const Record& q, const Record& k, const Record& v,
                       Record& out);
+// f32 attention on MFMA (k_attn32.hip), head dim 1..64: q/k/v/o point at the
+// operands' first elements; mask is NULL or f32 with the given strides.
+// Launch shape of the f32 GEMM (k_gemm.hip), shared with the launch-plan query.
+struct Gemm32Shape {
+  int tiles_m = 0, tiles_n = 0;
+  bool aligned = false;
+  int64_t used = 1;     // split-K slices launched (1: no split)
+  int64_t k_chunk = 0;  // K elements per slice (0: no split)
+};
+Gemm32Shape gemm32_shape(const bg_matmul_desc& d, bool ptrs_aligned);
+void plan_matmul(const bg_matmul_desc& d, bg_launch_plan& out);
+void plan_attention(const bg_attention_desc& d, bg_launch_plan& out);
+bool fa32_supported(const bg_attention_desc& d);
+void launch_fa32(bg_ctx* ctx, const bg_attention_desc& d, const float* q, const float* k, const float* v,
+                 const float* mask, int64_t m_sb, int64_t m_sh, int64_t m_ss, void* o);
 void launch_attention_generic(bg_ctx* ctx, const bg_attention_desc& d, const void* q,
                               const void* k, const void* v, const float* mask, int64_t mask_sb,
                               int64_t mask_sh, void* o, bool two_pass);

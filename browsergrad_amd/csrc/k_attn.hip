@@ -1411,6 +1411,12 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
                        d.v_sb % 4 == 0 && d.v_sh % 4 == 0 && d.o_sb % 4 == 0 && d.o_sh % 4 == 0 &&
                        al(qp, 16) && al(kp, 16) && al(vp, 8) && al(out.ptr(), 16) &&
                        d.batch * d.heads <= 0x7fffffff && sq <= (1 << 30) && sk <= (1 << 30);
+  if (d.in_dtype == BG_F32 && fa32_supported(d)) {
+    Profile prof(ctx, "attention_f32", bytes, flops);
+    launch_fa32(ctx, d, reinterpret_cast<const float*>(qp), reinterpret_cast<const float*>(kp),
+                reinterpret_cast<const float*>(vp), nullptr, 0, 0, 0, out.ptr());
+    return;
+  }
   if (!mfma_ok) {
     Profile prof(ctx, "attention_generic", bytes, flops);
     launch_attention_generic(ctx, d, qp, kp, vp, nullptr, 0, 0, out.ptr(),

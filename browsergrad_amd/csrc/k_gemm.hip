@@ -30,6 +30,7 @@
 // f32 path, gemm32_kernel: v_mfma_f32_32x32x2_f32 with k-major LDS tiles
 // (NN and NT), the same staged epilogue.
 #include <algorithm>
+#include <cstdio>
 
 #include <cstdlib>
 #include <string>
@@ -867,6 +868,28 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch, int act) {
 
 namespace bg {
 
+// Launch shape of the f32 GEMM, shared by run_gemm and the launch-plan
+// query.  ptrs_aligned: A and B (offsets applied) start on 16 bytes.
+// Few output tiles and a long K (C1's 64 x 784 x 128): one workgroup would
+// walk K alone, one global-memory latency per 16-wide k step, so K is split
+// over blockIdx.y (two k steps per slice) into f32 partials that one
+// summing pass adds in slice order, applying the epilogue.
+Gemm32Shape gemm32_shape(const bg_matmul_desc& d, bool ptrs_aligned) {
+  Gemm32Shape g;
+  g.tiles_m = int((d.m + 127) / 128);
+  g.tiles_n = int((d.n + 127) / 128);
+  g.aligned = ptrs_aligned && d.lda % 4 == 0 && d.ldb % 4 == 0 && d.k % 4 == 0 && (d.trans_b || d.n % 4 == 0) &&
+              d.stride_a % 4 == 0 && d.stride_b % 4 == 0;
+  const int64_t nk = (d.k + BK32 - 1) / BK32;
+  const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
+  if (d.batch == 1 && tiles <= 16 && nk >= 8) {
+    const int64_t splits = std::min<int64_t>(64, (nk + 1) / 2);
+    g.k_chunk = ((nk + splits - 1) / splits) * BK32;
+    g.used = (d.k + g.k_chunk - 1) / g.k_chunk;
+  }
+  return g;
+}
+
 // GEMM launch with C described by (c, ldc, stride_c, out_dtype, act).
 // True when run_gemm would pick a kernel whose epilogue applies GELU (the
 // direct-to-LDS kernel with 128-wide wavefront tiles).
@@ -919,22 +942,15 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const 
                         d.batch * d.m * d.n * dtype_size(out_dtype);
 
   if (d.in_dtype == BG_F32) {
-    P.tiles_m = int((d.m + 127) / 128);
-    P.tiles_n = int((d.n + 127) / 128);
-    const bool aligned = aligned_to(P.A, 16) && aligned_to(P.B, 16) && d.lda % 4 == 0 &&
-                         d.ldb % 4 == 0 && d.k % 4 == 0 && (d.trans_b || d.n % 4 == 0) &&
-                         d.stride_a % 4 == 0 && d.stride_b % 4 == 0;
+    const Gemm32Shape g = gemm32_shape(d, aligned_to(P.A, 16) && aligned_to(P.B, 16));
+    P.tiles_m = g.tiles_m;
+    P.tiles_n = g.tiles_n;
+    const bool aligned = g.aligned;
     Profile prof(ctx, "gemm_f32", bytes, flops);
-    // Few output tiles and a long K (C1's 64 x 784 x 128): one workgroup
-    // would walk K alone, one global-memory latency per 16-wide k step.
-    // Split K over blockIdx.y (two k steps per slice), write f32
-    // partials, and finish with one summing pass that applies the epilogue.
-    const int64_t nk = (d.k + BK32 - 1) / BK32;
     const int64_t tiles = int64_t(P.tiles_m) * P.tiles_n;
-    if (d.batch == 1 && tiles <= 16 && nk >= 8) {
-      const int64_t splits = std::min<int64_t>(64, (nk + 1) / 2);
-      P.k_chunk = ((nk + splits - 1) / splits) * BK32;
-      const int64_t used = (d.k + P.k_chunk - 1) / P.k_chunk;
+    if (g.k_chunk > 0) {
+      P.k_chunk = g.k_chunk;
+      const int64_t used = g.used;
       P.ws = static_cast<float*>(ws.get(size_t(used * d.m * d.n * 4), 0));
       dim3 grid(unsigned(tiles), unsigned(used), 1);
       if (d.trans_b) {
@@ -1101,6 +1117,51 @@ void launch_matmul(bg_ctx* ctx, const bg_matmul_desc& d, const Record& a, const 
   GemmWorkspace ws{ctx};
   run_matmul(ctx, d, a.ptr(), b.ptr(), bias ? reinterpret_cast<const float*>(bias->ptr()) : nullptr, out.ptr(),
              ws, ex);
+}
+
+// The launches bg_matmul_ex makes for an f32 GEMM whose operands start at
+// their offsets inside this library's (256-byte aligned) allocations.
+void plan_matmul(const bg_matmul_desc& d0, bg_launch_plan& out) {
+  bg_matmul_desc d = d0;
+  if (d.in_dtype != BG_F32) fail(BG_E_UNSUPPORTED, "matmul launch plan: float32 GEMMs only");
+  if (d.act == BG_ACT_GELU_TANH) fail(BG_E_UNSUPPORTED, "matmul launch plan: GELU epilogues are not covered");
+  if (d.m <= 0 || d.n <= 0 || d.k <= 0 || d.batch <= 0)
+    fail(BG_E_INVALID, "matmul: batch, m, k, n must be positive integers");
+  if (d.lda == 0) d.lda = d.k;
+  if (d.ldb == 0) d.ldb = d.trans_b ? d.k : d.n;
+  if (d.ldc == 0) d.ldc = d.n;
+  if (d.batch > 65535) fail(BG_E_UNSUPPORTED, "matmul: batch > 65535");
+  const bool ptrs = (d.offset_a * 4) % 16 == 0 && (d.offset_b * 4) % 16 == 0;
+  const Gemm32Shape g = gemm32_shape(d, ptrs);
+  out = bg_launch_plan{};
+  out.tile_m = 128;
+  out.tile_n = 128;
+  out.tile_k = BK32;
+  out.k_slices = int32_t(g.used);
+  out.lds_bytes = 2 * BK32 * (128 + 32 + 128 + 32) * 4;
+  bg_launch_plan_entry& e = out.launch[0];
+  std::snprintf(e.family, sizeof e.family, "%s", "gemm32_kernel");
+  e.n_targs = 4;
+  e.targs[0] = 128;
+  e.targs[1] = 128;
+  e.targs[2] = d.trans_b ? 1 : 0;
+  e.targs[3] = g.aligned ? 1 : 0;
+  e.block[0] = 256; e.block[1] = 1; e.block[2] = 1;
+  const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
+  if (g.k_chunk > 0) {
+    e.grid[0] = tiles; e.grid[1] = g.used; e.grid[2] = 1;
+    bg_launch_plan_entry& r = out.launch[1];
+    std::snprintf(r.family, sizeof r.family, "%s", "gemm32_splitk_reduce");
+    r.n_targs = 1;
+    r.targs[0] = d.out_dtype;
+    r.grid[0] = (d.m * d.n + 255) / 256; r.grid[1] = 1; r.grid[2] = 1;
+    r.block[0] = 256; r.block[1] = 1; r.block[2] = 1;
+    out.n_launches = 2;
+    out.workspace_bytes = g.used * d.m * d.n * 4;
+  } else {
+    e.grid[0] = tiles; e.grid[1] = 1; e.grid[2] = d.batch;
+    out.n_launches = 1;
+  }
 }
 
 }  // namespace bg

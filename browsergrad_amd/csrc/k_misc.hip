@@ -812,6 +812,10 @@ void launch_attention_masked_f32(bg_ctx* ctx, const float* q, const float* k, co
   d.scale = scale;
   d.in_dtype = BG_F32;
   d.out_dtype = BG_F32;
+  if (fa32_supported(d)) {
+    launch_fa32(ctx, d, q, k, v, mask, mask_b, mask_h, sk, o);
+    return;
+  }
   launch_attention_generic(ctx, d, q, k, v, mask, mask_b, mask_h, o, false);
 }
 

@@ -538,6 +538,40 @@ int bg_run_tensor_plan_semantic(bg_ctx* ctx, const char* plan_json,
 int bg_plan_inspect(const char* plan_json, const char* requests_json, char* out, size_t out_cap,
                     size_t* needed);
 
+/* Launch plan of one call, computed on the host before anything runs
+ * (extension; no context, no GPU): the kernels the call will launch, in
+ * order, with their template arguments, grids and workgroup sizes.  It backs
+ * the prepare step of the verified-artifact APIs, which fix a schedule before
+ * execution and check the run against it (prepareSemanticGemmWgsl,
+ * packages/browsergrad-kernels/src/semantic_gemm.ts:194-340;
+ * prepareSemanticAttentionWgsl, semantic_attention.ts:245-413).  Operands
+ * are taken to start at their descriptor offsets inside allocations made by
+ * this library (256-byte aligned), as the semantic runs upload them.
+ * Covered: float32 GEMMs without GELU (bg_matmul_launch_plan) and float32
+ * attention with head dim 1..64 (bg_attention_launch_plan); anything else
+ * returns BG_E_UNSUPPORTED. */
+#define BG_PLAN_MAX_LAUNCHES 4
+typedef struct bg_launch_plan_entry {
+  char family[48];        /* kernel function name, without namespace or template arguments */
+  int32_t n_targs;
+  int32_t targs[8];       /* integer / bool template arguments in declaration order */
+  int32_t block[3];
+  int64_t grid[3];
+} bg_launch_plan_entry;
+typedef struct bg_launch_plan {
+  int32_t n_launches;
+  int32_t tile_m, tile_n, tile_k;  /* GEMM: output tile and k step; attention: queries per
+                                      workgroup, keys per tile, padded head dim */
+  int32_t k_slices;                /* GEMM split-K slices (1 = none) */
+  int32_t reserved;
+  int64_t lds_bytes;               /* LDS per workgroup of the main kernel */
+  int64_t workspace_bytes;         /* context scratch the call takes */
+  bg_launch_plan_entry launch[BG_PLAN_MAX_LAUNCHES];
+} bg_launch_plan;
+/* A refusal's message goes to err (capacity err_cap, NUL-terminated; may be NULL). */
+int bg_matmul_launch_plan(const bg_matmul_desc* desc, bg_launch_plan* out, char* err, size_t err_cap);
+int bg_attention_launch_plan(const bg_attention_desc* desc, bg_launch_plan* out, char* err, size_t err_cap);
+
 /* Raw device pointer of a handle (extension; for harnesses that time
  * kernels with their own events).  Valid until the handle is released. */
 int bg_device_ptr(bg_ctx* ctx, bg_handle h, void** ptr);

@@ -71,6 +71,8 @@ def test_struct_layouts_match_header():
     assert C.sizeof(N.PassProfile) == 48 + 8 + 8 + 8
     assert C.sizeof(N.OptimArgs) == 6 * 8
     assert C.sizeof(N.ConvDesc) == 4 * 4 + 4 * 8 + 7 * 3 * 8 + 3 * 8
+    assert C.sizeof(N.LaunchPlanEntry) == 48 + 4 + 8 * 4 + 3 * 4 + 3 * 8
+    assert C.sizeof(N.LaunchPlan) == 6 * 4 + 2 * 8 + 4 * C.sizeof(N.LaunchPlanEntry)
 
 
 def test_fused_codegen_compiles_every_opcode(lib):

@@ -12,13 +12,18 @@ semantic-core tolerance (abs-or-rel 1e-4, attention-forward-model.ts:25-29).
 """
 from __future__ import annotations
 
+import dataclasses
+import threading
+
 import numpy as np
 import pytest
 
 from browsergrad_amd.semantic import (
-    canonical_hash, gemm_artifacts, gemm_tile_order,
+    canonical_hash, check_launches, check_layout, gemm_tile_order, parse_kernel_symbol,
     EXACT_F32_INTEGER_LIMIT, SemanticAttentionError, SemanticGemmError, certify_exact_f32_gemm_inputs,
-    run_semantic_attention_f32, run_semantic_gemm_exact_f32,
+    prepare_semantic_attention, prepare_semantic_gemm, run_prepared_semantic_attention_resident,
+    run_prepared_semantic_gemm_resident, run_semantic_attention, run_semantic_attention_f32, run_semantic_gemm,
+    run_semantic_gemm_exact_f32,
 )
 from oracle import ops as O
 
@@ -65,7 +70,7 @@ def test_exact_gemm_is_bit_exact(bridge, m, n, k, hi):
     # verified artifacts from the launches that ran, with their hashes
     arts = t["artifacts"]
     assert arts["layout"]["body"]["tensors"]["lhs"]["strides"] == [k, 1]
-    assert arts["schedule"]["body"]["launches"][0]["kernel"].find("gemm32") >= 0
+    assert arts["schedule"]["body"]["launches"][0]["family"] == "gemm32_kernel"
     for name, key in (("layout", "layoutSemanticHash"), ("tile", "kernelSemanticHash"),
                       ("schedule", "scheduleSemanticHash")):
         assert t[key] == arts[name]["hash"] == canonical_hash(arts[name]["body"])
@@ -110,6 +115,7 @@ def test_semantic_attention_f32(bridge, causal):
     t = res["trace"]
     assert t["kernelSemanticHash"] == t["artifacts"]["tile"]["hash"]
     assert t["artifacts"]["tile"]["body"]["rows"] == b * h * sq
+    assert t["artifacts"]["schedule"]["body"]["launches"][0]["family"] == "fa32_fwd_kernel"
     bad = q.copy()
     bad[0, 0, 0, 0] = np.inf
     with pytest.raises(SemanticAttentionError, match="finite"):
@@ -126,32 +132,182 @@ def test_gemm_tile_order_is_a_bijection():
             assert len(seen) == tm * tn and all(0 <= a < tm and 0 <= b < tn for a, b in seen), (tm, tn)
 
 
-def _rec(kernel, grid):
-    return {"kernel": kernel, "grid": grid, "block": [256, 1, 1], "dynamicLds": 0, "staticLds": 32768,
+def _rec(kernel, grid, block=(256, 1, 1)):
+    return {"kernel": kernel, "grid": list(grid), "block": list(block), "dynamicLds": 0, "staticLds": 32768,
             "vgprs": 128, "scratchBytesPerLane": 0}
 
 
-def test_gemm_artifacts_from_a_launch_log():
-    log = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEv8GemmArgs", [6, 1, 1])]
-    arts = gemm_artifacts(log, 300, 200, 64)
-    tile = arts["tile"]["body"]
-    assert (tile["tile"], tile["tilesM"], tile["tilesN"], tile["kSlices"]) == ({"m": 128, "n": 128}, 3, 2, 1)
-    assert arts["tile"]["hash"] == canonical_hash(tile)
-    # split K: partial GEMM over 4 slices and the finishing pass
-    log2 = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb1ELb1EEEv8GemmArgs", [1, 4, 1]),
-            _rec("_ZN12_GLOBAL__N_120gemm32_splitk_reduceILi0EEEv8GemmArgsi", [32, 1, 1])]
-    t2 = gemm_artifacts(log2, 64, 128, 784)["tile"]["body"]
-    assert t2["kSlices"] == 4 and "slice order" in t2["accumulation"]
+def test_prepare_gemm_fixes_schedule_before_any_launch():
+    """prepare_semantic_gemm needs no device: the schedule comes from the
+    library's own launch decision (bg_matmul_launch_plan).  300 x 200 x 64
+    is six 128 x 128 tiles in one launch; 64 x 128 x 784 (C1's shape) is one
+    tile with K split over 25 slices plus the finishing pass."""
+    p = prepare_semantic_gemm(300, 200, 64)
+    assert p.plan["launches"] == [{"family": "gemm32_kernel", "templateArgs": [128, 128, 0, 1],
+                                   "grid": [6, 1, 1], "block": [256, 1, 1]}]
+    tile = p.tile["body"]
+    assert (tile["tile"], tile["tilesM"], tile["tilesN"], tile["kSlices"]) == ({"m": 128, "n": 128, "k": 16}, 3, 2, 1)
+    for art in (p.layout, p.tile, p.schedule):
+        assert art["hash"] == canonical_hash(art["body"])
+    assert p.layout["body"]["tensors"]["lhs"] == {"shape": [300, 64], "strides": [64, 1], "dtype": "float32",
+                                                  "byteLength": 300 * 64 * 4}
+    # a second preparation of the same problem hashes the same
+    assert prepare_semantic_gemm(300, 200, 64).backendPreparationHash == p.backendPreparationHash
+    assert prepare_semantic_gemm(300, 200, 65).backendPreparationHash != p.backendPreparationHash
+    s = prepare_semantic_gemm(64, 128, 784)
+    assert [l["family"] for l in s.plan["launches"]] == ["gemm32_kernel", "gemm32_splitk_reduce"]
+    assert s.plan["launches"][0]["grid"] == [1, 25, 1] and s.tile["body"]["kSlices"] == 25
+    assert "slice order" in s.tile["body"]["accumulation"]
+    assert s.plannedTransientGpuBytes == 4 * (64 * 784 + 784 * 128 + 64 * 128) + 25 * 64 * 128 * 4
 
 
-@pytest.mark.parametrize("grid,m,n,msg", [
-    ([5, 1, 1], 300, 200, "grid.x"),            # one tile short
-    ([6, 1, 1], 300, 300, "grid.x"),            # wrong tile count for the shape
+@pytest.mark.parametrize("kw,path", [
+    ({"max_transient_working_set_bytes": 1 << 20}, "$.maxTransientWorkingSetBytes"),
+    ({"max_workgroup_storage_bytes": 16 * 1024}, "$.maxWorkgroupStorageBytes"),
+    ({"max_workgroup_invocations": 128}, "$.maxWorkgroupInvocations"),
 ])
-def test_gemm_artifacts_refuse_a_schedule_that_does_not_cover(grid, m, n, msg):
-    log = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEv8GemmArgs", grid)]
-    with pytest.raises(SemanticGemmError, match=msg) as e:
-        gemm_artifacts(log, m, n, 64)
-    assert e.value.code == "BG-WEBGPU-GEMM-VALIDATION"
-    with pytest.raises(SemanticGemmError, match="one GEMM kernel launch"):
-        gemm_artifacts([], m, n, 64)
+def test_prepare_gemm_enforces_limits(kw, path):
+    with pytest.raises(SemanticGemmError) as e:
+        prepare_semantic_gemm(1024, 1024, 64, **kw)
+    assert e.value.code == "BG-WEBGPU-GEMM-RESOURCE-LIMIT" and e.value.path == path
+
+
+@pytest.mark.parametrize("kw", [{"max_transient_working_set_bytes": 0},
+                                {"max_transient_working_set_bytes": (1 << 30) + 1},
+                                {"max_workgroup_storage_bytes": True}, {"max_workgroup_invocations": 2048}])
+def test_prepare_gemm_refuses_bad_limit_values(kw):
+    with pytest.raises(SemanticGemmError, match="positive integer"):
+        prepare_semantic_gemm(8, 8, 8, **kw)
+
+
+def test_prepared_objects_are_required_and_resident_runs_are_closed():
+    p = prepare_semantic_gemm(8, 8, 8)
+    with pytest.raises(SemanticGemmError) as e:
+        run_prepared_semantic_gemm_resident(p, {"lhs": 1, "rhs": 2})
+    assert e.value.code == "BG-WEBGPU-GEMM-NUMERICAL-PROOF"
+    forged = dataclasses.replace(p)  # same fields, not returned by prepare
+    a = np.ones((8, 8), F32)
+    cert = certify_exact_f32_gemm_inputs(a, a, 8, 8, 8)
+    for bad in (forged, {"m": 8}):
+        with pytest.raises(SemanticGemmError, match="returned by its prepare function") as e2:
+            run_semantic_gemm(None, bad, cert, a, a)
+        assert e2.value.code == "BG-WEBGPU-GEMM-INVALID-BINDING"
+    with pytest.raises(SemanticGemmError, match="the preparation for 8 x 8 x 8"):
+        b = np.ones((8, 4), F32)
+        run_semantic_gemm(None, p, certify_exact_f32_gemm_inputs(a, b, 8, 4, 8), a, b)
+    pa = prepare_semantic_attention(1, 1, 4, 4, 8)
+    with pytest.raises(SemanticAttentionError) as e3:
+        run_prepared_semantic_attention_resident(pa, None)
+    assert e3.value.code == "BG-WEBGPU-ATTENTION-NUMERICAL-PROOF"
+
+
+def test_cancel_and_wait_budget_are_checked_before_the_device():
+    p = prepare_semantic_gemm(8, 8, 8)
+    a = np.ones((8, 8), F32)
+    cert = certify_exact_f32_gemm_inputs(a, a, 8, 8, 8)
+    ev = threading.Event()
+    ev.set()
+    with pytest.raises(SemanticGemmError) as e:
+        run_semantic_gemm(None, p, cert, a, a, cancel=ev)  # the bridge is never reached
+    assert e.value.code == "BG-WEBGPU-GEMM-CANCELLED"
+    for bad in (0, 5 * 60_000 + 1, 1.5):
+        with pytest.raises(SemanticGemmError, match="positive integer") as e2:
+            run_semantic_gemm(None, p, cert, a, a, timeout_ms=bad)
+        assert e2.value.code == "BG-WEBGPU-GEMM-INVALID-BINDING"
+    with pytest.raises(SemanticGemmError, match="is_set"):
+        run_semantic_gemm(None, p, cert, a, a, cancel=object())
+
+
+def test_prepare_attention():
+    p = prepare_semantic_attention(2, 3, 37, 53, 64)
+    assert p.plan["launches"] == [{"family": "fa32_fwd_kernel", "templateArgs": [64, 1], "grid": [6, 1, 1],
+                                   "block": [256, 1, 1]}]
+    t = p.tile["body"]
+    assert (t["queriesPerWorkgroup"], t["keysPerTile"], t["paddedHeadDim"], t["rows"]) == (128, 64, 64, 2 * 3 * 37)
+    assert prepare_semantic_attention(1, 1, 300, 300, 20).plan["launches"][0]["templateArgs"] == [32, 1]
+    assert prepare_semantic_attention(1, 1, 300, 300, 7).plan["launches"][0]["templateArgs"] == [16, 0]
+    assert prepare_semantic_attention(2, 3, 37, 53, 64).backendPreparationHash == p.backendPreparationHash
+    assert prepare_semantic_attention(2, 3, 37, 53, 64, causal=False, scale=0.2).backendPreparationHash != \
+        p.backendPreparationHash
+    with pytest.raises(SemanticAttentionError, match="head dim 1..64") as e:
+        prepare_semantic_attention(1, 1, 8, 8, 65)
+    assert e.value.code == "BG-WEBGPU-ATTENTION-UNSUPPORTED-PROFILE"
+    with pytest.raises(SemanticAttentionError, match="q_len <= k_len"):
+        prepare_semantic_attention(1, 1, 9, 8, 16, causal=True)
+    with pytest.raises(SemanticAttentionError) as e2:
+        prepare_semantic_attention(1, 1, 8, 8, 64, max_workgroup_storage_bytes=32 * 1024)
+    assert e2.value.code == "BG-WEBGPU-ATTENTION-RESOURCE-LIMIT"
+    with pytest.raises(SemanticAttentionError) as e3:
+        prepare_semantic_attention(64, 16, 2048, 2048, 64)  # 1 GiB+ of planned buffers
+    assert e3.value.code == "BG-WEBGPU-ATTENTION-RESOURCE-LIMIT"
+
+
+@pytest.mark.parametrize("name,args", [
+    ("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEvNS_8GemmArgsE", [128, 128, 0, 1]),
+    ("(anonymous namespace)::gemm32_kernel<128, 128, false, true>((anonymous namespace)::GemmArgs)",
+     [128, 128, 0, 1]),
+    ("_ZN12_GLOBAL__N_120gemm32_splitk_reduceILi0EEEvNS_8GemmArgsEi", None),
+])
+def test_parse_kernel_symbol(name, args):
+    assert parse_kernel_symbol(name, "gemm32_kernel") == args
+
+
+def test_launch_log_must_match_the_prepared_schedule():
+    p = prepare_semantic_gemm(64, 128, 784)
+    good = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEvNS_8GemmArgsE", [1, 25, 1]),
+            _rec("_ZN12_GLOBAL__N_120gemm32_splitk_reduceILi0EEEvNS_8GemmArgsEi", [32, 1, 1])]
+    check_launches(p.plan, good, "BG-WEBGPU-GEMM-VALIDATION")
+    bad_grid = [dict(good[0], grid=[1, 24, 1]), good[1]]
+    bad_args = [dict(good[0], kernel=good[0]["kernel"].replace("ELb1EE", "ELb0EE")), good[1]]
+    for bad in (bad_grid, bad_args, good[:1], good + good[1:], [good[1], good[0]]):
+        with pytest.raises(SemanticGemmError) as e:
+            check_launches(p.plan, bad, "BG-WEBGPU-GEMM-VALIDATION")
+        assert e.value.code == "BG-WEBGPU-GEMM-VALIDATION"
+
+
+def test_layout_is_checked_against_device_records():
+    p = prepare_semantic_gemm(4, 6, 5)
+    info = lambda shp: {"shape": tuple(shp), "dtype": "float32", "nbytes": 4 * int(np.prod(shp))}  # noqa: E731
+    recs = {"lhs": info([4, 5]), "rhs": info([5, 6]), "output": info([4, 6])}
+    check_layout(p.layout, recs, "BG-WEBGPU-GEMM-VALIDATION")
+    for name, bad in (("rhs", info([6, 5])), ("output", dict(info([4, 6]), dtype="float16")),
+                      ("lhs", dict(info([4, 5]), nbytes=84))):
+        with pytest.raises(SemanticGemmError, match="does not match the prepared layout") as e:
+            check_layout(p.layout, {**recs, name: bad}, "BG-WEBGPU-GEMM-VALIDATION")
+        assert e.value.path == f"$.layout.{name}"
+
+
+@pytest.mark.gpu
+def test_prepared_gemm_runs_repeatably(bridge):
+    """One prepared specialization, several runs: every run's launch log is
+    the prepared schedule (split K for C1's 64 x 128 x 784), its device
+    records match the layout, its results are exact, and the preparation
+    hash in the trace is the same every time."""
+    rng = np.random.default_rng(11)
+    p = prepare_semantic_gemm(64, 128, 784)
+    hashes = set()
+    for _ in range(3):
+        a = rng.integers(0, 4, (64, 784)).astype(F32)
+        b = rng.integers(0, 4, (784, 128)).astype(F32)
+        res = run_semantic_gemm(bridge, p, certify_exact_f32_gemm_inputs(a, b, 64, 128, 784), a, b,
+                                timeout_ms=60_000)
+        got = np.frombuffer(res["destination"], F32).reshape(64, 128)
+        assert np.array_equal(got, (a.astype(np.int64) @ b.astype(np.int64)).astype(F32))
+        assert res["trace"]["launchesMatchedPreparation"] is True
+        hashes.add(res["trace"]["backendPreparationHash"])
+    assert hashes == {p.backendPreparationHash}
+
+
+@pytest.mark.gpu
+def test_prepared_attention_runs_repeatably(bridge):
+    rng = np.random.default_rng(12)
+    p = prepare_semantic_attention(2, 2, 100, 100, 24, causal=True)
+    hashes = set()
+    for _ in range(2):
+        q, k, v = (rng.standard_normal((2, 2, 100, 24)).astype(F32) for _ in range(3))
+        res = run_semantic_attention(bridge, p, q, k, v)
+        got = np.frombuffer(res["destination"], F32).reshape(2, 2, 100, 24)
+        ref = O.attention_f64(q, k, v, 1.0 / np.sqrt(24), causal=True)
+        assert O.within(got, ref, 1e-4).all(), O.report(got, ref, 1e-4)
+        hashes.add(res["trace"]["backendPreparationHash"])
+    assert hashes == {p.backendPreparationHash}

@@ -347,6 +347,7 @@ struct Fa2Args {
   int H, Sq, Sk, n_qblocks;
   float sl2;  // scale * log2(e), > 0
   int out_dtype;
+  int D;      // head dim: 64 (fa2 / fa6 / fa7), or 8..56 in steps of 8 (fa7: columns past D read as zero)
 };
 
 __device__ __forceinline__ int fa2_k_unit(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
@@ -925,6 +926,7 @@ __global__ void __launch_bounds__(kFa2NW * 64, 2) fa6_fwd_kernel(Fa2Args P, uint
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const int d0 = db * 32 + 8 * gq + 4 * hi;
+      if (d0 >= P.D) continue;
       const float y0 = acc[db][4 * gq] * inv, y1 = acc[db][4 * gq + 1] * inv;
       const float y2 = acc[db][4 * gq + 2] * inv, y3 = acc[db][4 * gq + 3] * inv;
       if (P.out_dtype == 0)
@@ -996,6 +998,7 @@ __device__ __forceinline__ void fa7_store(const Fa2Args& P, int b, int h, int qi
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const int d0 = db * 32 + 8 * gq + 4 * hi;
+      if (d0 >= P.D) continue;
       const float y0 = acc[db][4 * gq] * inv, y1 = acc[db][4 * gq + 1] * inv;
       const float y2 = acc[db][4 * gq + 2] * inv, y3 = acc[db][4 * gq + 3] * inv;
       if (P.out_dtype == 0)
@@ -1046,7 +1049,7 @@ __device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0
       if (j < nkeys) {
         const uint16_t* krow = Kp + int64_t(j) * P.k_ss;
         float acc = 0.f;
-        for (int d = 0; d < 64; d += 2) {
+        for (int d = 0; d < P.D; d += 2) {
           const uint32_t qw = *reinterpret_cast<const uint32_t*>(qrow + d);
           const uint32_t kw = *reinterpret_cast<const uint32_t*>(krow + d);
           if constexpr (ROUND_S) {
@@ -1070,15 +1073,17 @@ __device__ __forceinline__ void fa7_exact(const Fa2Args& P, int b, int h, int q0
       const int jn = min(64, nkeys - j0);
       for (int jj = 0; jj < jn; ++jj) {
         const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p16), jj));
-        const uint16_t vv = Vp[int64_t(j0 + jj) * P.v_ss + lane];
+        const uint16_t vv = lane < P.D ? Vp[int64_t(j0 + jj) * P.v_ss + lane] : uint16_t(0);
         o += pj * (BF16 ? bgk::bf16_bits_to_f32(vv) : bgk::f16_bits_to_f32(vv));
       }
     }
     const float y = l_run > 0.f ? o / l_run : 0.f;
-    const int64_t oi = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss + lane;
-    if (P.out_dtype == 0) reinterpret_cast<float*>(Ob)[oi] = y;
-    else if (P.out_dtype == 1) reinterpret_cast<uint16_t*>(Ob)[oi] = bgk::f32_to_f16_bits(y);
-    else reinterpret_cast<uint16_t*>(Ob)[oi] = bgk::f32_to_bf16_bits(y);
+    if (lane < P.D) {
+      const int64_t oi = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss + lane;
+      if (P.out_dtype == 0) reinterpret_cast<float*>(Ob)[oi] = y;
+      else if (P.out_dtype == 1) reinterpret_cast<uint16_t*>(Ob)[oi] = bgk::f32_to_f16_bits(y);
+      else reinterpret_cast<uint16_t*>(Ob)[oi] = bgk::f32_to_bf16_bits(y);
+    }
   }
 }
 
@@ -1171,8 +1176,10 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
     const int u = (w + p * NW) * 64 + lane;
     const int pc = u & 7;
     krow[p] = u >> 3;
-    koff[p] = uint32_t((int64_t(krow[p]) * P.k_ss + ((pc ^ ((krow[p] >> 1) & 7)) * 8)) * 2);
-    voff[p] = uint32_t((int64_t(krow[p]) * P.v_ss + ((pc ^ ((krow[p] & 3) << 1)) * 8)) * 2);
+    // 16-byte chunks past the head dim read zeros (an offset past the buffer).
+    const int kc = pc ^ ((krow[p] >> 1) & 7), vc = pc ^ ((krow[p] & 3) << 1);
+    koff[p] = kc * 8 < P.D ? uint32_t((int64_t(krow[p]) * P.k_ss + kc * 8) * 2) : kFa2Oob;
+    voff[p] = vc * 8 < P.D ? uint32_t((int64_t(krow[p]) * P.v_ss + vc * 8) * 2) : kFa2Oob;
   }
   const uint32_t kstep = uint32_t(int64_t(kFa2BK) * P.k_ss * 2);
   const uint32_t vstep = uint32_t(int64_t(kFa2BK) * P.v_ss * 2);
@@ -1194,8 +1201,9 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
   fa_u4 qf[4];
 #pragma unroll
   for (int dc = 0; dc < 4; ++dc)
-    qf[dc] = qi < P.Sq ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
-                       : fa_u4{0u, 0u, 0u, 0u};
+    qf[dc] = qi < P.Sq && dc * 16 + hi * 8 < P.D
+                 ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + dc * 16 + hi * 8)
+                 : fa_u4{0u, 0u, 0u, 0u};
   // PAIRS (the 4-slot ring): tiles are awaited and refilled two at a time,
   // one barrier per two tiles: at an even step t the wavefronts wait for
   // tiles t and t+1, pass the barrier and copy tiles t+2 and t+3 into the
@@ -1405,7 +1413,10 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
   const int64_t flops = 4 * pairs * d.d;
   const int64_t bytes = d.batch * d.heads * (sq * d.d + 2 * sk * d.d) * es +
                         d.batch * d.heads * sq * d.d * dtype_size(d.out_dtype);
-  const bool mfma_ok = (d.in_dtype == BG_F16 || d.in_dtype == BG_BF16) && d.d == 64 &&
+  // Head dims below 64 (multiples of 8) run the fast kernel with the
+  // missing 16-byte chunks read as zeros; the other kernels take 64 only.
+  const bool d64 = d.d == 64;
+  const bool mfma_ok = (d.in_dtype == BG_F16 || d.in_dtype == BG_BF16) && d.d % 8 == 0 && d.d <= 64 &&
                        d.q_ss % 8 == 0 && d.k_ss % 8 == 0 && d.v_ss % 4 == 0 && d.o_ss % 4 == 0 &&
                        d.q_sb % 8 == 0 && d.q_sh % 8 == 0 && d.k_sb % 8 == 0 && d.k_sh % 8 == 0 &&
                        d.v_sb % 4 == 0 && d.v_sh % 4 == 0 && d.o_sb % 4 == 0 && d.o_sh % 4 == 0 &&
@@ -1417,7 +1428,10 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
                 reinterpret_cast<const float*>(vp), nullptr, 0, 0, 0, out.ptr());
     return;
   }
-  if (!mfma_ok) {
+  const bool r = d.round_scores != 0;
+  const float sl2 = d.scale * 1.4426950408889634f;
+  const bool fa7_takes = r || d.in_dtype == BG_BF16 || sl2 <= 1.0f;  // Q * scale * log2 e stays in f16 range
+  if (!mfma_ok || (!d64 && (attn_version() != 7 || !fa7_takes))) {
     Profile prof(ctx, "attention_generic", bytes, flops);
     launch_attention_generic(ctx, d, qp, kp, vp, nullptr, 0, 0, out.ptr(),
                              d.in_dtype != BG_F32);
@@ -1432,6 +1446,11 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
                      d.v_sb % 8 == 0 && d.v_sh % 8 == 0 && al(vp, 16) && d.scale > 0.f &&
                      k_span > 0 && v_span > 0 && k_head < (int64_t(1) << 31) &&
                      v_head < (int64_t(1) << 31) && (sq + kFa2BQ - 1) / kFa2BQ <= 65535;
+  if (!d64 && !v2_ok) {
+    Profile prof(ctx, "attention_generic", bytes, flops);
+    launch_attention_generic(ctx, d, qp, kp, vp, nullptr, 0, 0, out.ptr(), true);
+    return;
+  }
   if (v2_ok) {
     Fa2Args A{};
     A.q = reinterpret_cast<const uint16_t*>(qp);
@@ -1446,18 +1465,18 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     A.Sq = int(sq);
     A.Sk = int(sk);
     A.n_qblocks = int((sq + kFa2BQ - 1) / kFa2BQ);
-    A.sl2 = d.scale * 1.4426950408889634f;
+    A.sl2 = sl2;
     A.out_dtype = d.out_dtype;
+    A.D = int(d.d);
     const int bh = int(d.batch * d.heads);
     const bool bf = d.in_dtype == BG_BF16;
     const bool c = d.causal != 0;
-    const bool r = d.round_scores != 0;
     const uint32_t kb = uint32_t(k_head), vb = uint32_t(v_head);
     Profile prof(ctx, bf ? "attention_bf16" : "attention_f16", bytes, flops);
     const int ver = attn_version();
     // fa7 with the scale folded into Q needs |Q * scale * log2 e| <= |Q| for
     // f16 (no overflow); its ROUND_S form scales each rounded score instead.
-    const bool fast = ver != 2 && (r || bf || A.sl2 <= 1.0f);
+    const bool fast = ver != 2 && fa7_takes;
 #define BG_FA2(B_, C_, R_)                                                                     \
   (fast ? (ver == 6 && !R_ ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb)               \
                            : launch_fa7<B_, C_, R_>(ctx, A, bh, kb, vb))                     \
@@ -1491,7 +1510,6 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
   const int bh = int(d.batch * d.heads);
   const bool bf = d.in_dtype == BG_BF16;
   const bool c = d.causal != 0;
-  const bool r = d.round_scores != 0;
   Profile prof(ctx, bf ? "attention_bf16" : "attention_f16", bytes, flops);
 #define BG_FA(B_, C_, R_) launch_fa<B_, C_, R_>(ctx, A, bh, A.n_qblocks)
   if (bf) {

@@ -255,6 +255,60 @@ def test_attention_mfma(bridge, rng, fa7_block, b, h, s, causal, dtype, round_sc
     assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
 
 
+@pytest.mark.parametrize("d", [8, 16, 32, 48])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("round_scores", [False, True])
+def test_attention_mfma_small_head_dims(bridge, rng, fa7_block, d, causal, dtype, round_scores):
+    """Head dims below 64 (multiples of 8, the reference admits 1..64) run
+    the fast MFMA kernel with the missing 16-byte chunks of Q, K and V read
+    as zeros and only the first d output columns stored."""
+    b, h, sq, sk = 2, 3, 200, 200
+    print(f"[case] small head dim d={d} causal={causal} {dtype} round_scores={round_scores}", flush=True)
+    q, k, v = (rng.standard_normal((b, h, s_, d)).astype(np.float32) for s_ in (sq, sk, sk))
+    scale = 1.0 / np.sqrt(d)
+    if dtype == "float16":
+        ts = [t.astype(np.float16) for t in (q, k, v)]
+        hs = [up(bridge, t) for t in ts]
+        ref = O.sdpa_amp(*ts, scale, causal).astype(np.float32)
+    else:
+        ts = [O.f32_to_bf16_bits(t) for t in (q, k, v)]
+        hs = [up(bridge, t, "bfloat16") for t in ts]
+        ref = O.bf16_bits_to_f32(O.sdpa_bf16(*ts, scale, causal))
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        ho = bridge.attention_ex(*hs, batch=b, heads=h, sq=sq, sk=sk, d=d, scale=scale, causal=causal,
+                                 in_dtype=dtype, round_scores=round_scores)
+        names = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    assert any("fa7_fwd_kernel" in t for t in names), names
+    y = bridge.to_numpy(ho)
+    y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
+    assert y.shape == (b, h, sq, d)
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
+def test_attention_small_head_dim_dominant_key(bridge, rng):
+    """d = 32 with a key that beats the first 32 by far more than 2^16: the
+    exact recompute pass also reads and writes only the first d columns."""
+    b, h, s, d = 1, 1, 300, 32
+    q = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    k = (0.25 * rng.standard_normal((b, h, s, d))).astype(np.float32)
+    v = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    u = np.ones(d, np.float32) / np.sqrt(d / 16.0)
+    q[0, 0] += 4.0 * u
+    k[0, 0, 100] = 4.0 * u
+    ts = [t.astype(np.float16) for t in (q, k, v)]
+    ho = bridge.attention_ex(*[up(bridge, t) for t in ts], batch=b, heads=h, sq=s, sk=s, d=d, scale=0.125,
+                             causal=True, in_dtype="float16")
+    y = bridge.to_numpy(ho).astype(np.float32)
+    ref = O.sdpa_amp(*ts, 0.125, True).astype(np.float32)
+    assert np.isfinite(y).all()
+    assert O.within(y, ref, TOL16).all(), O.report(y, ref, TOL16)
+
+
 def test_attention_generic_f32_legacy(bridge, rng):
     b, h, s, d = 1, 2, 33, 16
     q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))

@@ -327,6 +327,33 @@ def bench_c3(br, steps, warmup, dtype):
     return out
 
 
+def bench_c3_library(steps, warmup):
+    """The same 4096^3 fp16 GEMM through torch (hipBLASLt on this image), in
+    the same process: the library baseline the hand-written kernel is
+    compared with (f16 in, f16 out, no epilogue), timed with torch's events
+    on torch's stream.  Not part of any parity claim."""
+    import torch
+    M = N = K = 4096
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = (torch.rand((M, K), generator=g, device="cuda") * 2 - 1).half()
+    bt = (torch.rand((N, K), generator=g, device="cuda") * 2 - 1).half()
+    for _ in range(warmup):
+        torch.nn.functional.linear(a, bt)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record()
+        torch.nn.functional.linear(a, bt)
+        e1.record()
+    torch.cuda.synchronize()
+    ms = [e0.elapsed_time(e1) for e0, e1 in ev]
+    k_ms = float(np.median(ms))
+    flops = 2.0 * M * N * K
+    return {"kernel_ms_median": k_ms, "tflops": flops / (k_ms * 1e-3) / 1e12,
+            "frac_of_peak": flops / (k_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
+            "library": f"torch {torch.__version__} F.linear (hipBLASLt), f16 out"}
+
+
 def _walk_timed(br, uop, buffers, steps, warmup, recast=False):
     """Walk a prepared graph from resident leaves: (wall ms/step, kernel ms
     per step by profile label, walker output of one more step).  With
@@ -745,13 +772,32 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c1,c2,c3,c4,c5,train,conv")
+    ap.add_argument("--only", default="c1,c2,c3,c3lib,c4,c5,train,conv")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
               f"the multi-GPU path is design-only", file=sys.stderr)
         return 2
     only = set(a.only.split(","))
+
+    if only == {"c3lib"}:  # the library baseline alone (no HIP context of this library in the process)
+        print(json.dumps(bench_c3_library(a.steps, a.warmup)), flush=True)
+        return 0
+    lib_baseline = None
+    if "c3lib" in only:
+        # torch ships its own HIP runtime, which finds no device once this
+        # library's runtime holds it: the library leg runs first, in a child
+        # process started before this process touches the GPU.
+        log("c3 4096^3 fp16 through the library (torch / hipBLASLt), child process on the same GPU")
+        import subprocess
+        proc = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "c3lib", "--steps",
+                               str(max(10, a.steps // 2)), "--warmup", str(a.warmup)],
+                              stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+        try:
+            lib_baseline = json.loads(proc.stdout.strip().splitlines()[-1])
+        except (ValueError, IndexError):
+            lib_baseline = {"error": proc.stderr[-500:]}
+        log(f"  {lib_baseline}")
 
     from browsergrad_amd.bridge import HipRealizerBridge
     br = HipRealizerBridge(device=0, profiling=True)
@@ -778,6 +824,8 @@ def main() -> int:
         log("c3 gemm 4096^3 fp32")
         extra["c3_gemm_fp32"] = bench_c3(br, max(5, a.steps // 10), 2, "float32")
         log(f"  {extra['c3_gemm_fp32']}")
+    if lib_baseline is not None:
+        extra["c3_gemm_fp16_library_baseline"] = lib_baseline
     if "c4" in only:
         log("c4 causal attention B8 H16 S2048 D64 fp16")
         extra["c4_attention_fp16"] = bench_c4(br, max(10, a.steps // 2), a.warmup)

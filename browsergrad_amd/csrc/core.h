@@ -242,8 +242,7 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d,
 struct Gemm32Shape {
   int tiles_m = 0, tiles_n = 0;
   bool aligned = false;
-  int64_t used = 1;     // split-K slices launched (1: no split)
-  int64_t k_chunk = 0;  // K elements per slice (0: no split)
+  bool wide = false;  // gemm32_wide_k_kernel: 32 x 32 blocks, K split over 16 wavefronts
 };
 Gemm32Shape gemm32_shape(const bg_matmul_desc& d, bool ptrs_aligned);
 void plan_matmul(const bg_matmul_desc& d, bg_launch_plan& out);

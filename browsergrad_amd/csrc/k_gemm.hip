@@ -62,8 +62,6 @@ struct GemmArgs {
   int act;          // BG_ACT_*
   int out_dtype;    // BG_F32 / BG_F16 / BG_BF16
   int vec_store;    // C rows can take 4-element vector stores (ldc % 4, alignment)
-  int64_t k_chunk;  // f32 split-K: K elements per blockIdx.y slice (0: no split)
-  float* ws;        // f32 split-K: [splits][M][N] partial sums
   const float* R;   // residual f32 [batch][M][N] added last (NULL: none)
   int64_t ldr, sr;  // its row and batch strides (elements)
 };
@@ -606,9 +604,7 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  // Split-K: this workgroup sums k in [kbeg, kend) only.
-  const int64_t kbeg = P.k_chunk ? int64_t(blockIdx.y) * P.k_chunk : 0;
-  const int64_t kend = P.k_chunk ? min(P.K, kbeg + P.k_chunk) : P.K;
+  const int64_t kbeg = 0, kend = P.K;
 
   float16v acc[TM][TN];
 #pragma unroll
@@ -729,33 +725,94 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs P) {
     __syncthreads();
   }
 
-  if (P.k_chunk) {
-    // Partial sums, plain f32, into this slice of the workspace.
-    GemmArgs Q = P;
-    Q.bias = nullptr;
-    Q.round_dtype = 0;
-    Q.act = BG_ACT_NONE;
-    Q.out_dtype = BG_F32;
-    Q.ldc = P.N;
-    Q.R = nullptr;
-    direct_epilogue<TM, TN, false>(Q, reinterpret_cast<char*>(P.ws + int64_t(blockIdx.y) * P.M * P.N), acc,
-                                   m0 + wm * WTM, n0 + wn * WTN);
-    return;
-  }
   direct_epilogue<TM, TN, false>(P, C, acc, m0 + wm * WTM, n0 + wn * WTN);
 }
 
-// Split-K finish: C = epilogue(sum over slices in slice order).
-template <int OUT>
-__global__ void __launch_bounds__(256) gemm32_splitk_reduce(GemmArgs P, int splits) {
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= P.M * P.N) return;
-  const int64_t m = i / P.N, n = i % P.N;
-  float s = P.ws[i];
-  for (int k = 1; k < splits; ++k) s += P.ws[int64_t(k) * P.M * P.N + i];
-  float v = epilogue_value(P, s, P.bias ? P.bias[n] : 0.f);
-  if (P.R) v = v + P.R[m * P.ldr + n];
-  store_elem<OUT>(static_cast<char*>(P.C) + (m * P.ldc + n) * (OUT == BG_F32 ? 4 : 2), v);
+// ---- f32 GEMM for small outputs with a long K (C1's 64 x 784 x 128) ---------------
+//
+// One workgroup per 32 x 32 block of C; its 16 wavefronts split K into
+// 8-wide chunks (wavefront w takes a contiguous run of them), each
+// accumulating a full 32 x 32 partial with v_mfma_f32_32x32x2_f32, then the
+// 16 partials are summed through LDS in wavefront order (fixed, so results
+// do not depend on timing) and the epilogue is applied and stored in the
+// same launch.  MFMA t of chunk c takes k = 8c + 4 (lane / 32) + t on both
+// operands, so a lane's A and B values for four MFMAs are one 16-byte load
+// each (ALIGNED: rows 16-byte aligned, K % 4 == 0, B as [N][K]); otherwise
+// per-element loads.  Operands come straight from global memory (L2): each
+// element is read by one lane of one wavefront.
+constexpr int kWideWaves = 16;
+
+template <bool TRANS_B, bool ALIGNED>
+__device__ __forceinline__ void wide_k_load(const GemmArgs& P, const float* A, const float* B, int64_t m,
+                                            int64_t n, int64_t k0, float (&a)[4], float (&b)[4]) {
+  if constexpr (ALIGNED && TRANS_B) {
+    const bool kin = k0 < P.K;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 z = {0.f, 0.f, 0.f, 0.f};
+    const f4 av = (kin && m < P.M) ? *reinterpret_cast<const f4*>(A + m * P.lda + k0) : z;
+    const f4 bv = (kin && n < P.N) ? *reinterpret_cast<const f4*>(B + n * P.ldb + k0) : z;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      a[t] = av[t];
+      b[t] = bv[t];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t k = k0 + t;
+      const bool kin = k < P.K;
+      a[t] = (kin && m < P.M) ? A[m * P.lda + k] : 0.f;
+      b[t] = (kin && n < P.N) ? (TRANS_B ? B[n * P.ldb + k] : B[k * P.ldb + n]) : 0.f;
+    }
+  }
+}
+
+template <int OUT, bool TRANS_B, bool ALIGNED>
+__global__ void __launch_bounds__(kWideWaves * 64) gemm32_wide_k_kernel(GemmArgs P) {
+  __shared__ float red[kWideWaves][1024];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int hi = lane >> 5, l32 = lane & 31;
+  const int tiles_n = (int)((P.N + 31) / 32);
+  const int64_t m0 = int64_t(blockIdx.x / tiles_n) * 32, n0 = int64_t(blockIdx.x % tiles_n) * 32;
+  const float* A = static_cast<const float*>(P.A);
+  const float* B = static_cast<const float*>(P.B);
+  const int64_t nchunks = (P.K + 7) / 8;
+  const int64_t per = (nchunks + kWideWaves - 1) / kWideWaves;
+  const int64_t cb = w * per, ce = min(nchunks, cb + per);
+  float16v acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  const int64_t m = m0 + l32, n = n0 + l32;
+  int64_t c = cb;
+  for (; c + 2 <= ce; c += 2) {  // two chunks' loads in flight before their MFMAs
+    float a0[4], b0[4], a1[4], b1[4];
+    wide_k_load<TRANS_B, ALIGNED>(P, A, B, m, n, 8 * c + 4 * hi, a0, b0);
+    wide_k_load<TRANS_B, ALIGNED>(P, A, B, m, n, 8 * (c + 1) + 4 * hi, a1, b1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc, 0, 0, 0);
+  }
+  if (c < ce) {
+    float a0[4], b0[4];
+    wide_k_load<TRANS_B, ALIGNED>(P, A, B, m, n, 8 * c + 4 * hi, a0, b0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc, 0, 0, 0);
+  }
+  // acc[e] = partial C[m0 + 8 (e / 4) + 4 hi + e % 4][n0 + lane % 32].
+#pragma unroll
+  for (int e = 0; e < 16; ++e) red[w][e * 64 + lane] = acc[e];
+  __syncthreads();
+  const int t = threadIdx.x, e = t >> 6, l = t & 63;
+  float s = red[0][t];
+#pragma unroll
+  for (int ww = 1; ww < kWideWaves; ++ww) s += red[ww][t];
+  const int64_t mm = m0 + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3), nn = n0 + (l & 31);
+  if (mm >= P.M || nn >= P.N) return;
+  float v = epilogue_value(P, s, P.bias ? P.bias[nn] : 0.f);
+  if (P.R) v = v + P.R[mm * P.ldr + nn];
+  store_elem<OUT>(static_cast<char*>(P.C) + (mm * P.ldc + nn) * (OUT == BG_F32 ? 4 : 2), v);
 }
 
 template <int BM, int BN, bool BF16, int SWZ>
@@ -870,10 +927,11 @@ namespace bg {
 
 // Launch shape of the f32 GEMM, shared by run_gemm and the launch-plan
 // query.  ptrs_aligned: A and B (offsets applied) start on 16 bytes.
-// Few output tiles and a long K (C1's 64 x 784 x 128): one workgroup would
-// walk K alone, one global-memory latency per 16-wide k step, so K is split
-// over blockIdx.y (two k steps per slice) into f32 partials that one
-// summing pass adds in slice order, applying the epilogue.
+// Few output tiles and a long K (C1's 64 x 784 x 128): one 128 x 128
+// workgroup would walk K alone, one global-memory latency per 16-wide k
+// step, so such GEMMs take the wide-K kernel instead (32 x 32 blocks, K
+// split over the wavefronts of a workgroup and summed through LDS, one
+// launch).
 Gemm32Shape gemm32_shape(const bg_matmul_desc& d, bool ptrs_aligned) {
   Gemm32Shape g;
   g.tiles_m = int((d.m + 127) / 128);
@@ -883,9 +941,12 @@ Gemm32Shape gemm32_shape(const bg_matmul_desc& d, bool ptrs_aligned) {
   const int64_t nk = (d.k + BK32 - 1) / BK32;
   const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
   if (d.batch == 1 && tiles <= 16 && nk >= 8) {
-    const int64_t splits = std::min<int64_t>(64, (nk + 1) / 2);
-    g.k_chunk = ((nk + splits - 1) / splits) * BK32;
-    g.used = (d.k + g.k_chunk - 1) / g.k_chunk;
+    // One launch: 32 x 32 blocks of C, K split over 16 wavefronts inside
+    // each workgroup (gemm32_wide_k_kernel).
+    g.wide = true;
+    g.tiles_m = int((d.m + 31) / 32);
+    g.tiles_n = int((d.n + 31) / 32);
+    g.aligned = g.aligned && d.trans_b;
   }
   return g;
 }
@@ -947,24 +1008,18 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const 
     P.tiles_n = g.tiles_n;
     const bool aligned = g.aligned;
     Profile prof(ctx, "gemm_f32", bytes, flops);
-    const int64_t tiles = int64_t(P.tiles_m) * P.tiles_n;
-    if (g.k_chunk > 0) {
-      P.k_chunk = g.k_chunk;
-      const int64_t used = g.used;
-      P.ws = static_cast<float*>(ws.get(size_t(used * d.m * d.n * 4), 0));
-      dim3 grid(unsigned(tiles), unsigned(used), 1);
-      if (d.trans_b) {
-        if (aligned) bg::dispatch(ctx, gemm32_kernel<128, 128, true, true>, grid, dim3(256), 0, P);
-        else bg::dispatch(ctx, gemm32_kernel<128, 128, true, false>, grid, dim3(256), 0, P);
-      } else {
-        if (aligned) bg::dispatch(ctx, gemm32_kernel<128, 128, false, true>, grid, dim3(256), 0, P);
-        else bg::dispatch(ctx, gemm32_kernel<128, 128, false, false>, grid, dim3(256), 0, P);
-      }
-      const dim3 rg(unsigned((d.m * d.n + 255) / 256));
-      const int sp = int(used);
-      if (out_dtype == BG_F32) bg::dispatch(ctx, gemm32_splitk_reduce<BG_F32>, rg, dim3(256), 0, P, sp);
-      else if (out_dtype == BG_F16) bg::dispatch(ctx, gemm32_splitk_reduce<BG_F16>, rg, dim3(256), 0, P, sp);
-      else bg::dispatch(ctx, gemm32_splitk_reduce<BG_BF16>, rg, dim3(256), 0, P, sp);
+    if (g.wide) {
+      const dim3 grid(unsigned(g.tiles_m * g.tiles_n));
+      const dim3 block(kWideWaves * 64);
+      auto go = [&](auto kern) { bg::dispatch(ctx, kern, grid, block, 0, P); };
+      const bool tb = d.trans_b != 0;
+#define BG_WIDE(O_)                                                                              \
+  (tb ? (aligned ? go(gemm32_wide_k_kernel<O_, true, true>) : go(gemm32_wide_k_kernel<O_, true, false>)) \
+      : go(gemm32_wide_k_kernel<O_, false, false>))
+      if (out_dtype == BG_F32) BG_WIDE(BG_F32);
+      else if (out_dtype == BG_F16) BG_WIDE(BG_F16);
+      else BG_WIDE(BG_BF16);
+#undef BG_WIDE
       return;
     }
     launch32<128, 128>(ctx, P, d.batch, d.trans_b != 0, aligned);
@@ -1134,12 +1189,28 @@ void plan_matmul(const bg_matmul_desc& d0, bg_launch_plan& out) {
   const bool ptrs = (d.offset_a * 4) % 16 == 0 && (d.offset_b * 4) % 16 == 0;
   const Gemm32Shape g = gemm32_shape(d, ptrs);
   out = bg_launch_plan{};
+  out.k_slices = 1;
+  out.n_launches = 1;
+  bg_launch_plan_entry& e = out.launch[0];
+  if (g.wide) {
+    out.tile_m = 32;
+    out.tile_n = 32;
+    out.tile_k = 8;
+    out.k_slices = kWideWaves;
+    out.lds_bytes = kWideWaves * 1024 * 4;
+    std::snprintf(e.family, sizeof e.family, "%s", "gemm32_wide_k_kernel");
+    e.n_targs = 3;
+    e.targs[0] = d.out_dtype;
+    e.targs[1] = d.trans_b ? 1 : 0;
+    e.targs[2] = g.aligned ? 1 : 0;
+    e.grid[0] = int64_t(g.tiles_m) * g.tiles_n; e.grid[1] = 1; e.grid[2] = 1;
+    e.block[0] = kWideWaves * 64; e.block[1] = 1; e.block[2] = 1;
+    return;
+  }
   out.tile_m = 128;
   out.tile_n = 128;
   out.tile_k = BK32;
-  out.k_slices = int32_t(g.used);
   out.lds_bytes = 2 * BK32 * (128 + 32 + 128 + 32) * 4;
-  bg_launch_plan_entry& e = out.launch[0];
   std::snprintf(e.family, sizeof e.family, "%s", "gemm32_kernel");
   e.n_targs = 4;
   e.targs[0] = 128;
@@ -1147,21 +1218,7 @@ void plan_matmul(const bg_matmul_desc& d0, bg_launch_plan& out) {
   e.targs[2] = d.trans_b ? 1 : 0;
   e.targs[3] = g.aligned ? 1 : 0;
   e.block[0] = 256; e.block[1] = 1; e.block[2] = 1;
-  const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
-  if (g.k_chunk > 0) {
-    e.grid[0] = tiles; e.grid[1] = g.used; e.grid[2] = 1;
-    bg_launch_plan_entry& r = out.launch[1];
-    std::snprintf(r.family, sizeof r.family, "%s", "gemm32_splitk_reduce");
-    r.n_targs = 1;
-    r.targs[0] = d.out_dtype;
-    r.grid[0] = (d.m * d.n + 255) / 256; r.grid[1] = 1; r.grid[2] = 1;
-    r.block[0] = 256; r.block[1] = 1; r.block[2] = 1;
-    out.n_launches = 2;
-    out.workspace_bytes = g.used * d.m * d.n * 4;
-  } else {
-    e.grid[0] = tiles; e.grid[1] = 1; e.grid[2] = d.batch;
-    out.n_launches = 1;
-  }
+  e.grid[0] = int64_t(g.tiles_m) * g.tiles_n; e.grid[1] = 1; e.grid[2] = d.batch;
 }
 
 }  // namespace bg

@@ -388,28 +388,34 @@ def prepare_semantic_gemm(m: int, n: int, k: int, *, max_transient_working_set_b
     main = plan["launches"][0]
     bm, bn, bk = plan["tile"]
     tiles_m, tiles_n = -(-m // bm), -(-n // bn)
+    wide = main["family"] == "gemm32_wide_k_kernel"
     if main["grid"][0] != tiles_m * tiles_n or not (tiles_m * bm >= m > (tiles_m - 1) * bm
                                                       and tiles_n * bn >= n > (tiles_n - 1) * bn):
         _fail(code, "$.tile", f"{main['grid'][0]} workgroups do not cover {m} x {n} once with {bm} x {bn} tiles")
-    seen = {gemm_tile_order(p, tiles_m, tiles_n) for p in range(tiles_m * tiles_n)}
+    # Workgroup -> tile: the wide-K kernel walks tiles row-major; the others
+    # use the XCD-aware order restated by gemm_tile_order.
+    order = (lambda p: (p // tiles_n, p % tiles_n)) if wide else (lambda p: gemm_tile_order(p, tiles_m, tiles_n))
+    seen = {order(p) for p in range(tiles_m * tiles_n)}
     if len(seen) != tiles_m * tiles_n or not all(0 <= a < tiles_m and 0 <= b < tiles_n for a, b in seen):
         _fail(code, "$.schedule.tileOrder", "workgroup -> tile order is not a bijection onto the tile grid")
     slices = plan["kSlices"]
-    if slices > 1 and (main["grid"][1] != slices or len(plan["launches"]) != 2
-                       or plan["workspaceBytes"] != 4 * slices * m * n):
-        _fail(code, "$.tile.kSlices", f"{slices} K slices need one partial per slice and a finishing pass")
+    if wide and (slices != main["block"][0] // 64 or len(plan["launches"]) != 1 or plan["workspaceBytes"] != 0):
+        _fail(code, "$.tile.kSlices", f"{slices} in-workgroup K slices need one wavefront each and one launch")
+    if not wide and (slices != 1 or len(plan["launches"]) != 1):
+        _fail(code, "$.tile.kSlices", "the tiled kernel runs the whole K range in one launch")
     layout = layout_artifact({"lhs": {"shape": [m, k], "dtype": "float32"},
                               "rhs": {"shape": [k, n], "dtype": "float32"},
                               "output": {"shape": [m, n], "dtype": "float32"}})
     tile = _artifact("logical-gemm-tile", {
         "m": m, "n": n, "k": k, "tile": {"m": bm, "n": bn, "k": bk}, "tilesM": tiles_m, "tilesN": tiles_n,
         "kSlices": slices,
-        "accumulation": "f32; ascending k inside a slice; slices summed in slice order by a finishing pass"
-                        if slices > 1 else "f32; ascending k",
-    }, ["tiles-cover-output-once", "k-slices-have-partials-and-finish"])
+        "accumulation": ("f32; each of the workgroup's wavefronts sums a contiguous run of 8-wide k chunks in "
+                         "ascending order; the partials are added in wavefront order through LDS")
+                        if wide else "f32; ascending k",
+    }, ["tiles-cover-output-once", "k-slices-one-per-wavefront"])
     schedule = _artifact("schedule", {
         "launches": plan["launches"], "ldsBytes": plan["ldsBytes"], "workspaceBytes": plan["workspaceBytes"],
-        "tileOrder": "xcd-round-robin-consecutive, groups of 4 tile rows",
+        "tileOrder": "row-major" if wide else "xcd-round-robin-consecutive, groups of 4 tile rows",
     }, ["tile-order-bijection", "within-workgroup-limits"])
     gpu = 4 * (m * k + k * n + m * n) + plan["workspaceBytes"]
     host = 4 * (m * k + k * n) + 2 * 4 * m * n  # certified input copies, readback, returned bytes

@@ -72,6 +72,50 @@ def test_gemm_f32(bridge, rng, m, k, n, trans_b):
     assert ok.all(), O.report(y, ref, TOL32)
 
 
+@pytest.mark.parametrize("m,k,n", [(64, 784, 128), (64, 128, 10), (1, 129, 1), (100, 1001, 37), (512, 300, 512),
+                                   (33, 4096, 65)])
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("epi", ["plain", "bias_relu_residual", "f16_out"])
+def test_gemm_f32_wide_k(bridge, rng, m, k, n, trans_b, epi):
+    """Few output tiles and a long K take the one-launch wide-K kernel (32 x
+    32 blocks, K split over 16 wavefronts, partials summed through LDS in
+    wavefront order), with the full epilogue; against float64 truth within
+    the rounding bound of a K-term f32 sum, and the same bits on a second
+    run (fixed summation order)."""
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, k) if trans_b else (k, n)).astype(np.float32)
+    bias = rng.uniform(-1, 1, (n,)).astype(np.float32)
+    res = rng.uniform(-1, 1, (m, n)).astype(np.float32)
+    kw = dict(m=m, n=n, k=k, trans_b=trans_b, in_dtype="float32")
+    if epi == "bias_relu_residual":
+        kw.update(bias=up(bridge, bias), act=1, residual=up(bridge, res))
+    if epi == "f16_out":
+        kw.update(out_dtype="float16")
+    ha, hb = up(bridge, a), up(bridge, b)
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        h = bridge.matmul_ex(ha, hb, **kw)
+        names = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    assert [t for t in names if "gemm32_wide_k_kernel" in t] and len(names) == 1, names
+    y = bridge.to_numpy(h).astype(np.float32)
+    y2 = bridge.to_numpy(bridge.matmul_ex(ha, hb, **kw)).astype(np.float32)
+    assert np.array_equal(y, y2)
+    bm = (b.T if trans_b else b).astype(np.float64)
+    truth = a.astype(np.float64) @ bm
+    mass = np.abs(a.astype(np.float64)) @ np.abs(bm)
+    if epi == "bias_relu_residual":
+        truth = np.maximum(truth + bias, 0) + res
+        mass = mass + np.abs(bias) + np.abs(res)
+    bound = 2.0 * np.sqrt(k) * 2.0 ** -24 * mass + 1e-7
+    if epi == "f16_out":
+        bound = bound + np.abs(truth) * 2.0 ** -11  # one rounding to f16
+    err = np.abs(y - truth)
+    assert np.all(err <= bound), float(np.max(err / bound))
+
+
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("m,k,n,trans_b", [(17, 24, 19, False), (128, 64, 128, True), (256, 256, 256, False),
                                            (300, 136, 200, True), (512, 1024, 768, True)])

@@ -70,7 +70,7 @@ def test_exact_gemm_is_bit_exact(bridge, m, n, k, hi):
     # verified artifacts from the launches that ran, with their hashes
     arts = t["artifacts"]
     assert arts["layout"]["body"]["tensors"]["lhs"]["strides"] == [k, 1]
-    assert arts["schedule"]["body"]["launches"][0]["family"] == "gemm32_kernel"
+    assert arts["schedule"]["body"]["launches"][0]["family"] in ("gemm32_kernel", "gemm32_wide_k_kernel")
     for name, key in (("layout", "layoutSemanticHash"), ("tile", "kernelSemanticHash"),
                       ("schedule", "scheduleSemanticHash")):
         assert t[key] == arts[name]["hash"] == canonical_hash(arts[name]["body"])
@@ -155,10 +155,11 @@ def test_prepare_gemm_fixes_schedule_before_any_launch():
     assert prepare_semantic_gemm(300, 200, 64).backendPreparationHash == p.backendPreparationHash
     assert prepare_semantic_gemm(300, 200, 65).backendPreparationHash != p.backendPreparationHash
     s = prepare_semantic_gemm(64, 128, 784)
-    assert [l["family"] for l in s.plan["launches"]] == ["gemm32_kernel", "gemm32_splitk_reduce"]
-    assert s.plan["launches"][0]["grid"] == [1, 25, 1] and s.tile["body"]["kSlices"] == 25
-    assert "slice order" in s.tile["body"]["accumulation"]
-    assert s.plannedTransientGpuBytes == 4 * (64 * 784 + 784 * 128 + 64 * 128) + 25 * 64 * 128 * 4
+    assert s.plan["launches"] == [{"family": "gemm32_wide_k_kernel", "templateArgs": [0, 0, 0],
+                                   "grid": [8, 1, 1], "block": [1024, 1, 1]}]
+    assert s.tile["body"]["kSlices"] == 16 and "wavefront order" in s.tile["body"]["accumulation"]
+    assert s.schedule["body"]["tileOrder"] == "row-major"
+    assert s.plannedTransientGpuBytes == 4 * (64 * 784 + 784 * 128 + 64 * 128)
 
 
 @pytest.mark.parametrize("kw,path", [
@@ -253,13 +254,17 @@ def test_parse_kernel_symbol(name, args):
 
 
 def test_launch_log_must_match_the_prepared_schedule():
-    p = prepare_semantic_gemm(64, 128, 784)
-    good = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEvNS_8GemmArgsE", [1, 25, 1]),
-            _rec("_ZN12_GLOBAL__N_120gemm32_splitk_reduceILi0EEEvNS_8GemmArgsEi", [32, 1, 1])]
+    p = prepare_semantic_gemm(300, 200, 64)
+    good = [_rec("_ZN12_GLOBAL__N_113gemm32_kernelILi128ELi128ELb0ELb1EEEvNS_8GemmArgsE", [6, 1, 1])]
     check_launches(p.plan, good, "BG-WEBGPU-GEMM-VALIDATION")
-    bad_grid = [dict(good[0], grid=[1, 24, 1]), good[1]]
-    bad_args = [dict(good[0], kernel=good[0]["kernel"].replace("ELb1EE", "ELb0EE")), good[1]]
-    for bad in (bad_grid, bad_args, good[:1], good + good[1:], [good[1], good[0]]):
+    w = prepare_semantic_gemm(64, 128, 784)
+    check_launches(w.plan, [_rec("_ZN12_GLOBAL__N_120gemm32_wide_k_kernelILi0ELb0ELb0EEEvNS_8GemmArgsE", [8, 1, 1],
+                                 (1024, 1, 1))], "BG-WEBGPU-GEMM-VALIDATION")
+    bad_grid = [dict(good[0], grid=[5, 1, 1])]
+    bad_args = [dict(good[0], kernel=good[0]["kernel"].replace("ELb1EE", "ELb0EE"))]
+    bad_block = [dict(good[0], block=[512, 1, 1])]
+    other = [_rec("_ZN12_GLOBAL__N_120gemm32_wide_k_kernelILi0ELb0ELb0EEEvNS_8GemmArgsE", [6, 1, 1])]
+    for bad in (bad_grid, bad_args, bad_block, other, good + good, []):
         with pytest.raises(SemanticGemmError) as e:
             check_launches(p.plan, bad, "BG-WEBGPU-GEMM-VALIDATION")
         assert e.value.code == "BG-WEBGPU-GEMM-VALIDATION"
@@ -280,7 +285,7 @@ def test_layout_is_checked_against_device_records():
 @pytest.mark.gpu
 def test_prepared_gemm_runs_repeatably(bridge):
     """One prepared specialization, several runs: every run's launch log is
-    the prepared schedule (split K for C1's 64 x 128 x 784), its device
+    the prepared schedule (the wide-K kernel for C1's 64 x 128 x 784), its device
     records match the layout, its results are exact, and the preparation
     hash in the trace is the same every time."""
     rng = np.random.default_rng(11)

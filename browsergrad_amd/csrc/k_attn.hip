@@ -1344,6 +1344,412 @@ fa7_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
   fa7_store(P, b, h, qi, acc, l_run);
 }
 
+// ---- v8: fa7's ring and schedule on 16x16x32 MFMAs ------------------------------
+//
+// The same workgroup shapes, LDS ring, copies, barriers, reference-max rule
+// and exact recompute pass as fa7, with every product on
+// v_mfma_f32_16x16x32_{f16,bf16} instead of 32x32x16 (the 16x16 form
+// sustains more of the matrix core's nominal rate on random data than the
+// 32x32 form in this library's register-only measurements).  Per 32-key half
+// and wavefront (32 queries): S^T is 2 key blocks x 2 query blocks of 16x16,
+// two MFMAs each over d; O^T += V^T P^T is 4 d blocks x 2 query blocks, one
+// MFMA each over the half's 32 keys.
+//   * S^T accumulator layout: lane l holds rows (keys) 4 (l / 16) + i of its
+//     16-key block for query l % 16 of its query block.  So a lane's 8 P
+//     values of one query block (keys 4g + i and 16 + 4g + i, g = l / 16)
+//     are, packed, the B operand of the PV MFMA when its k-slot 8g + j means
+//     key 4g + j (j < 4) or 16 + 4g + j - 4; the V^T operand takes the same
+//     keys, read by two ds_read_b64_tr_b16 per d block (rows 4g .. 4g + 3 and
+//     16 + 4g .. 16 + 4g + 3 of the half).  P never leaves the registers.
+//   * K operand: one ds_read_b128 per (key block, d half): row 16 kb + l % 16,
+//     16-byte chunk 4 dc + l / 16.  K keeps fa7's layout (chunk c of row r at
+//     c ^ ((r >> 1) & 7)): the 16 rows one read cycle serves land on 16
+//     distinct 4-bank groups.
+//   * V rows store 32-byte block b at b ^ ((r >> 1) & 3) (chunk c at
+//     c ^ (((r >> 1) & 3) << 1)): a transpose read cycle serves two 16-lane
+//     groups, 8 rows at one 32-byte column block, and rows of one parity then
+//     take four distinct blocks (conflict-free).
+//   * The reference max is per query: the max over its first 32 keys, which
+//     four lanes (l % 16 equal) hold between them; the row sum l is kept per
+//     lane and query block and summed over those four lanes at the end.
+typedef float fa_f4 __attribute__((ext_vector_type(4)));
+
+template <bool BF16>
+__device__ __forceinline__ fa_f4 fa8_mfma(fa_u4 a, fa_u4 b, fa_f4 c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf168, a), __builtin_bit_cast(bf168, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c,
+                                                  0, 0, 0);
+}
+
+// Value of the lanes 16 and 32 apart combined by max / sum: the four lanes
+// with one l % 16 hold one query between them.
+__device__ __forceinline__ float fa8_max4(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  return fmaxf(x, __shfl_xor(x, 32, 64));
+}
+__device__ __forceinline__ float fa8_sum4(float x) {
+  x = x + __shfl_xor(x, 16, 64);
+  return x + __shfl_xor(x, 32, 64);
+}
+
+// Per-lane LDS byte offsets of the fragment reads within a tile (the key
+// block, the half and the transpose read's second row set only add
+// multiples of 2048 bytes, since rows 16 apart share both swizzles).
+struct Fa8Offs {
+  uint32_t k[2];  // d half dc: row l % 16, chunk 4 dc + l / 16
+  uint32_t v[4];  // d block db: row 4 (l / 16) + (l % 16) / 4, d = 16 db + 4 (l % 4)
+  __device__ __forceinline__ Fa8Offs() {
+    const int lane = threadIdx.x & 63, g = lane >> 4, w = lane & 15;
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc) k[dc] = uint32_t(fa2_k_unit(w, 4 * dc + g) * 16);
+    const int r = 4 * g + (w >> 2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int c = 2 * db + ((w & 3) >> 1);
+      const int pc = c ^ (((r >> 1) & 3) << 1);
+      v[db] = uint32_t(r * 128 + pc * 16 + 8 * (w & 1));
+    }
+  }
+};
+
+template <bool BF16>
+__device__ __forceinline__ void fa8_scores_half(const char* kt, const Fa8Offs& o, const fa_u4 (&qf)[2][2],
+                                                const fa_f4 (&seed)[2], int h, fa_f4 (&s)[2][2]) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    fa_u4 kf[2];
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc)
+      kf[dc] = *reinterpret_cast<const fa_u4*>(kt + o.k[dc] + h * 4096 + kb * 2048);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      s[kb][qb] = fa8_mfma<BF16>(kf[0], qf[qb][0], seed[qb]);
+      s[kb][qb] = fa8_mfma<BF16>(kf[1], qf[qb][1], s[kb][qb]);
+    }
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void fa8_pv_half(const char* vt, const Fa8Offs& o, const fa_u4 (&pf)[2], fa_f4 (&acc)[4][2],
+                                            int h) {
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    fa_v4s part[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const char* addr = vt + o.v[db] + h * 4096 + r * 2048;
+      part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) fa_v4s*)(reinterpret_cast<uintptr_t>(addr)));
+    }
+    const fa_u4 vf = __builtin_bit_cast(fa_u4, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) acc[db][qb] = fa8_mfma<BF16>(vf, pf[qb], acc[db][qb]);
+  }
+}
+
+// P of one query block: exp2 of the 8 scores (key blocks 0 and 1), packed
+// as the PV B operand; returns their f32 sum.  ROUND_S: the scores are raw
+// S, rounded to the input dtype, then scaled and shifted (negm).
+template <bool BF16, bool ROUND_S>
+__device__ __forceinline__ float fa8_exp(const fa_f4& x0, const fa_f4& x1, float sl2, float negm, fa_u4& pf) {
+  float e[8];
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    if constexpr (ROUND_S) {
+      const uint32_t a = fa2_pack<BF16>(x0[i], x0[i + 1]), b = fa2_pack<BF16>(x1[i], x1[i + 1]);
+      e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(fa2_lo<BF16>(a), sl2, negm));
+      e[i + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(fa2_hi<BF16>(a), sl2, negm));
+      e[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(fa2_lo<BF16>(b), sl2, negm));
+      e[5 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(fa2_hi<BF16>(b), sl2, negm));
+    } else {
+      e[i] = __builtin_amdgcn_exp2f(x0[i]);
+      e[i + 1] = __builtin_amdgcn_exp2f(x0[i + 1]);
+      e[4 + i] = __builtin_amdgcn_exp2f(x1[i]);
+      e[5 + i] = __builtin_amdgcn_exp2f(x1[i + 1]);
+    }
+  }
+  pf = fa_u4{fa2_pack<BF16>(e[0], e[1]), fa2_pack<BF16>(e[2], e[3]), fa2_pack<BF16>(e[4], e[5]),
+             fa2_pack<BF16>(e[6], e[7])};
+  return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+}
+
+// O = acc / l; acc[db][qb] lane l holds O^T[d = 16 db + 4 (l / 16) + i][q = 16 qb + l % 16].
+__device__ __forceinline__ void fa8_store(const Fa2Args& P, int b, int h, int q0w, const fa_f4 (&acc)[4][2],
+                                          const float (&l_run)[2]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  char* Ob = static_cast<char*>(P.o);
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float lt = fa8_sum4(l_run[qb]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    const int qi = q0w + 16 * qb + (lane & 15);
+    if (qi >= P.Sq) continue;
+    const int64_t obase = int64_t(b) * P.o_sb + int64_t(h) * P.o_sh + int64_t(qi) * P.o_ss;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int d0 = 16 * db + 4 * g;
+      if (d0 >= P.D) continue;
+      const float y0 = acc[db][qb][0] * inv, y1 = acc[db][qb][1] * inv;
+      const float y2 = acc[db][qb][2] * inv, y3 = acc[db][qb][3] * inv;
+      if (P.out_dtype == 0)
+        *reinterpret_cast<float4*>(Ob + (obase + d0) * 4) = make_float4(y0, y1, y2, y3);
+      else if (P.out_dtype == 1)
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<false>(y0, y1), fa2_pack<false>(y2, y3));
+      else
+        *reinterpret_cast<uint2*>(Ob + (obase + d0) * 2) =
+            make_uint2(fa2_pack<true>(y0, y1), fa2_pack<true>(y2, y3));
+    }
+  }
+}
+
+template <bool BF16, bool CAUSAL, int NW, int RING, bool ROUND_S>
+__global__ void __launch_bounds__(NW * 64, NW == 8 ? 4 : 3)  // the LDS-bound occupancy
+fa8_fwd_kernel(Fa2Args P, uint32_t k_bytes, uint32_t v_bytes) {
+  static_assert(NW == 8 && RING == 4, "v8 is built for the 256-query shape only");
+  constexpr int BQ = NW * kFa2QW;
+  constexpr int PARTS = 8 / NW;
+  constexpr int DMA = 2 * PARTS;
+  __shared__ fa_u4 smem[2 * RING * kFa2Tile / 16];
+  char* sb = reinterpret_cast<char*>(smem);
+  char* kring = sb;
+  char* vring = sb + RING * kFa2Tile;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4;
+  int bh, qblk;
+  fa7_block_of(int64_t(blockIdx.y) * gridDim.x + blockIdx.x, int(gridDim.x), P.n_qblocks, NW == 4, bh, qblk);
+  const int b = bh / P.H, h = bh % P.H;
+  const int q0 = qblk * BQ;
+  const int q0w = q0 + w * kFa2QW;
+
+  const uint16_t* Qp = P.q + b * P.q_sb + h * P.q_sh;
+  const uint16_t* Kp = P.k + b * P.k_sb + h * P.k_sh;
+  const uint16_t* Vp = P.v + b * P.v_sb + h * P.v_sh;
+  const bgk::sgpr4_t rk = bgk::buffer_rsrc(Kp, k_bytes);
+  const bgk::sgpr4_t rv = bgk::buffer_rsrc(Vp, v_bytes);
+
+  const int nt_all = (P.Sk + kFa2BK - 1) / kFa2BK;
+  const int nt = CAUSAL ? min(nt_all, (q0 + BQ + kFa2BK - 1) / kFa2BK) : nt_all;
+  const int ntw = CAUSAL ? min(nt, (q0w + kFa2QW + kFa2BK - 1) / kFa2BK) : nt;
+  const int t_clean = min(nt, CAUSAL ? min(P.Sk / kFa2BK, (q0 + 1) / kFa2BK) : P.Sk / kFa2BK);
+
+  // Copies as fa7's, with V's 32-byte-block swizzle.
+  uint32_t koff[PARTS], voff[PARTS];
+  int krow[PARTS];
+#pragma unroll
+  for (int p = 0; p < PARTS; ++p) {
+    const int u = (w + p * NW) * 64 + lane;
+    const int pc = u & 7;
+    krow[p] = u >> 3;
+    const int kc = pc ^ ((krow[p] >> 1) & 7), vc = pc ^ (((krow[p] >> 1) & 3) << 1);
+    koff[p] = kc * 8 < P.D ? uint32_t((int64_t(krow[p]) * P.k_ss + kc * 8) * 2) : kFa2Oob;
+    voff[p] = vc * 8 < P.D ? uint32_t((int64_t(krow[p]) * P.v_ss + vc * 8) * 2) : kFa2Oob;
+  }
+  const uint32_t kstep = uint32_t(int64_t(kFa2BK) * P.k_ss * 2);
+  const uint32_t vstep = uint32_t(int64_t(kFa2BK) * P.v_ss * 2);
+  const uint32_t kl = bgk::lds_addr(kring) + uint32_t(w) * 1024u;
+  const uint32_t vl = bgk::lds_addr(vring) + uint32_t(w) * 1024u;
+  auto issue = [&](int j) {
+    const bool real = j >= 0 && j < nt;
+    const uint32_t sl = uint32_t(j % RING) * kFa2Tile;
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p) {
+      const bool ok = real && j * kFa2BK + krow[p] < P.Sk;
+      const uint32_t at = sl + uint32_t(p * NW) * 1024u;
+      bgk::dma16_to_lds(kl + at, ok ? koff[p] : kFa2Oob, rk, real ? uint32_t(j) * kstep : 0u);
+      bgk::dma16_to_lds(vl + at, ok ? voff[p] : kFa2Oob, rv, real ? uint32_t(j) * vstep : 0u);
+    }
+  };
+
+  const float sl2 = P.sl2;
+  // Q operand: qf[qb][dc] = Q[q0w + 16 qb + l % 16][32 dc + 8 (l / 16) .. + 7].
+  fa_u4 qf[2][2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc) {
+      const int qi = q0w + 16 * qb + (lane & 15);
+      const int d0 = 32 * dc + 8 * g;
+      qf[qb][dc] = qi < P.Sq && d0 < P.D ? *reinterpret_cast<const fa_u4*>(Qp + int64_t(qi) * P.q_ss + d0)
+                                         : fa_u4{0u, 0u, 0u, 0u};
+    }
+  constexpr bool PAIRS = RING == 4;
+  if constexpr (PAIRS) {
+    issue(0);
+    issue(1);
+  } else {
+#pragma unroll
+    for (int j = 0; j < RING - 1; ++j) issue(j);
+  }
+  fa2_wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  if constexpr (PAIRS) {
+    issue(2);
+    issue(3);
+  }
+  if constexpr (!ROUND_S) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qf[qb][dc][i] = fa6_scale2<BF16>(qf[qb][dc][i], sl2);
+  }
+
+  const Fa8Offs offs;
+  // Reference max per query block: the exact maximum over keys 0..31 (key 0
+  // is always visible), combined over the four lanes of the query.
+  fa_f4 seed[2];
+  float negm[2];
+  {
+    fa_f4 zero[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) zero[qb] = fa_f4{0.f, 0.f, 0.f, 0.f};
+    fa_f4 x[2][2];
+    fa8_scores_half<BF16>(kring, offs, qf, zero, 0, x);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int qi = q0w + 16 * qb + (lane & 15);
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kj = 16 * kb + 4 * g + i;
+          const float xe = ROUND_S ? fa7_round<BF16>(x[kb][qb][i]) * sl2 : x[kb][qb][i];
+          if (!(kj >= P.Sk || (CAUSAL && kj > qi))) mt = fmaxf(mt, xe);
+        }
+      mt = fa8_max4(mt);
+      const float m_use = mt == -INFINITY ? 0.f : mt;
+      negm[qb] = -m_use;
+      const float sv = ROUND_S ? 0.f : -m_use;
+      seed[qb] = fa_f4{sv, sv, sv, sv};
+    }
+  }
+
+  fa_f4 acc[4][2];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) acc[db][qb] = fa_f4{0.f, 0.f, 0.f, 0.f};
+  float l_run[2] = {0.f, 0.f};
+
+  int t = 0;
+  for (; t < t_clean; ++t) {
+    if constexpr (PAIRS) {
+      if (t > 0 && (t & 1) == 0) {
+        fa2_wait_vm_lgkm0<0>();
+        __builtin_amdgcn_s_barrier();
+        issue(t + 2);
+        issue(t + 3);
+      }
+    } else {
+      if (t > 0) {
+        fa2_wait_vm_lgkm0<(RING - 2) * DMA>();
+        __builtin_amdgcn_s_barrier();
+      }
+      issue(t + RING - 1);
+    }
+    const char* kt = kring + (t % RING) * kFa2Tile;
+    const char* vt = vring + (t % RING) * kFa2Tile;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      fa_f4 x[2][2];
+      fa8_scores_half<BF16>(kt, offs, qf, seed, hh, x);
+      fa_u4 pf[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) l_run[qb] += fa8_exp<BF16, ROUND_S>(x[0][qb], x[1][qb], sl2, negm[qb], pf[qb]);
+      fa8_pv_half<BF16>(vt, offs, pf, acc, hh);
+    }
+  }
+  for (; t < nt; ++t) {
+    if constexpr (PAIRS) {
+      if (t > 0 && (t & 1) == 0) {
+        fa2_wait_vm_lgkm0<0>();
+        __builtin_amdgcn_s_barrier();
+        issue(t + 2);
+        issue(t + 3);
+      }
+    } else {
+      if (t > 0) {
+        fa2_wait_vm_lgkm0<(RING - 2) * DMA>();
+        __builtin_amdgcn_s_barrier();
+      }
+      issue(t + RING - 1);
+    }
+    const char* kt = kring + (t % RING) * kFa2Tile;
+    const char* vt = vring + (t % RING) * kFa2Tile;
+    if (t < ntw) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j0 = t * kFa2BK + hh * 32;
+        if (CAUSAL && j0 > q0w) break;
+        fa_f4 x[2][2];
+        fa8_scores_half<BF16>(kt, offs, qf, seed, hh, x);
+        if ((CAUSAL && j0 + 31 > q0w) || (j0 + 32 > P.Sk)) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int kj = j0 + 16 * kb + 4 * g + i;
+                const int qi = q0w + 16 * qb + (lane & 15);
+                if (kj >= P.Sk || (CAUSAL && kj > qi)) x[kb][qb][i] = -INFINITY;
+              }
+        }
+        fa_u4 pf[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          l_run[qb] += fa8_exp<BF16, ROUND_S>(x[0][qb], x[1][qb], sl2, negm[qb], pf[qb]);
+        fa8_pv_half<BF16>(vt, offs, pf, acc, hh);
+      }
+    }
+  }
+  fa2_wait_vm_lgkm0<0>();
+
+  bool bad = !(fabsf(l_run[0]) <= 3.0e38f) || !(fabsf(l_run[1]) <= 3.0e38f);
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bad |= !(fabsf(acc[db][qb][i]) <= 3.0e38f);
+  if (__any(bad)) {
+    fa7_exact<BF16, CAUSAL, ROUND_S>(P, b, h, q0w);
+    return;
+  }
+  fa8_store(P, b, h, q0w, acc, l_run);
+}
+
+// The 256-query shape runs v8 (measured against v7 on one box, C4: 87.3 /
+// 88.1 us against 90.8 / 90.5; with the score rounding 96.1 / 96.2 against
+// 99.6 / 99.0); the 128-query shape runs v7, which was faster there (C5
+// attention 26.0 / 26.2 us against 27.4 / 27.8 for v8's 128-query form,
+// which is therefore not built).  BG_ATTN_KERNEL=7 runs v7 for both.
+template <bool BF16, bool CAUSAL, bool ROUND_S>
+void launch_fa8(bg_ctx* ctx, const Fa2Args& A0, int bh, uint32_t kb, uint32_t vb) {
+  Fa2Args A = A0;
+  const int64_t big = int64_t(bh) * ((A.Sq + 255) / 256);
+  const char* force = std::getenv("BG_FA7_BLOCK");
+  const bool want256 = force && std::strcmp(force, "256") == 0;
+  const bool want128 = force && std::strcmp(force, "128") == 0;
+  if (want256 || (!want128 && big >= 768) || (A.Sq + 127) / 128 > 65535) {
+    A.n_qblocks = (A.Sq + 255) / 256;
+    bg::dispatch(ctx, fa8_fwd_kernel<BF16, CAUSAL, 8, 4, ROUND_S>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
+                 dim3(8 * 64), 0, A, kb, vb);
+  } else {
+    A.n_qblocks = (A.Sq + 127) / 128;
+    bg::dispatch(ctx, fa7_fwd_kernel<BF16, CAUSAL, 4, 3, ROUND_S>, dim3(unsigned(bh), unsigned(A.n_qblocks), 1),
+                 dim3(4 * 64), 0, A, kb, vb);
+  }
+}
+
 // 256-query workgroups when they give at least three per CU's two slots
 // (C4: 128 heads x 8 blocks); 128-query workgroups otherwise (C5: 96 heads
 // x 4 blocks of 256 would leave a 2:1 imbalance between CUs).
@@ -1372,7 +1778,8 @@ void launch_fa6(bg_ctx* ctx, const Fa2Args& A, int bh, int nqb, uint32_t kb, uin
                dim3(kFa2NW * 64), 0, A, kb, vb);
 }
 
-// BG_ATTN_KERNEL=2 selects the v2 kernel for every call, for comparisons.
+// BG_ATTN_KERNEL=2 / 6 / 7 selects the v2 / v6 / v7 kernel for every call,
+// for comparisons (default: v8 for 256-query workgroups, v7 for 128).
 // Independently of it, v6 runs only where its numerics hold: S is not
 // rounded (round_scores == 0; v2 rounds S exactly), and Q' = Q * scale *
 // log2(e) cannot overflow f16 (scale * log2(e) <= 1, so |Q'| <= |Q|).
@@ -1381,7 +1788,8 @@ int attn_version() {
     const char* e = std::getenv("BG_ATTN_KERNEL");
     if (e && e[0] == '2') return 2;
     if (e && e[0] == '6') return 6;
-    return 7;
+    if (e && e[0] == '7') return 7;
+    return 8;  // v8 for 256-query workgroups, v7 for 128-query ones
   }();
   return v;
 }
@@ -1431,7 +1839,7 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
   const bool r = d.round_scores != 0;
   const float sl2 = d.scale * 1.4426950408889634f;
   const bool fa7_takes = r || d.in_dtype == BG_BF16 || sl2 <= 1.0f;  // Q * scale * log2 e stays in f16 range
-  if (!mfma_ok || (!d64 && (attn_version() != 7 || !fa7_takes))) {
+  if (!mfma_ok || (!d64 && (attn_version() < 7 || !fa7_takes))) {
     Profile prof(ctx, "attention_generic", bytes, flops);
     launch_attention_generic(ctx, d, qp, kp, vp, nullptr, 0, 0, out.ptr(),
                              d.in_dtype != BG_F32);
@@ -1479,7 +1887,8 @@ void launch_attention(bg_ctx* ctx, const bg_attention_desc& d, const Record& q, 
     const bool fast = ver != 2 && fa7_takes;
 #define BG_FA2(B_, C_, R_)                                                                     \
   (fast ? (ver == 6 && !R_ ? launch_fa6<B_, C_>(ctx, A, bh, A.n_qblocks, kb, vb)               \
-                           : launch_fa7<B_, C_, R_>(ctx, A, bh, kb, vb))                     \
+           : ver == 7       ? launch_fa7<B_, C_, R_>(ctx, A, bh, kb, vb)                     \
+                            : launch_fa8<B_, C_, R_>(ctx, A, bh, kb, vb))                    \
         : launch_fa2<B_, C_, R_>(ctx, A, bh, A.n_qblocks, kb, vb))
     if (bf) {
       if (c) { if (r) BG_FA2(true, true, true); else BG_FA2(true, true, false); }

@@ -327,7 +327,7 @@ def test_attention_mfma_small_head_dims(bridge, rng, fa7_block, d, causal, dtype
         names = [r["kernel"] for r in bridge.take_launch_log()]
     finally:
         bridge.set_launch_log(False)
-    assert any("fa7_fwd_kernel" in t for t in names), names
+    assert any("fa7_fwd_kernel" in t or "fa8_fwd_kernel" in t for t in names), names
     y = bridge.to_numpy(ho)
     y = y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
     assert y.shape == (b, h, sq, d)
@@ -632,7 +632,7 @@ def test_attention_round_scores_is_honoured(bridge, dtype):
     # Both forms run the fast kernel; its last template argument is ROUND_S.
     def fa7(ts, rs):  # mangled (...ELb1EEEvNS_7Fa2Args...) or demangled (..., true>(...)
         flag = ("ELb1EEEv", ", true>(") if rs else ("ELb0EEEv", ", false>(")
-        return any("fa7_fwd_kernel" in t and (flag[0] in t or flag[1] in t) for t in ts)
+        return any(("fa7_fwd_kernel" in t or "fa8_fwd_kernel" in t) and (flag[0] in t or flag[1] in t) for t in ts)
     assert fa7(names[True], True), names[True]
     assert fa7(names[False], False), names[False]
     assert np.all(out[True] == 0.0), out[True][..., :4]

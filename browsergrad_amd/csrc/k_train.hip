@@ -248,34 +248,130 @@ __global__ void __launch_bounds__(256) ln_col_rows_kernel(const float* __restric
     part[int64_t(blockIdx.x) * cols + c] = ((sm[0][c] + sm[1][c]) + sm[2][c]) + sm[3][c];
 }
 
-// out[c] = sum over k < chunks of part[k][c], for 16 columns per block: the
-// 16 lanes of a column each sum every 16th partial row, then lane 0 adds
-// the 16 sums in order (deterministic, and parallel along the reduced axis).
-__global__ void __launch_bounds__(256) ln_col_final_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                           int64_t chunks, int64_t cols) {
-  __shared__ float sm[16][17];
+// out[c] = sum over k < chunks of part[k][c]: 16 columns per 1024-thread
+// block, 64 lanes per column each summing every 64th partial row (their
+// loads all in flight, 64 bytes of one partial row per 16 lanes), then one
+// lane per column adds the 64 sums in lane order (deterministic).
+__global__ void __launch_bounds__(1024) ln_col_final_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                            int64_t chunks, int64_t cols) {
+  __shared__ float sm[64][17];
   const int cl = threadIdx.x & 15;
   const int kl = threadIdx.x >> 4;
   const int64_t c = int64_t(blockIdx.x) * 16 + cl;
   float acc = 0.f;
   if (c < cols) {
     int64_t k = kl;
-    for (; k + 112 < chunks; k += 128) {  // eight independent loads per round
-      float t[8];
+    for (; k + 3 * 64 < chunks; k += 4 * 64) {
+      float t[4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = part[(k + 16 * u) * cols + c];
+      for (int u = 0; u < 4; ++u) t[u] = part[(k + 64 * u) * cols + c];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc += t[u];
+      for (int u = 0; u < 4; ++u) acc += t[u];
     }
-    for (; k < chunks; k += 16) acc += part[k * cols + c];
+    for (; k < chunks; k += 64) acc += part[k * cols + c];
   }
   sm[kl][cl] = acc;
   __syncthreads();
   if (kl == 0 && c < cols) {
     float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) t += sm[i][cl];
+#pragma unroll 8
+    for (int i = 0; i < 64; ++i) t += sm[i][cl];
     out[c] = t;
+  }
+}
+
+typedef float lnf4 __attribute__((ext_vector_type(4)));
+
+// float4 form of ln_col_rows_kernel for 4-aligned rows of at most 256 * PER4
+// columns: lane l of a wavefront owns column groups j * 64 + l (j < PER4, 4
+// columns each); a block of NW wavefronts owns NW * RPW consecutive rows,
+// wavefront w the rows w, w + NW, ...  Every load is unconditional (row and
+// group indices clamped, out-of-range values zeroed after the load), so a
+// wavefront issues all of them before its first row reduction.  The NW
+// wavefront sums are added in wavefront order through LDS into part[block].
+template <int PER4, int RPW, int NW, bool WEIGHT>
+__global__ void __launch_bounds__(NW * 64) ln_col4_kernel(const lnf4* __restrict__ dy, const lnf4* __restrict__ x,
+                                                        lnf4* __restrict__ part, int64_t rows, int64_t groups,
+                                                        float eps) {
+  __shared__ lnf4 sm[NW][64 * PER4];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const float n = float(groups * 4);
+  const int64_t r0 = int64_t(blockIdx.x) * (NW * RPW) + w;
+  lnf4 d[RPW][PER4];
+  lnf4 v[WEIGHT ? RPW : 1][PER4];
+  bool gin[PER4];
+  int64_t gc[PER4];
+#pragma unroll
+  for (int j = 0; j < PER4; ++j) {
+    gin[j] = int64_t(j) * 64 + lane < groups;
+    gc[j] = min(int64_t(j) * 64 + lane, groups - 1);
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int64_t base = min(r0 + NW * i, rows - 1) * groups;
+#pragma unroll
+    for (int j = 0; j < PER4; ++j) {
+      d[i][j] = dy[base + gc[j]];
+      if constexpr (WEIGHT) v[i][j] = x[base + gc[j]];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int j = 0; j < PER4; ++j) {
+      if (!gin[j]) d[i][j] = lnf4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (WEIGHT)
+        if (!gin[j]) v[i][j] = lnf4{0.f, 0.f, 0.f, 0.f};
+    }
+  lnf4 acc[PER4];
+#pragma unroll
+  for (int j = 0; j < PER4; ++j) acc[j] = lnf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    // Rows past the end repeat the last row (clamped above) and are dropped
+    // by selects, not by a branch: a branch would let the compiler sink
+    // their loads behind the previous row's reductions.
+    const bool rin = r0 + NW * i < rows;
+    if constexpr (WEIGHT) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER4; ++j) s += (v[i][j].x + v[i][j].y) + (v[i][j].z + v[i][j].w);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+      const float mean = s / n;
+      float q = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER4; ++j) {
+        lnf4 t = v[i][j] - mean;
+        if (!gin[j]) t = lnf4{0.f, 0.f, 0.f, 0.f};
+        v[i][j] = t;
+        q += (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+      const float inv = 1.0f / sqrtf(q / n + eps);
+#pragma unroll
+      for (int j = 0; j < PER4; ++j) {
+        const lnf4 t = acc[j] + d[i][j] * (v[i][j] * inv);
+        acc[j] = rin ? t : acc[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER4; ++j) {
+        const lnf4 t = acc[j] + d[i][j];
+        acc[j] = rin ? t : acc[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PER4; ++j) sm[w][j * 64 + lane] = acc[j];
+  __syncthreads();
+  for (int64_t g = threadIdx.x; g < groups; g += NW * 64) {
+    lnf4 t = sm[0][g];
+#pragma unroll
+    for (int u = 1; u < NW; ++u) t += sm[u][g];
+    part[int64_t(blockIdx.x) * groups + g] = t;
   }
 }
 
@@ -445,11 +541,42 @@ void launch_ln_col_rows(bg_ctx* ctx, const float* dy, const float* x, float* par
                  cols, eps);
 }
 
+template <int PER4>
+void launch_ln_col4(bg_ctx* ctx, const lnf4* dy, const lnf4* x, lnf4* part, int64_t rows, int64_t groups,
+                    int64_t blocks, float eps, bool weight) {
+  constexpr int RPW = 2, NW = 8;
+  if (weight)
+    bg::dispatch(ctx, ln_col4_kernel<PER4, RPW, NW, true>, dim3(unsigned(blocks)), dim3(NW * 64), 0, dy, x, part,
+                 rows, groups, eps);
+  else
+    bg::dispatch(ctx, ln_col4_kernel<PER4, RPW, NW, false>, dim3(unsigned(blocks)), dim3(NW * 64), 0, dy, x, part,
+                 rows, groups, eps);
+}
+
 void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float* out, int64_t rows, int64_t cols,
                              float eps, bool weight) {
   float* part;
   int64_t chunks;
-  if (cols <= 1024) {
+  const bool al4 = cols % 4 == 0 && (reinterpret_cast<uintptr_t>(dy) & 15) == 0 &&
+                   (!weight || (reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  if (al4 && cols <= 1024) {
+    // 16-byte loads, 16 rows per block (2 per wavefront, 8 wavefronts).
+    const int64_t rpb = 16;
+    chunks = (rows + rpb - 1) / rpb;
+    part = static_cast<float*>(bg::scratch(ctx, size_t(chunks * cols) * sizeof(float), 0));
+    const lnf4* dy4 = reinterpret_cast<const lnf4*>(dy);
+    const lnf4* x4 = reinterpret_cast<const lnf4*>(weight ? x : dy);
+    lnf4* p4 = reinterpret_cast<lnf4*>(part);
+    const int64_t g = cols / 4;
+    if (cols <= 256)
+      launch_ln_col4<1>(ctx, dy4, x4, p4, rows, g, chunks, eps, weight);
+    else if (cols <= 512)
+      launch_ln_col4<2>(ctx, dy4, x4, p4, rows, g, chunks, eps, weight);
+    else if (cols <= 768)
+      launch_ln_col4<3>(ctx, dy4, x4, p4, rows, g, chunks, eps, weight);
+    else
+      launch_ln_col4<4>(ctx, dy4, x4, p4, rows, g, chunks, eps, weight);
+  } else if (cols <= 1024) {
     // Rows held in registers, 16 rows per block (4 per wavefront).
     const int64_t rpb = 16;  // 4 * RPW
     chunks = (rows + rpb - 1) / rpb;
@@ -482,7 +609,7 @@ void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float
       bg::dispatch(ctx, ln_col_partial_kernel<false>, dim3(unsigned(col_blocks), unsigned(chunks)), dim3(256), 0,
                    dy, x, stats, part, rows, cols, rpc);
   }
-  bg::dispatch(ctx, ln_col_final_kernel, dim3(unsigned((cols + 15) / 16)), dim3(256), 0, part, out, chunks, cols);
+  bg::dispatch(ctx, ln_col_final_kernel, dim3(unsigned((cols + 15) / 16)), dim3(1024), 0, part, out, chunks, cols);
   hip_check(hipGetLastError(), "layer_norm_backward column launch");
 }
 

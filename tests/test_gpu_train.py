@@ -192,6 +192,41 @@ def test_layer_norm_backward_gpt2_shape_against_float64(bridge, rng):
         assert np.all(err <= bound), float(np.max(err / bound))
 
 
+def test_layer_norm_backward_columns_repeat_across_shapes(bridge, rng):
+    """Column sums over 1 to 1024 partial rows (16-byte and 4-byte pass-1
+    kernels, 256 to 1024 columns, single-block and ragged cases), called in a
+    row twice: each must match float64 sums and repeat bit for bit, so a sum
+    whose order depended on scheduling, or state left by an earlier call,
+    would show."""
+    shapes = [(16, 768), (256, 768), (300, 512), (4352, 256), (16384, 1024), (5, 4), (33, 260)]
+    first = {}
+    for rep in range(2):
+        for rows, cols in shapes:
+            r = np.random.default_rng(rows * 7 + cols)
+            x = (r.standard_normal((rows, cols)) * 1.5 + 0.25).astype(F32)
+            dy = r.standard_normal((rows, cols)).astype(F32)
+            hx, hdy = up(bridge, x), up(bridge, dy)
+            dw = fetch(bridge, bridge.layer_norm_backward_weight(hdy, hx, rows, cols, 1e-5))
+            db = fetch(bridge, bridge.layer_norm_backward_bias(hdy, rows, cols))
+            bridge.release(hx)
+            bridge.release(hdy)
+            if rep == 0:
+                # float64 sums, bound 1e-5 x the column's L1 mass (as at the
+                # GPT-2 shape: 16384-row f32 sums drift past 1e-4 relative
+                # where the column nearly cancels).
+                x64 = x.astype(np.float64)
+                mu = x64.mean(axis=1, keepdims=True)
+                xh = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+                for got, terms in ((dw, dy.astype(np.float64) * xh), (db, dy.astype(np.float64))):
+                    bound = 1e-5 * np.abs(terms).sum(axis=0) + 1e-6
+                    err = np.abs(got - terms.sum(axis=0))
+                    assert np.all(err <= bound), (rows, cols, float(np.max(err / bound)))
+                first[(rows, cols)] = (dw, db)
+            else:
+                assert np.array_equal(dw, first[(rows, cols)][0]), (rows, cols)
+                assert np.array_equal(db, first[(rows, cols)][1]), (rows, cols)
+
+
 def test_layer_norm_backward_errors(bridge):
     x = up(bridge, np.ones((2, 3), F32))
     w = up(bridge, np.ones(4, F32))

@@ -7,6 +7,8 @@ f16/bf16 MFMA paths (the tolerances BASELINE.json's north star states).
 """
 from __future__ import annotations
 
+import re
+
 import numpy as np
 import pytest
 
@@ -629,10 +631,16 @@ def test_attention_round_scores_is_honoured(bridge, dtype):
             names[rs] = [r["kernel"] for r in bridge.take_launch_log()]
     finally:
         bridge.set_launch_log(False)
-    # Both forms run the fast kernel; its last template argument is ROUND_S.
-    def fa7(ts, rs):  # mangled (...ELb1EEEvNS_7Fa2Args...) or demangled (..., true>(...)
-        flag = ("ELb1EEEv", ", true>(") if rs else ("ELb0EEEv", ", false>(")
-        return any(("fa7_fwd_kernel" in t or "fa8_fwd_kernel" in t) and (flag[0] in t or flag[1] in t) for t in ts)
+    # Both forms run the fast kernel; its fifth template argument is ROUND_S
+    # (<BF16, CAUSAL, NW, RING, ROUND_S[, queries per wavefront / 16]>).
+    def fa7(ts, rs):
+        want = "1" if rs else "0"
+        for t in ts:
+            m = (re.search(r"fa[78]_fwd_kernelILb[01]ELb[01]ELi\d+ELi\d+ELb([01])E", t)  # mangled
+                 or re.search(r"fa[78]_fwd_kernel<(?:true|false), (?:true|false), \d+, \d+, (true|false)[,>]", t))
+            if m and {"true": "1", "false": "0"}.get(m.group(1), m.group(1)) == want:
+                return True
+        return False
     assert fa7(names[True], True), names[True]
     assert fa7(names[False], False), names[False]
     assert np.all(out[True] == 0.0), out[True][..., :4]

@@ -64,6 +64,7 @@ struct ConvK {
   int sd, sh, sw, pd, ph, pw, dd, dh, dw;
   int M, NC, K;  // per-group GEMM: rows, columns, reduction
   int tiles_m, ksplit, k_chunk;
+  int b_kmajor;         // FWD ring kernel: b is w laid out [G][K][Opg]
   int64_t part_stride;  // WGRAD: floats per split slice (G * Opg * NC)
   FDiv f_oS, f_oHW, f_oW, f_S, f_HW, f_W, f_KV, f_KHW, f_KW, f_sd, f_sh, f_sw;
 };
@@ -411,7 +412,13 @@ __global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_
   const int p0 = int(od) * P.sd - P.pd, p1 = int(oh) * P.sh - P.ph, p2 = int(ow) * P.sw - P.pw;
   // B: this lane's output channel o -> w row.
   const int o = n0 + qb * 64 + lane;
-  const uint32_t b_lane = o < P.NC ? uint32_t((int64_t(g) * P.Opg + o) * K * 4) : kConvOob;
+  // w [G][Opg][K] makes one copy instruction (64 channels at one k) touch 64
+  // rows 4K bytes apart; the k-major copy [G][K][Opg] makes it 256
+  // contiguous bytes.
+  const uint32_t b_lane = o >= P.NC ? kConvOob
+                          : P.b_kmajor ? uint32_t((int64_t(g) * K * P.Opg + o) * 4)
+                                       : uint32_t((int64_t(g) * P.Opg + o) * K * 4);
+  const uint32_t b_kstride = P.b_kmajor ? uint32_t(P.Opg) * 4u : 4u;
 
   const bgk::sgpr4_t ra = bgk::buffer_rsrc(P.a, a_bytes);
   const bgk::sgpr4_t rb = bgk::buffer_rsrc(P.b, b_bytes);
@@ -441,7 +448,7 @@ __global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_
       const int kl = (i * 4 + wave) / QB;
       const int k = k0 + kl;  // uniform
       const uint32_t off = k < K ? b_lane : kConvOob;
-      conv_dma4_to_lds(bgk::lds_addr(&Bs[slot][kl * LDB + qb * 64]), off, rb, uint32_t(k < K ? k * 4 : 0));
+      conv_dma4_to_lds(bgk::lds_addr(&Bs[slot][kl * LDB + qb * 64]), off, rb, k < K ? uint32_t(k) * b_kstride : 0u);
     }
   };
 
@@ -573,6 +580,26 @@ __global__ void __launch_bounds__(256) conv_bias_final_kernel(const float* __res
 // w2[(g*Cpg + c)*Opg*KV + o*KV + kv] = w[((g*Opg + o)*Cpg + c)*KV + KV-1-kv]:
 // the weight of the forward convolution equal to a stride-1 input gradient
 // (channel roles exchanged, every spatial tap reversed).
+// wt[g][k][o] = w[g][o][k] through a 32 x 32 LDS tile (both sides coalesced).
+__global__ void __launch_bounds__(256) conv_w_kmajor_kernel(const float* __restrict__ w, float* __restrict__ wt,
+                                                            int Opg, int K) {
+  __shared__ float t[32][33];
+  const int64_t g = blockIdx.z;
+  const int k0 = int(blockIdx.x) * 32, o0 = int(blockIdx.y) * 32;
+  const int tx = int(threadIdx.x) & 31, ty = int(threadIdx.x) >> 5;
+  const float* src = w + g * Opg * int64_t(K);
+  float* dst = wt + g * int64_t(K) * Opg;
+  for (int r = ty; r < 32; r += 8) {
+    const int o = o0 + r, k = k0 + tx;
+    if (o < Opg && k < K) t[r][tx] = src[int64_t(o) * K + k];
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int k = k0 + r, o = o0 + tx;
+    if (o < Opg && k < K) dst[int64_t(k) * Opg + o] = t[tx][r];
+  }
+}
+
 __global__ void __launch_bounds__(256) conv_flip_weight_kernel(const float* __restrict__ w, float* __restrict__ w2,
                                                                int64_t G, int64_t Opg, int64_t Cpg, int64_t KV) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -708,6 +735,12 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   const bool ring = mode == 0 && a_bytes < (int64_t(1) << 31) && b_bytes < (int64_t(1) << 31) &&
                     !(ring_env && ring_env[0] == '0');
   if (ring) {
+    // The weight copied k-major first (0.6 MB for a 128 x 128 3x3 layer).
+    float* wt = static_cast<float*>(scratch(ctx, size_t(b_bytes), 2));
+    dispatch(ctx, conv_w_kmajor_kernel, dim3(unsigned((k.K + 31) / 32), unsigned((k.Opg + 31) / 32), unsigned(G)),
+             dim3(256), 0, k.b, wt, k.Opg, k.K);
+    k.b = wt;
+    k.b_kmajor = 1;
     auto go_ring = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes)); };
     if (bm == 128 && bn == 128) go_ring(conv_fwd_ring_kernel<128, 128, 4>);
     else if (bm == 128) go_ring(conv_fwd_ring_kernel<128, 64, 4>);

@@ -577,9 +577,43 @@ __global__ void __launch_bounds__(256) conv_bias_final_kernel(const float* __res
   db[o] = acc;
 }
 
-// w2[(g*Cpg + c)*Opg*KV + o*KV + kv] = w[((g*Opg + o)*Cpg + c)*KV + KV-1-kv]:
-// the weight of the forward convolution equal to a stride-1 input gradient
-// (channel roles exchanged, every spatial tap reversed).
+// db[o] = sum over (n, p) of dy[n][o][p] in one launch, one workgroup per
+// channel: thread t adds the float4 groups t, t + 1024, ... of the channel's
+// n x spatial4 groups in order, then the 1024 sums are added pairwise in a
+// fixed tree through LDS (the result does not depend on scheduling).
+__global__ void __launch_bounds__(1024) conv_bias_grad1_kernel(const float4* __restrict__ dy, float* __restrict__ db,
+                                                               int64_t n, int64_t o_count, int64_t spatial4) {
+  __shared__ float red[1024];
+  const int64_t o = blockIdx.x;
+  const int64_t total = n * spatial4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int64_t i = threadIdx.x;
+  for (; i + 3 * 1024 < total; i += 4 * 1024) {
+    float4 t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t ii = i + u * 1024;
+      const int64_t nn = ii / spatial4, q = ii - nn * spatial4;
+      t[u] = dy[(nn * o_count + o) * spatial4 + q];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += (t[u].x + t[u].y) + (t[u].z + t[u].w);
+  }
+  for (; i < total; i += 1024) {
+    const int64_t nn = i / spatial4, q = i - nn * spatial4;
+    const float4 t = dy[(nn * o_count + o) * spatial4 + q];
+    acc[0] += (t.x + t.y) + (t.z + t.w);
+  }
+  red[threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+#pragma unroll
+  for (int w = 512; w >= 1; w >>= 1) {
+    if (int(threadIdx.x) < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) db[o] = red[0];
+}
+
 // wt[g][k][o] = w[g][o][k] through a 32 x 32 LDS tile (both sides coalesced).
 __global__ void __launch_bounds__(256) conv_w_kmajor_kernel(const float* __restrict__ w, float* __restrict__ wt,
                                                             int Opg, int K) {
@@ -600,6 +634,9 @@ __global__ void __launch_bounds__(256) conv_w_kmajor_kernel(const float* __restr
   }
 }
 
+// w2[(g*Cpg + c)*Opg*KV + o*KV + kv] = w[((g*Opg + o)*Cpg + c)*KV + KV-1-kv]:
+// the weight of the forward convolution equal to a stride-1 input gradient
+// (channel roles exchanged, every spatial tap reversed).
 __global__ void __launch_bounds__(256) conv_flip_weight_kernel(const float* __restrict__ w, float* __restrict__ w2,
                                                                int64_t G, int64_t Opg, int64_t Cpg, int64_t KV) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -771,6 +808,14 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
 void launch_conv_bias_grad(bg_ctx* ctx, const float* dy, float* out, int64_t n, int64_t o, int64_t spatial) {
   if (o == 0) return;
   const int64_t rows = n * o;
+  if (spatial % 4 == 0 && (reinterpret_cast<uintptr_t>(dy) & 15) == 0 && n * (spatial / 4) <= (int64_t(1) << 16) &&
+      o <= 65535) {
+    // Up to 1 MB per channel: one workgroup per channel, one launch.
+    dispatch(ctx, conv_bias_grad1_kernel, dim3(unsigned(o)), dim3(1024), 0, reinterpret_cast<const float4*>(dy), out,
+             n, o, spatial / 4);
+    hip_check(hipGetLastError(), "conv bias-gradient launch");
+    return;
+  }
   float* part = static_cast<float*>(scratch(ctx, size_t(rows) * 4, 0));
   if (spatial % 4 == 0 && (reinterpret_cast<uintptr_t>(dy) & 15) == 0)
     dispatch(ctx, conv_row_sum4_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0,

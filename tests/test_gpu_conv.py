@@ -104,6 +104,27 @@ def test_bridge_conv2d_reference_config(bridge):
         assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
 
 
+@pytest.mark.parametrize("n,o,oh,ow", [(32, 128, 28, 28), (5, 7, 8, 8), (3, 2, 400, 250), (4, 3, 5, 7), (1, 1, 1, 4)])
+def test_conv2d_backward_bias_paths(bridge, n, o, oh, ow):
+    """The bias gradient sums dy over (n, p) per channel: one workgroup per
+    channel in one launch when rows are 4-aligned and a channel holds at most
+    2^16 float4 groups (the ResNet layer, a small grid, a 1x4 image), else
+    per-row sums then an in-order sum over n (3 x 100000 positions, 5x7
+    images).  Checked against float64 sums with a bound of 1e-5 times the
+    channel's L1 mass, and repeated bit for bit."""
+    rng = np.random.default_rng(n * 1000 + o)
+    dy = rng.standard_normal((n, o, oh, ow)).astype(F32)
+    h = up(bridge, dy)
+    gb = bridge.to_numpy(bridge.conv2d_backward_bias(h, n, o, oh, ow, "float32"))
+    gb2 = bridge.to_numpy(bridge.conv2d_backward_bias(h, n, o, oh, ow, "float32"))
+    bridge.release(h)
+    d64 = dy.astype(np.float64)
+    ref = d64.sum(axis=(0, 2, 3))
+    bound = 1e-5 * np.abs(d64).sum(axis=(0, 2, 3)) + 1e-6
+    assert np.all(np.abs(gb - ref) <= bound), float(np.max(np.abs(gb - ref) / bound))
+    assert np.array_equal(gb, gb2)
+
+
 def test_bridge_conv_errors(bridge):
     x = up(bridge, np.ones((1, 4, 9), F32))
     w = up(bridge, np.ones((6, 2, 3), F32))

@@ -622,7 +622,9 @@ def bench_train(br, steps, warmup):
     ops = {
         "adamw_update_m": ("ADAMW_UPDATE_M", ["m", "g"], 12),
         "adamw_update_v": ("ADAMW_UPDATE_V", ["v", "g"], 12),
-        "adamw_update_param": ("ADAMW_UPDATE_PARAM", ["p", "g", "m", "v"], 20),
+        # The op takes (param, grad, m', v') but its update reads no
+        # gradient: 12 B read + 4 B written per parameter.
+        "adamw_update_param": ("ADAMW_UPDATE_PARAM", ["p", "g", "m", "v"], 16),
     }
     out = {"elements": n}
     for label, (op, names, bpe) in ops.items():

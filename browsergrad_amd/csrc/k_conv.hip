@@ -772,12 +772,15 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   const bool ring = mode == 0 && a_bytes < (int64_t(1) << 31) && b_bytes < (int64_t(1) << 31) &&
                     !(ring_env && ring_env[0] == '0');
   if (ring) {
-    // The weight copied k-major first (0.6 MB for a 128 x 128 3x3 layer).
-    float* wt = static_cast<float*>(scratch(ctx, size_t(b_bytes), 2));
-    dispatch(ctx, conv_w_kmajor_kernel, dim3(unsigned((k.K + 31) / 32), unsigned((k.Opg + 31) / 32), unsigned(G)),
-             dim3(256), 0, k.b, wt, k.Opg, k.K);
-    k.b = wt;
-    k.b_kmajor = 1;
+    // The weight copied k-major first (0.6 MB for a 128 x 128 3x3 layer;
+    // the copy's grid takes the groups along z).
+    if (G <= 65535) {
+      float* wt = static_cast<float*>(scratch(ctx, size_t(b_bytes), 2));
+      dispatch(ctx, conv_w_kmajor_kernel, dim3(unsigned((k.K + 31) / 32), unsigned((k.Opg + 31) / 32), unsigned(G)),
+               dim3(256), 0, k.b, wt, k.Opg, k.K);
+      k.b = wt;
+      k.b_kmajor = 1;
+    }
     auto go_ring = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes)); };
     if (bm == 128 && bn == 128) go_ring(conv_fwd_ring_kernel<128, 128, 4>);
     else if (bm == 128) go_ring(conv_fwd_ring_kernel<128, 64, 4>);

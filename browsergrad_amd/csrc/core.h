@@ -185,8 +185,10 @@ struct ConvProblem {
 };
 // mode 0: y = conv(a = x, b = w) (+ bias[o]); 1: dx = a = dy against b = w
 // (+ bias[c]); 2: dw from a = dy, b = x.
+// b_kmajor: mode 0 only, b already laid out [G][K][Opg] (the ring kernel's
+// operand order).
 void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, const float* b, const float* bias,
-                 float* out);
+                 float* out, bool b_kmajor = false);
 void launch_conv_bias_grad(bg_ctx* ctx, const float* dy, float* out, int64_t n, int64_t o, int64_t spatial);
 void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, const float* w, float* dx,
                               int64_t rows, int64_t cols, float eps);

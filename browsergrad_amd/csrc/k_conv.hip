@@ -649,12 +649,38 @@ __global__ void __launch_bounds__(256) conv_flip_weight_kernel(const float* __re
   w2[i] = w[((g * Opg + o) * Cpg + c) * KV + (KV - 1 - kv)];
 }
 
+// The same flipped weight written k-major for the LDS-ring forward kernel:
+// w2t[g][k][c] with k = o * KV + kv (the flipped problem's reduction index)
+// and c its output channel.
+__global__ void __launch_bounds__(256) conv_flip_kmajor_kernel(const float* __restrict__ w, float* __restrict__ w2t,
+                                                               int64_t G, int64_t Opg, int64_t Cpg, int64_t KV) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t K2 = Opg * KV;
+  const int64_t total = G * K2 * Cpg;
+  if (i >= total) return;
+  const int64_t c = i % Cpg;
+  const int64_t k = (i / Cpg) % K2;
+  const int64_t g = i / (Cpg * K2);
+  const int64_t o = k / KV, kv = k % KV;
+  w2t[i] = w[((g * Opg + o) * Cpg + c) * KV + (KV - 1 - kv)];
+}
+
+// Whether the forward of problem p runs the LDS-ring kernel (x and w within
+// 32-bit byte offsets; BG_CONV_RING=0 selects the register-staged kernel).
+bool conv_fwd_ring(const bg::ConvProblem& p) {
+  const int64_t S = p.in[0] * p.in[1] * p.in[2];
+  const int64_t K = (p.c / p.groups) * p.k[0] * p.k[1] * p.k[2];
+  const int64_t a_bytes = p.n * p.c * S * 4, b_bytes = p.o * K * 4;
+  const char* ring_env = std::getenv("BG_CONV_RING");
+  return a_bytes < (int64_t(1) << 31) && b_bytes < (int64_t(1) << 31) && !(ring_env && ring_env[0] == '0');
+}
+
 }  // namespace
 
 namespace bg {
 
 void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, const float* b, const float* bias,
-                 float* out) {
+                 float* out, bool b_kmajor) {
   if (mode == 1 && p.stride[0] == 1 && p.stride[1] == 1 && p.stride[2] == 1) {
     // dx[q] = sum dy[q + pad - kv*dil] w[kv] is, with kv' = K-1-kv, the
     // forward convolution of dy by the tap-reversed, channel-exchanged
@@ -673,10 +699,13 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
       const int64_t G = p.groups, Opg = p.o / G, Cpg = p.c / G, KV = p.k[0] * p.k[1] * p.k[2];
       const int64_t total = G * Opg * Cpg * KV;
       float* w2 = static_cast<float*>(scratch(ctx, size_t(total) * 4, 1));
+      // The ring kernel takes the flipped weight k-major, written in the
+      // same pass; the register-staged kernel takes it as [G][Opg'][K'].
+      const bool km = conv_fwd_ring(f) && G <= 65535;
       if (total > 0)
-        dispatch(ctx, conv_flip_weight_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, b, w2, G, Opg,
-                 Cpg, KV);
-      launch_conv(ctx, f, 0, a, w2, bias, out);
+        dispatch(ctx, km ? conv_flip_kmajor_kernel : conv_flip_weight_kernel, dim3(unsigned((total + 255) / 256)),
+                 dim3(256), 0, b, w2, G, Opg, Cpg, KV);
+      launch_conv(ctx, f, 0, a, w2, bias, out, km);
       return;
     }
   }
@@ -768,13 +797,14 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   // Forward: the LDS-ring kernel when x and w fit 32-bit byte offsets
   // (BG_CONV_RING=0 selects the register-staged kernel, for comparisons).
   const int64_t a_bytes = p.n * int64_t(k.C) * k.S * 4, b_bytes = int64_t(k.O) * k.K * 4;
-  const char* ring_env = std::getenv("BG_CONV_RING");
-  const bool ring = mode == 0 && a_bytes < (int64_t(1) << 31) && b_bytes < (int64_t(1) << 31) &&
-                    !(ring_env && ring_env[0] == '0');
+  const bool ring = mode == 0 && conv_fwd_ring(p);
+  if (b_kmajor && !ring) fail(BG_E_UNSUPPORTED, "conv: a k-major weight reached the register-staged kernel");
   if (ring) {
     // The weight copied k-major first (0.6 MB for a 128 x 128 3x3 layer;
-    // the copy's grid takes the groups along z).
-    if (G <= 65535) {
+    // the copy's grid takes the groups along z), unless it arrives so.
+    if (b_kmajor) {
+      k.b_kmajor = 1;
+    } else if (G <= 65535) {
       float* wt = static_cast<float*>(scratch(ctx, size_t(b_bytes), 2));
       dispatch(ctx, conv_w_kmajor_kernel, dim3(unsigned((k.K + 31) / 32), unsigned((k.Opg + 31) / 32), unsigned(G)),
                dim3(256), 0, k.b, wt, k.Opg, k.K);

@@ -378,16 +378,22 @@ __device__ __forceinline__ void conv_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM, int BN, int S>
+// B16: the weight arrives k-major with Opg % 4 == 0, and its tile is copied
+// with 16-byte copies, one 1 KB instruction per 1024 / (4 BN) k rows of an
+// unpadded tile (4x fewer copy instructions for it than one 64-float row
+// per instruction).
+template <int BM, int BN, int S, bool B16>
 __global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_bytes, uint32_t b_bytes) {
-  constexpr int LDA = BM + 1, LDB = BN + 1;
+  constexpr int LDA = BM + 1, LDB = B16 ? BN : BN + 1;
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr int QA = BM / 64, QB = BN / 64;  // 64-float rows per k row
-  constexpr int IA = CBK * QA / 4, IB = CBK * QB / 4;  // instructions per wavefront per stage
+  constexpr int IA = CBK * QA / 4;           // instructions per wavefront per stage
+  constexpr int IB = B16 ? CBK * BN / 256 / 4 : CBK * QB / 4;
   constexpr int NLD = IA + IB;
   static_assert(NLD * (S - 1) < 64, "vmcnt range");
-  __shared__ float As[S][CBK * LDA];
-  __shared__ float Bs[S][CBK * LDB];
+  static_assert(!B16 || IB >= 1, "one 1 KB copy per wavefront at least");
+  __shared__ __attribute__((aligned(16))) float As[S][CBK * LDA];
+  __shared__ __attribute__((aligned(16))) float Bs[S][CBK * LDB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -419,6 +425,20 @@ __global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_
                           : P.b_kmajor ? uint32_t((int64_t(g) * K * P.Opg + o) * 4)
                                        : uint32_t((int64_t(g) * P.Opg + o) * K * 4);
   const uint32_t b_kstride = P.b_kmajor ? uint32_t(P.Opg) * 4u : 4u;
+  // B16: copy i of this wavefront fills tile floats f = (4 i + w) * 256 + 4 l
+  // .. + 3: k row f / BN, channels n0 + f % BN .. + 3 (all valid or all past
+  // NC, since NC % 4 == 0).
+  uint32_t b16_off[B16 ? IB : 1];
+  int b16_row[B16 ? IB : 1];
+  if constexpr (B16) {
+#pragma unroll
+    for (int i = 0; i < IB; ++i) {
+      const int f = (i * 4 + wave) * 256 + lane * 4;
+      b16_row[i] = f / BN;
+      const int oc = n0 + f % BN;
+      b16_off[i] = oc < P.NC ? uint32_t(((int64_t(g) * K + b16_row[i]) * P.Opg + oc) * 4) : kConvOob;
+    }
+  }
 
   const bgk::sgpr4_t ra = bgk::buffer_rsrc(P.a, a_bytes);
   const bgk::sgpr4_t rb = bgk::buffer_rsrc(P.b, b_bytes);
@@ -443,12 +463,22 @@ __global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_
           ok ? uint32_t((a_base + int64_t(c) * P.S + (int64_t(id) * P.H + ih) * P.W + iw) * 4) : kConvOob;
       conv_dma4_to_lds(bgk::lds_addr(&As[slot][kl * LDA + qa * 64]), off, ra, 0u);
     }
+    if constexpr (B16) {
 #pragma unroll
-    for (int i = 0; i < IB; ++i) {
-      const int kl = (i * 4 + wave) / QB;
-      const int k = k0 + kl;  // uniform
-      const uint32_t off = k < K ? b_lane : kConvOob;
-      conv_dma4_to_lds(bgk::lds_addr(&Bs[slot][kl * LDB + qb * 64]), off, rb, k < K ? uint32_t(k) * b_kstride : 0u);
+      for (int i = 0; i < IB; ++i) {
+        const uint32_t off = k0 + b16_row[i] < K ? b16_off[i] : kConvOob;
+        bgk::dma16_to_lds(bgk::lds_addr(&Bs[slot][(i * 4 + wave) * 256]), off, rb,
+                          k0 < K ? uint32_t(k0) * b_kstride : 0u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < IB; ++i) {
+        const int kl = (i * 4 + wave) / QB;
+        const int k = k0 + kl;  // uniform
+        const uint32_t off = k < K ? b_lane : kConvOob;
+        conv_dma4_to_lds(bgk::lds_addr(&Bs[slot][kl * LDB + qb * 64]), off, rb,
+                         k < K ? uint32_t(k) * b_kstride : 0u);
+      }
     }
   };
 
@@ -812,10 +842,15 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
       k.b_kmajor = 1;
     }
     auto go_ring = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes)); };
-    if (bm == 128 && bn == 128) go_ring(conv_fwd_ring_kernel<128, 128, 4>);
-    else if (bm == 128) go_ring(conv_fwd_ring_kernel<128, 64, 4>);
-    else if (bn == 128) go_ring(conv_fwd_ring_kernel<64, 128, 4>);
-    else go_ring(conv_fwd_ring_kernel<64, 64, 4>);
+    const bool b16 = k.b_kmajor && k.Opg % 4 == 0;
+#define BG_RING(BM_, BN_)                                      \
+  (b16 ? go_ring(conv_fwd_ring_kernel<BM_, BN_, 4, true>)      \
+       : go_ring(conv_fwd_ring_kernel<BM_, BN_, 4, false>))
+    if (bm == 128 && bn == 128) BG_RING(128, 128);
+    else if (bm == 128) BG_RING(128, 64);
+    else if (bn == 128) BG_RING(64, 128);
+    else BG_RING(64, 64);
+#undef BG_RING
     hip_check(hipGetLastError(), "conv launch");
     return;
   }

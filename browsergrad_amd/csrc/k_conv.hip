@@ -75,12 +75,13 @@ constexpr int CBK = 16;  // k-step of every tile; WGRAD slices are multiples of 
 // wavefront's (BM/2) x (BN/2) block (WGRAD: into its split slice).
 template <int MODE, int BM, int BN>
 __device__ __forceinline__ void conv_epilogue(const ConvK& P, float16v (&acc)[BM / 64][BN / 64], int m0, int n0,
-                                              int wm, int wn, int g, int split) {
+                                              int wm, int wn, int g, int split, int m_end) {
   constexpr int TM = BM / 64, TN = BN / 64;
   const int lane = threadIdx.x & 63;
   // Lane l holds rows 8*(e/4) + (e%4) + 4*(l/32) and column l%32 of each
   // 32 x 32 tile: groups of four consecutive rows, stored as one float4 when
-  // they are contiguous and aligned in the output (spatial size % 4 == 0).
+  // they are contiguous and aligned in the output (spatial size % 4 == 0 and
+  // the first row a multiple of 4).  Rows from m_end on are not stored.
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
@@ -96,12 +97,12 @@ __device__ __forceinline__ void conv_epilogue(const ConvK& P, float16v (&acc)[BM
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int row = m0 + wm * (BM / 2) + i * 32 + 8 * q + 4 * (lane >> 5);
-        if (row >= P.M) continue;
+        if (row >= m_end) continue;
         if constexpr (MODE == MODE_WGRAD) {
           float* dst = P.out + int64_t(split) * P.part_stride + (int64_t(g) * P.Opg + row) * P.NC + col;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (row + e < P.M) dst[int64_t(e) * P.NC] = acc[i][j][4 * q + e];
+            if (row + e < m_end) dst[int64_t(e) * P.NC] = acc[i][j][4 * q + e];
         } else {
           const int spatial = MODE == MODE_FWD ? P.oS : P.S;
           const int chans = MODE == MODE_FWD ? P.O : P.C;
@@ -111,7 +112,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvK& P, float16v (&acc)[BM
           float* dst = P.out + (int64_t(n) * chans + int64_t(g) * cpg + col) * spatial + sp;
           const float4 v = make_float4(acc[i][j][4 * q] + bz, acc[i][j][4 * q + 1] + bz,
                                        acc[i][j][4 * q + 2] + bz, acc[i][j][4 * q + 3] + bz);
-          if ((spatial & 3) == 0 && row + 3 < P.M) {
+          if ((spatial & 3) == 0 && (row & 3) == 0 && row + 3 < m_end) {
             *reinterpret_cast<float4*>(dst) = v;
           } else {
             // Rows may cross into the next image: place each one on its own.
@@ -119,7 +120,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvK& P, float16v (&acc)[BM
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int re = row + e;
-              if (re >= P.M) break;
+              if (re >= m_end) break;
               const uint32_t ne = fdiv(uint32_t(re), MODE == MODE_FWD ? P.f_oS : P.f_S);
               const uint32_t se = uint32_t(re) - ne * uint32_t(spatial);
               P.out[(int64_t(ne) * chans + int64_t(g) * cpg + col) * spatial + se] = vals[e];
@@ -342,7 +343,7 @@ __global__ void __launch_bounds__(256) conv_gemm_kernel(ConvK P) {
     __syncthreads();
   }
 
-  conv_epilogue<MODE, BM, BN>(P, acc, m0, n0, wm, wn, g, split);
+  conv_epilogue<MODE, BM, BN>(P, acc, m0, n0, wm, wn, g, split, P.M);
 }
 
 // Forward convolution with the operands gathered straight into an S-stage
@@ -519,7 +520,135 @@ __global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_
   }
   conv_wait_vmcnt<0>();  // the run-out copies still write LDS; let them land before exit
 
-  conv_epilogue<MODE_FWD, BM, BN>(P, acc, m0, n0, wm, wn, g, 0);
+  conv_epilogue<MODE_FWD, BM, BN>(P, acc, m0, n0, wm, wn, g, 0, P.M);
+}
+
+// ---- 3x3 stride-1 forward with input patches (2-D) --------------------------------
+//
+// The ring kernel copies, for every k = (c, tap), the 64 input values its 64
+// output rows need: nine shifted, unaligned gathers per channel.  Here a
+// 64-row tile is TR whole output rows of one image (TR = 64 / oW), and each
+// stage copies, for HC = 2 input channels, the (TR + 2) x (W + 2 pad) input
+// patch those rows read (pad columns and rows outside the image read 0), a
+// few row-contiguous copies per channel instead of nine gathers.  The A
+// operand of k = (c, kh, kw) for tile row s = r oW + cc is patch[c][(r + kh)
+// (oW + 2) + cc + kw] (stride 1, so oW + 2 = W + 2 pad).  The weight tile
+// (k-major, 18 k rows x 64 channels) streams in with 16-byte copies.  Each
+// stage is the 18 k of two channels, taken in the ring kernel's k order and
+// MFMA pairs, so the sums are bit-identical to it.
+constexpr int kHaloCB = 2;                   // channels per stage
+constexpr int kHaloKS = kHaloCB * 9;         // k per stage
+constexpr int kHaloPatchCopies = 2;          // dword copies per wavefront per stage (<= 512 floats)
+constexpr int kHaloBCopies = 2;              // 1 KB weight copies per wavefront per stage (8 KB >= 18 x 256 B)
+
+template <int S>
+__global__ void __launch_bounds__(256) conv_fwd_halo_kernel(ConvK P, uint32_t a_bytes, uint32_t b_bytes, int TR) {
+  constexpr int PATCH = 4 * kHaloPatchCopies * 64;  // floats per stage slot
+  constexpr int BTILE = 4 * kHaloBCopies * 256;     // floats per stage slot (18 x 64 used)
+  constexpr int NLD = kHaloPatchCopies + kHaloBCopies;
+  static_assert(NLD * (S - 1) < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(16))) float Ps[S][PATCH];
+  __shared__ __attribute__((aligned(16))) float Bs[S][BTILE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tm = int(blockIdx.x) % P.tiles_m, tn = int(blockIdx.x) / P.tiles_m;
+  const int g = int(blockIdx.y);
+  const int n0 = tn * 64;
+  const int K = P.K;
+  // Tile tm: image n, output rows oh0 .. oh0 + TR - 1.
+  const int tiles_per_image = (P.oH + TR - 1) / TR;
+  const int n = tm / tiles_per_image;
+  const int oh0 = (tm - n * tiles_per_image) * TR;
+  const int m0 = n * P.oS + oh0 * P.oW;
+  const int m_end = min(m0 + TR * P.oW, (n + 1) * P.oS);
+  const int PW = P.oW + 2, PR = TR + 2, PSZ = PR * PW;  // patch row width, rows, floats per channel
+
+  // A operand: this lane's tile row s = wm * 32 + lane % 32 -> patch offset.
+  const int s_row = wm * 32 + (lane & 31);
+  const int r = s_row / P.oW, cc = s_row - r * P.oW;
+  const int a_base = s_row < TR * P.oW ? r * PW + cc : 0;  // rows past the tile read row 0 (never stored)
+  // Per MFMA pair p of a stage, this lane-half's k = 2 p + lane / 32 ->
+  // (channel, kh, kw) -> patch offset.
+  int a_off[kHaloKS / 2];
+#pragma unroll
+  for (int p = 0; p < kHaloKS / 2; ++p) {
+    const int k = 2 * p + (lane >> 5);
+    const int cl = k / 9, t = k % 9;
+    a_off[p] = a_base + cl * PSZ + (t / 3) * PW + (t % 3);
+  }
+  // Patch copies: copy i of wave w fills patch floats f = (4 i + w) * 64 + l.
+  int64_t x_img = (int64_t(n) * P.C + int64_t(g) * P.Cpg) * P.S;
+  int pc_c[kHaloPatchCopies], pc_ih[kHaloPatchCopies], pc_iw[kHaloPatchCopies];
+  bool pc_ok[kHaloPatchCopies];
+#pragma unroll
+  for (int i = 0; i < kHaloPatchCopies; ++i) {
+    const int f = (i * 4 + wave) * 64 + lane;
+    const int cl = f / PSZ, rem = f - cl * PSZ;
+    const int pr = rem / PW, pcol = rem - pr * PW;
+    pc_c[i] = cl;
+    pc_ih[i] = oh0 - P.ph + pr;
+    pc_iw[i] = pcol - P.pw;
+    pc_ok[i] = cl < kHaloCB && unsigned(pc_ih[i]) < unsigned(P.H) && unsigned(pc_iw[i]) < unsigned(P.W);
+  }
+  // Weight copies (k-major [G][K][Opg], Opg % 4 == 0): copy i of wave w
+  // fills tile floats f = (4 i + w) * 256 + 4 l: k row f / 64, channels
+  // n0 + f % 64 .. + 3.
+  uint32_t b_off[kHaloBCopies];
+  int b_row[kHaloBCopies];
+#pragma unroll
+  for (int i = 0; i < kHaloBCopies; ++i) {
+    const int f = (i * 4 + wave) * 256 + lane * 4;
+    b_row[i] = f / 64;
+    const int oc = n0 + (f & 63);
+    b_off[i] = oc < P.NC && b_row[i] < kHaloKS ? uint32_t(((int64_t(g) * K + b_row[i]) * P.Opg + oc) * 4)
+                                                : kConvOob;
+  }
+
+  const bgk::sgpr4_t ra = bgk::buffer_rsrc(P.a, a_bytes);
+  const bgk::sgpr4_t rb = bgk::buffer_rsrc(P.b, b_bytes);
+  const int nk = (P.Cpg + kHaloCB - 1) / kHaloCB;
+
+  auto issue_stage = [&](int t) {
+    const int slot = t % S;
+    const int c0 = t * kHaloCB;
+#pragma unroll
+    for (int i = 0; i < kHaloPatchCopies; ++i) {
+      const bool ok = pc_ok[i] && c0 + pc_c[i] < P.Cpg;
+      const uint32_t off =
+          ok ? uint32_t((x_img + int64_t(c0 + pc_c[i]) * P.S + int64_t(pc_ih[i]) * P.W + pc_iw[i]) * 4) : kConvOob;
+      conv_dma4_to_lds(bgk::lds_addr(&Ps[slot][(i * 4 + wave) * 64]), off, ra, 0u);
+    }
+    const int k0 = c0 * 9;
+#pragma unroll
+    for (int i = 0; i < kHaloBCopies; ++i) {
+      const uint32_t off = k0 + b_row[i] < K ? b_off[i] : kConvOob;
+      bgk::dma16_to_lds(bgk::lds_addr(&Bs[slot][(i * 4 + wave) * 256]), off, rb,
+                        k0 < K ? uint32_t(k0) * uint32_t(P.Opg) * 4u : 0u);
+    }
+  };
+
+  float16v acc[1][1];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[0][0][e] = 0.f;
+
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t) issue_stage(t);
+  for (int kt = 0; kt < nk; ++kt) {
+    conv_wait_vmcnt<NLD * (S - 2)>();
+    __syncthreads();
+    issue_stage(kt + S - 1);
+    const int buf = kt % S;
+#pragma unroll
+    for (int p = 0; p < kHaloKS / 2; ++p) {
+      const float af = Ps[buf][a_off[p]];
+      const float bf = Bs[buf][(2 * p + (lane >> 5)) * 64 + wn * 32 + (lane & 31)];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(af, bf, acc[0][0], 0, 0, 0);
+    }
+  }
+  conv_wait_vmcnt<0>();  // the run-out copies still write LDS; let them land before exit
+
+  conv_epilogue<MODE_FWD, 64, 64>(P, acc, m0, n0, wm, wn, g, 0, m_end);
 }
 
 // dw[i] = sum over split slices (in order) of part[s][i].
@@ -841,8 +970,22 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
       k.b = wt;
       k.b_kmajor = 1;
     }
-    auto go_ring = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes)); };
     const bool b16 = k.b_kmajor && k.Opg % 4 == 0;
+    // 3x3, stride 1, dilation 1, 2-D, output rows of at most 64: tiles of
+    // whole output rows fed from input patches (BG_CONV_HALO=0 keeps the
+    // ring kernel, for comparisons).
+    const char* halo_env = std::getenv("BG_CONV_HALO");
+    const int tr = k.oW > 0 && k.oW <= 64 ? 64 / k.oW : 0;
+    if (b16 && k.D == 1 && k.oD == 1 && k.KD == 1 && k.KH == 3 && k.KW == 3 && k.sh == 1 && k.sw == 1 &&
+        k.dh == 1 && k.dw == 1 && tr > 0 && kHaloCB * (tr + 2) * (k.oW + 2) <= 4 * kHaloPatchCopies * 64 &&
+        !(halo_env && halo_env[0] == '0')) {
+      k.tiles_m = int(p.n * ((k.oH + tr - 1) / tr));
+      const dim3 hgrid(unsigned(int64_t(k.tiles_m) * ((k.NC + 63) / 64)), unsigned(G));
+      dispatch(ctx, conv_fwd_halo_kernel<4>, hgrid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes), tr);
+      hip_check(hipGetLastError(), "conv launch");
+      return;
+    }
+    auto go_ring = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes)); };
 #define BG_RING(BM_, BN_)                                      \
   (b16 ? go_ring(conv_fwd_ring_kernel<BM_, BN_, 4, true>)      \
        : go_ring(conv_fwd_ring_kernel<BM_, BN_, 4, false>))

@@ -409,9 +409,11 @@ def test_conv2d_large_against_float64(bridge, case):
         assert np.all(err <= bound), float(np.max(err / bound))
 
 
-def test_conv_ring_wide_tiles_launched(bridge):
+def test_conv_ring_wide_tiles_launched(bridge, monkeypatch):
     """BIG's last case runs the ring kernel's 128 x 128 shape (forward) and
-    128 x 64 shape (stride-1 input gradient), as the launch log shows."""
+    128 x 64 shape (stride-1 input gradient), as the launch log shows (with
+    the 3x3 input-patch kernel switched off: it takes this shape by default)."""
+    monkeypatch.setenv("BG_CONV_HALO", "0")
     n, ci, hw, co, k, s, p = BIG[-1]
     rng = np.random.default_rng(5)
     x = rng.standard_normal((n, ci) + hw).astype(F32)
@@ -448,6 +450,7 @@ def test_conv_ring_64x128_tiles(bridge, monkeypatch):
     kw = dict(n=n, c_in=ci, c_out=co, in_size=hw, out_size=hw, k=k, stride=(1, 1), pad=(1, 1), dilation=(1, 1),
               groups=g)
     monkeypatch.setenv("BG_CONV_RING", "1")
+    monkeypatch.setenv("BG_CONV_HALO", "0")
     bridge.set_launch_log(True)
     try:
         bridge.take_launch_log()
@@ -466,6 +469,58 @@ def test_conv_ring_64x128_tiles(bridge, monkeypatch):
     mass = F.conv2d(xt.abs(), wt.abs(), bt.abs(), padding=1, groups=g).numpy()
     err = np.abs(y - y64)
     assert np.all(err <= _bound(y64, mass, cpg * 9)), float(np.max(err / _bound(y64, mass, cpg * 9)))
+
+
+HALO = [
+    # n, c_in, (H, W), c_out, pad, groups
+    (2, 5, (28, 28), 12, (1, 1), 1),    # two output rows per tile, odd channel count
+    (3, 4, (18, 18), 8, (1, 1), 1),     # 54-row tiles: every other one starts off a multiple of 4
+    (2, 6, (7, 9), 16, (1, 1), 2),      # groups; 63 of the 64 tile rows used
+    (1, 3, (64, 64), 68, (1, 1), 1),    # one output row per tile; a second column tile
+    (2, 4, (10, 12), 4, (0, 0), 1),     # no padding; the last tile of each image is partial
+    (1, 2, (5, 3), 8, (2, 2), 1),       # padding 2: whole patch rows and columns outside the image
+    (1, 9, (1, 1), 4, (1, 1), 1),       # a 1 x 1 image
+    (32, 128, (28, 28), 128, (1, 1), 1),  # the benchmark layer (register kernel only, no oracle)
+]
+
+
+@pytest.mark.parametrize("case", HALO)
+def test_conv3x3_input_patch_kernel(bridge, case, monkeypatch):
+    """3x3 stride-1 2-D convolutions with output rows of at most 64 run on
+    the input-patch kernel (the launch log shows it; the stride-1 input
+    gradient too, when c_in per group is a multiple of 4).  It takes the
+    ring kernel's k order and MFMA pairs, so it is bit-identical to the
+    register-staged kernel (BG_CONV_RING=0), and it matches the oracle."""
+    n, ci, hw, co, p, g = case
+    k, s, d = (3, 3), (1, 1), (1, 1)
+    rng = np.random.default_rng(n * 1000 + ci * 10 + co)
+    x = rng.standard_normal((n, ci) + hw).astype(F32)
+    w = rng.standard_normal((co, ci // g) + k).astype(F32)
+    b = rng.standard_normal(co).astype(F32)
+    out = _out_size(hw, k, s, p, d)
+    dy = rng.standard_normal((n, co) + out).astype(F32)
+    kw = dict(n=n, c_in=ci, c_out=co, in_size=hw, out_size=out, k=k, stride=s, pad=p, dilation=d, groups=g)
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        y = conv_ex(bridge, "forward", x, w, b, **kw)
+        fwd = [r["kernel"] for r in bridge.take_launch_log()]
+        gx = conv_ex(bridge, "backward_input", dy, w, **kw)
+        bwd = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    assert any("conv_fwd_halo_kernel" in t for t in fwd), fwd
+    if (ci // g) % 4 == 0:
+        assert any("conv_fwd_halo_kernel" in t for t in bwd), bwd
+    monkeypatch.setenv("BG_CONV_RING", "0")
+    y0 = conv_ex(bridge, "forward", x, w, b, **kw)
+    gx0 = conv_ex(bridge, "backward_input", dy, w, **kw)
+    assert np.array_equal(y, y0)
+    assert np.array_equal(gx, gx0)
+    if n * ci * hw[0] * hw[1] <= 1 << 16:
+        for got, ref in ((y, O.conv_forward(x, w, b, s, p, d, g, out)),
+                         (gx, O.conv_backward_input(dy, w, s, p, d, g, hw))):
+            assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
 
 
 @pytest.mark.parametrize("shape", [(4, 16, 28, 28), (3, 5, 7, 7), (2, 3, 4, 300)])

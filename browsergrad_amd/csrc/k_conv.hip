@@ -527,34 +527,43 @@ __global__ void __launch_bounds__(256) conv_fwd_ring_kernel(ConvK P, uint32_t a_
 //
 // The ring kernel copies, for every k = (c, tap), the 64 input values its 64
 // output rows need: nine shifted, unaligned gathers per channel.  Here a
-// 64-row tile is TR whole output rows of one image (TR = 64 / oW), and each
-// stage copies, for HC = 2 input channels, the (TR + 2) x (W + 2 pad) input
+// BM-row tile is TR whole output rows of one image (TR = BM / oW), and each
+// stage copies, for CB input channels, the (TR + 2) x (W + 2 pad) input
 // patch those rows read (pad columns and rows outside the image read 0), a
 // few row-contiguous copies per channel instead of nine gathers.  The A
 // operand of k = (c, kh, kw) for tile row s = r oW + cc is patch[c][(r + kh)
 // (oW + 2) + cc + kw] (stride 1, so oW + 2 = W + 2 pad).  The weight tile
-// (k-major, 18 k rows x 64 channels) streams in with 16-byte copies.  Each
-// stage is the 18 k of two channels, taken in the ring kernel's k order and
-// MFMA pairs, so the sums are bit-identical to it.
-constexpr int kHaloCB = 2;                   // channels per stage
-constexpr int kHaloKS = kHaloCB * 9;         // k per stage
-constexpr int kHaloPatchCopies = 2;          // dword copies per wavefront per stage (<= 512 floats)
-constexpr int kHaloBCopies = 2;              // 1 KB weight copies per wavefront per stage (8 KB >= 18 x 256 B)
-
-template <int S>
-__global__ void __launch_bounds__(256) conv_fwd_halo_kernel(ConvK P, uint32_t a_bytes, uint32_t b_bytes, int TR) {
-  constexpr int PATCH = 4 * kHaloPatchCopies * 64;  // floats per stage slot
-  constexpr int BTILE = 4 * kHaloBCopies * 256;     // floats per stage slot (18 x 64 used)
-  constexpr int NLD = kHaloPatchCopies + kHaloBCopies;
+// (k-major, 9 CB k rows x BN channels) streams in with 16-byte copies.  Each
+// stage is the 9 CB k of CB channels (CB even, so every stage starts on an
+// even k), taken in the ring kernel's k order and MFMA pairs, so the sums
+// are bit-identical to it.
+//
+// WM wavefronts along M (BM = 32 WM tile rows) and WN along N (BN = 32 WN
+// columns), each with one 32 x 32 accumulator; PC dword copies per
+// wavefront per stage hold the CB patches.  Weight copies past
+// the tile's rows land in a scratch area of LDS nobody reads, so that every
+// wavefront issues the same number of copies per stage (the vmcnt waits
+// count them).
+template <int S, int CB, int WM, int WN, int PC>
+__global__ void __launch_bounds__(64 * WM * WN) conv_fwd_halo_kernel(ConvK P, uint32_t a_bytes, uint32_t b_bytes,
+                                                                     int TR) {
+  constexpr int NW = WM * WN, BN = 32 * WN, KS = 9 * CB;
+  static_assert(CB % 2 == 0, "stages must start on even k");
+  constexpr int PATCH = PC * NW * 64;               // floats per stage slot
+  constexpr int BCOPIES = (KS * BN + 255) / 256;    // 1 KB copies that hold the weight tile
+  constexpr int BC = (BCOPIES + NW - 1) / NW;       // per wavefront
+  constexpr int NLD = PC + BC;
   static_assert(NLD * (S - 1) < 64, "vmcnt range");
   __shared__ __attribute__((aligned(16))) float Ps[S][PATCH];
-  __shared__ __attribute__((aligned(16))) float Bs[S][BTILE];
+  __shared__ __attribute__((aligned(16))) float Bs[S][BCOPIES * 256];
+  __shared__ __attribute__((aligned(16))) float Bsink[NW * BC > BCOPIES ? 256 : 4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int tm = int(blockIdx.x) % P.tiles_m, tn = int(blockIdx.x) / P.tiles_m;
+  const int wm = wave % WM, wn = wave / WM;
+  const int tiles_n = (P.NC + BN - 1) / BN;
+  const int tn = int(blockIdx.x) % tiles_n, tm = int(blockIdx.x) / tiles_n;
   const int g = int(blockIdx.y);
-  const int n0 = tn * 64;
+  const int n0 = tn * BN;
   const int K = P.K;
   // Tile tm: image n, output rows oh0 .. oh0 + TR - 1.
   const int tiles_per_image = (P.oH + TR - 1) / TR;
@@ -562,7 +571,7 @@ __global__ void __launch_bounds__(256) conv_fwd_halo_kernel(ConvK P, uint32_t a_
   const int oh0 = (tm - n * tiles_per_image) * TR;
   const int m0 = n * P.oS + oh0 * P.oW;
   const int m_end = min(m0 + TR * P.oW, (n + 1) * P.oS);
-  const int PW = P.oW + 2, PR = TR + 2, PSZ = PR * PW;  // patch row width, rows, floats per channel
+  const int PW = P.oW + 2, PSZ = (TR + 2) * PW;  // patch row width, floats per channel
 
   // A operand: this lane's tile row s = wm * 32 + lane % 32 -> patch offset.
   const int s_row = wm * 32 + (lane & 31);
@@ -570,61 +579,64 @@ __global__ void __launch_bounds__(256) conv_fwd_halo_kernel(ConvK P, uint32_t a_
   const int a_base = s_row < TR * P.oW ? r * PW + cc : 0;  // rows past the tile read row 0 (never stored)
   // Per MFMA pair p of a stage, this lane-half's k = 2 p + lane / 32 ->
   // (channel, kh, kw) -> patch offset.
-  int a_off[kHaloKS / 2];
+  int a_off[KS / 2];
 #pragma unroll
-  for (int p = 0; p < kHaloKS / 2; ++p) {
+  for (int p = 0; p < KS / 2; ++p) {
     const int k = 2 * p + (lane >> 5);
     const int cl = k / 9, t = k % 9;
     a_off[p] = a_base + cl * PSZ + (t / 3) * PW + (t % 3);
   }
-  // Patch copies: copy i of wave w fills patch floats f = (4 i + w) * 64 + l.
-  int64_t x_img = (int64_t(n) * P.C + int64_t(g) * P.Cpg) * P.S;
-  int pc_c[kHaloPatchCopies], pc_ih[kHaloPatchCopies], pc_iw[kHaloPatchCopies];
-  bool pc_ok[kHaloPatchCopies];
+  // Patch copies: copy i of wave w fills patch floats f = (NW i + w) * 64 + l.
+  const int64_t x_img = (int64_t(n) * P.C + int64_t(g) * P.Cpg) * P.S;
+  int pc_c[PC], pc_src[PC];
+  bool pc_ok[PC];
 #pragma unroll
-  for (int i = 0; i < kHaloPatchCopies; ++i) {
-    const int f = (i * 4 + wave) * 64 + lane;
+  for (int i = 0; i < PC; ++i) {
+    const int f = (i * NW + wave) * 64 + lane;
     const int cl = f / PSZ, rem = f - cl * PSZ;
     const int pr = rem / PW, pcol = rem - pr * PW;
+    const int ih = oh0 - P.ph + pr, iw = pcol - P.pw;
     pc_c[i] = cl;
-    pc_ih[i] = oh0 - P.ph + pr;
-    pc_iw[i] = pcol - P.pw;
-    pc_ok[i] = cl < kHaloCB && unsigned(pc_ih[i]) < unsigned(P.H) && unsigned(pc_iw[i]) < unsigned(P.W);
+    pc_src[i] = ih * P.W + iw;
+    pc_ok[i] = cl < CB && unsigned(ih) < unsigned(P.H) && unsigned(iw) < unsigned(P.W);
   }
-  // Weight copies (k-major [G][K][Opg], Opg % 4 == 0): copy i of wave w
-  // fills tile floats f = (4 i + w) * 256 + 4 l: k row f / 64, channels
-  // n0 + f % 64 .. + 3.
-  uint32_t b_off[kHaloBCopies];
-  int b_row[kHaloBCopies];
+  // Weight copies (k-major [G][K][Opg], Opg % 4 == 0): copy c = NW i + w
+  // fills tile floats f = 256 c + 4 l: k row f / BN, channels n0 + f % BN
+  // .. + 3.
+  uint32_t b_off[BC];
+  int b_row[BC];
+  uint32_t b_lds[BC];
 #pragma unroll
-  for (int i = 0; i < kHaloBCopies; ++i) {
-    const int f = (i * 4 + wave) * 256 + lane * 4;
-    b_row[i] = f / 64;
-    const int oc = n0 + (f & 63);
-    b_off[i] = oc < P.NC && b_row[i] < kHaloKS ? uint32_t(((int64_t(g) * K + b_row[i]) * P.Opg + oc) * 4)
-                                                : kConvOob;
+  for (int i = 0; i < BC; ++i) {
+    const int c = i * NW + wave;
+    const int f = c * 256 + lane * 4;
+    b_row[i] = f / BN;
+    const int oc = n0 + f % BN;
+    b_off[i] = c < BCOPIES && oc < P.NC && b_row[i] < KS ? uint32_t(((int64_t(g) * K + b_row[i]) * P.Opg + oc) * 4)
+                                                          : kConvOob;
+    if (c >= BCOPIES) b_row[i] = K;  // never in range
+    b_lds[i] = c < BCOPIES ? uint32_t(c * 256 * 4) : 0u;
   }
 
   const bgk::sgpr4_t ra = bgk::buffer_rsrc(P.a, a_bytes);
   const bgk::sgpr4_t rb = bgk::buffer_rsrc(P.b, b_bytes);
-  const int nk = (P.Cpg + kHaloCB - 1) / kHaloCB;
+  const int nk = (P.Cpg + CB - 1) / CB;
 
   auto issue_stage = [&](int t) {
     const int slot = t % S;
-    const int c0 = t * kHaloCB;
+    const int c0 = t * CB;
 #pragma unroll
-    for (int i = 0; i < kHaloPatchCopies; ++i) {
+    for (int i = 0; i < PC; ++i) {
       const bool ok = pc_ok[i] && c0 + pc_c[i] < P.Cpg;
-      const uint32_t off =
-          ok ? uint32_t((x_img + int64_t(c0 + pc_c[i]) * P.S + int64_t(pc_ih[i]) * P.W + pc_iw[i]) * 4) : kConvOob;
-      conv_dma4_to_lds(bgk::lds_addr(&Ps[slot][(i * 4 + wave) * 64]), off, ra, 0u);
+      const uint32_t off = ok ? uint32_t((x_img + int64_t(c0 + pc_c[i]) * P.S + pc_src[i]) * 4) : kConvOob;
+      conv_dma4_to_lds(bgk::lds_addr(&Ps[slot][(i * NW + wave) * 64]), off, ra, 0u);
     }
     const int k0 = c0 * 9;
 #pragma unroll
-    for (int i = 0; i < kHaloBCopies; ++i) {
+    for (int i = 0; i < BC; ++i) {
       const uint32_t off = k0 + b_row[i] < K ? b_off[i] : kConvOob;
-      bgk::dma16_to_lds(bgk::lds_addr(&Bs[slot][(i * 4 + wave) * 256]), off, rb,
-                        k0 < K ? uint32_t(k0) * uint32_t(P.Opg) * 4u : 0u);
+      const uint32_t dst = i * NW + wave < BCOPIES ? bgk::lds_addr(&Bs[slot][0]) + b_lds[i] : bgk::lds_addr(&Bsink[0]);
+      bgk::dma16_to_lds(dst, off, rb, k0 < K ? uint32_t(k0) * uint32_t(P.Opg) * 4u : 0u);
     }
   };
 
@@ -640,15 +652,17 @@ __global__ void __launch_bounds__(256) conv_fwd_halo_kernel(ConvK P, uint32_t a_
     issue_stage(kt + S - 1);
     const int buf = kt % S;
 #pragma unroll
-    for (int p = 0; p < kHaloKS / 2; ++p) {
+    for (int p = 0; p < KS / 2; ++p) {
       const float af = Ps[buf][a_off[p]];
-      const float bf = Bs[buf][(2 * p + (lane >> 5)) * 64 + wn * 32 + (lane & 31)];
+      const float bf = Bs[buf][(2 * p + (lane >> 5)) * BN + wn * 32 + (lane & 31)];
       acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(af, bf, acc[0][0], 0, 0, 0);
     }
   }
   conv_wait_vmcnt<0>();  // the run-out copies still write LDS; let them land before exit
 
-  conv_epilogue<MODE_FWD, 64, 64>(P, acc, m0, n0, wm, wn, g, 0, m_end);
+  // Wavefront (wm, wn) holds rows m0 + 32 wm .. + 31 and columns n0 + 32 wn
+  // .. + 31: wavefront (0, 0) of a 64 x 64 epilogue placed there.
+  conv_epilogue<MODE_FWD, 64, 64>(P, acc, m0 + wm * 32, n0 + wn * 32, 0, 0, g, 0, m_end);
 }
 
 // dw[i] = sum over split slices (in order) of part[s][i].
@@ -971,19 +985,42 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
       k.b_kmajor = 1;
     }
     const bool b16 = k.b_kmajor && k.Opg % 4 == 0;
-    // 3x3, stride 1, dilation 1, 2-D, output rows of at most 64: tiles of
-    // whole output rows fed from input patches (BG_CONV_HALO=0 keeps the
-    // ring kernel, for comparisons).
+    // 3x3, stride 1, dilation 1, 2-D: tiles of whole output rows fed from
+    // input patches, 128 x 64 (eight wavefronts) where two channels' patches
+    // fit 512 floats and the grid still has a workgroup per CU, else 64 x 64
+    // (BG_CONV_HALO=0 keeps the ring kernel; =64 or =128 asks for that tile
+    // height where it fits, for comparisons).
     const char* halo_env = std::getenv("BG_CONV_HALO");
-    const int tr = k.oW > 0 && k.oW <= 64 ? 64 / k.oW : 0;
+    const int halo_ask = halo_env ? std::atoi(halo_env) : -1;
+    auto halo_rows = [&](int bm) {  // output rows per tile, 0 if the patches do not fit
+      const int tr = k.oW > 0 ? bm / k.oW : 0;
+      return tr > 0 && 2 * (tr + 2) * (k.oW + 2) <= 512 ? tr : 0;
+    };
     if (b16 && k.D == 1 && k.oD == 1 && k.KD == 1 && k.KH == 3 && k.KW == 3 && k.sh == 1 && k.sw == 1 &&
-        k.dh == 1 && k.dw == 1 && tr > 0 && kHaloCB * (tr + 2) * (k.oW + 2) <= 4 * kHaloPatchCopies * 64 &&
-        !(halo_env && halo_env[0] == '0')) {
-      k.tiles_m = int(p.n * ((k.oH + tr - 1) / tr));
-      const dim3 hgrid(unsigned(int64_t(k.tiles_m) * ((k.NC + 63) / 64)), unsigned(G));
-      dispatch(ctx, conv_fwd_halo_kernel<4>, hgrid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes), tr);
-      hip_check(hipGetLastError(), "conv launch");
-      return;
+        k.dh == 1 && k.dw == 1 && halo_ask != 0) {
+      const int64_t tiles_n64 = (k.NC + 63) / 64;
+      const int tr128 = halo_rows(128), tr64 = halo_rows(64);
+      int bm = 0;
+      if (halo_ask == 128 || halo_ask == 64) {
+        bm = halo_rows(halo_ask) ? halo_ask : 0;
+      } else if (tr128 && p.n * ((k.oH + tr128 - 1) / tr128) * tiles_n64 * G >= 256) {
+        bm = 128;
+      } else if (tr64) {
+        bm = 64;
+      }
+      if (bm) {
+        const int tr = bm == 128 ? tr128 : tr64;
+        k.tiles_m = int(p.n * ((k.oH + tr - 1) / tr));
+        const dim3 hgrid(unsigned(int64_t(k.tiles_m) * tiles_n64), unsigned(G));
+        if (bm == 128)
+          dispatch(ctx, conv_fwd_halo_kernel<4, 2, 4, 2, 1>, hgrid, dim3(512), 0, k, uint32_t(a_bytes),
+                   uint32_t(b_bytes), tr);
+        else
+          dispatch(ctx, conv_fwd_halo_kernel<4, 2, 2, 2, 2>, hgrid, dim3(256), 0, k, uint32_t(a_bytes),
+                   uint32_t(b_bytes), tr);
+        hip_check(hipGetLastError(), "conv launch");
+        return;
+      }
     }
     auto go_ring = [&](auto kern) { dispatch(ctx, kern, grid, dim3(256), 0, k, uint32_t(a_bytes), uint32_t(b_bytes)); };
 #define BG_RING(BM_, BN_)                                      \

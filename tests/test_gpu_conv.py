@@ -476,7 +476,8 @@ HALO = [
     (2, 5, (28, 28), 12, (1, 1), 1),    # two output rows per tile, odd channel count
     (3, 4, (18, 18), 8, (1, 1), 1),     # 54-row tiles: every other one starts off a multiple of 4
     (2, 6, (7, 9), 16, (1, 1), 2),      # groups; 63 of the 64 tile rows used
-    (1, 3, (64, 64), 68, (1, 1), 1),    # one output row per tile; a second column tile
+    (1, 3, (64, 64), 68, (1, 1), 1),    # one output row per 64-row tile; a second column tile
+    (2, 4, (40, 40), 8, (1, 1), 1),     # three output rows per 128-row tile (120 of 128 used)
     (2, 4, (10, 12), 4, (0, 0), 1),     # no padding; the last tile of each image is partial
     (1, 2, (5, 3), 8, (2, 2), 1),       # padding 2: whole patch rows and columns outside the image
     (1, 9, (1, 1), 4, (1, 1), 1),       # a 1 x 1 image
@@ -484,13 +485,28 @@ HALO = [
 ]
 
 
+def _halo_fits(bm, ow):
+    tr = bm // ow
+    return tr > 0 and 2 * (tr + 2) * (ow + 2) <= 512
+
+
+def _halo_tile(names):
+    """Tile height of the input-patch kernel in a launch log (0 if absent)."""
+    for t in names:
+        if "conv_fwd_halo_kernel" in t:
+            return 128 if ("ILi4ELi2ELi4ELi2ELi1E" in t or "<4, 2, 4, 2, 1>" in t) else 64
+    return 0
+
+
 @pytest.mark.parametrize("case", HALO)
 def test_conv3x3_input_patch_kernel(bridge, case, monkeypatch):
-    """3x3 stride-1 2-D convolutions with output rows of at most 64 run on
-    the input-patch kernel (the launch log shows it; the stride-1 input
-    gradient too, when c_in per group is a multiple of 4).  It takes the
-    ring kernel's k order and MFMA pairs, so it is bit-identical to the
-    register-staged kernel (BG_CONV_RING=0), and it matches the oracle."""
+    """3x3 stride-1 2-D convolutions run on the input-patch kernel, in
+    128 x 64 or 64 x 64 tiles (BG_CONV_HALO=128 / =64 ask for one where
+    the two channels' patches fit; the launch log shows which ran; the
+    stride-1 input gradient takes it too when c_in per group is a multiple
+    of 4).  Both take the ring kernel's k order and MFMA pairs, so they are
+    bit-identical to the register-staged kernel (BG_CONV_RING=0), and they
+    match the oracle."""
     n, ci, hw, co, p, g = case
     k, s, d = (3, 3), (1, 1), (1, 1)
     rng = np.random.default_rng(n * 1000 + ci * 10 + co)
@@ -500,26 +516,41 @@ def test_conv3x3_input_patch_kernel(bridge, case, monkeypatch):
     out = _out_size(hw, k, s, p, d)
     dy = rng.standard_normal((n, co) + out).astype(F32)
     kw = dict(n=n, c_in=ci, c_out=co, in_size=hw, out_size=out, k=k, stride=s, pad=p, dilation=d, groups=g)
-    bridge.set_launch_log(True)
-    try:
-        bridge.take_launch_log()
-        y = conv_ex(bridge, "forward", x, w, b, **kw)
-        fwd = [r["kernel"] for r in bridge.take_launch_log()]
-        gx = conv_ex(bridge, "backward_input", dy, w, **kw)
-        bwd = [r["kernel"] for r in bridge.take_launch_log()]
-    finally:
-        bridge.set_launch_log(False)
-    assert any("conv_fwd_halo_kernel" in t for t in fwd), fwd
-    if (ci // g) % 4 == 0:
-        assert any("conv_fwd_halo_kernel" in t for t in bwd), bwd
+    runs = {}
+    for ask in ("", "64", "128"):
+        if ask and not _halo_fits(int(ask), out[1]):
+            continue
+        if ask:
+            monkeypatch.setenv("BG_CONV_HALO", ask)
+        bridge.set_launch_log(True)
+        try:
+            bridge.take_launch_log()
+            y = conv_ex(bridge, "forward", x, w, b, **kw)
+            fwd = [r["kernel"] for r in bridge.take_launch_log()]
+            gx = conv_ex(bridge, "backward_input", dy, w, **kw)
+            bwd = [r["kernel"] for r in bridge.take_launch_log()]
+        finally:
+            bridge.set_launch_log(False)
+        if ask:
+            assert _halo_tile(fwd) == int(ask), fwd
+        else:  # 128-row tiles where they fit and still give a workgroup per CU
+            tr = 128 // out[1]
+            tiles = n * -(-out[0] // tr) * -(-(co // g) // 64) * g if tr else 0
+            assert _halo_tile(fwd) == (128 if _halo_fits(128, out[1]) and tiles >= 256 else 64), fwd
+        if (ci // g) % 4 == 0 and _halo_fits(64, hw[1]):
+            assert _halo_tile(bwd), bwd
+        runs[ask] = (y, gx)
+    assert "128" in runs or "64" in runs
     monkeypatch.setenv("BG_CONV_RING", "0")
+    monkeypatch.delenv("BG_CONV_HALO", raising=False)
     y0 = conv_ex(bridge, "forward", x, w, b, **kw)
     gx0 = conv_ex(bridge, "backward_input", dy, w, **kw)
-    assert np.array_equal(y, y0)
-    assert np.array_equal(gx, gx0)
+    for y, gx in runs.values():
+        assert np.array_equal(y, y0)
+        assert np.array_equal(gx, gx0)
     if n * ci * hw[0] * hw[1] <= 1 << 16:
-        for got, ref in ((y, O.conv_forward(x, w, b, s, p, d, g, out)),
-                         (gx, O.conv_backward_input(dy, w, s, p, d, g, hw))):
+        for got, ref in ((y0, O.conv_forward(x, w, b, s, p, d, g, out)),
+                         (gx0, O.conv_backward_input(dy, w, s, p, d, g, hw))):
             assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
 
 

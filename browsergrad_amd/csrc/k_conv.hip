@@ -947,12 +947,16 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   const int64_t tiles_n = (k.NC + bn - 1) / bn;
   const int64_t tiles = int64_t(k.tiles_m) * tiles_n;
   if (mode == 2) {
-    // Split the (n, p) reduction so that about 1024 workgroups run (the
-    // kernel is latency-bound per workgroup), each over at least 8 k-steps,
-    // and at most 64 slices, whose partial sums a second kernel adds in order.
+    // Split the (n, p) reduction into at most 128 slices, whose partial sums
+    // a second kernel adds in order, each over at least 8 k-steps, so that
+    // at most 512 workgroups run: two per CU.  A CU's time is the slices it
+    // holds times the slice length, so the grid stays within a whole number
+    // of workgroups per CU (a 3x3 128 -> 128 layer over 32 x 28 x 28: 567
+    // workgroups of 25 k-steps run in 136 us, 621 of 23 in 128 us, 504 of
+    // 28 in 113 us).
     const int64_t steps = (int64_t(k.K) + CBK - 1) / CBK;
-    int64_t splits = std::max<int64_t>(1, std::min<int64_t>(1024 / std::max<int64_t>(tiles * G, 1), steps / 8));
-    splits = std::min<int64_t>(splits, 64);
+    int64_t splits = std::max<int64_t>(1, std::min<int64_t>(512 / std::max<int64_t>(tiles * G, 1), steps / 8));
+    splits = std::min<int64_t>(splits, 128);
     splits = std::min<int64_t>(splits, 65535 / G);
     const int64_t chunk_steps = (steps + splits - 1) / std::max<int64_t>(splits, 1);
     k.k_chunk = int(std::max<int64_t>(chunk_steps, 1) * CBK);

@@ -554,6 +554,32 @@ def test_conv3x3_input_patch_kernel(bridge, case, monkeypatch):
             assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
 
 
+def test_conv3x3_input_patch_output_beyond_formula(bridge, monkeypatch):
+    """A caller-given output larger than the formula's (8 x 7 from a 6 x 6
+    input with padding 1) reads zeros past the input, as the reference's
+    bounds-checked loop does; the input-patch kernel runs it (launch log),
+    bit-identical to the register-staged kernel and equal to the oracle."""
+    rng = np.random.default_rng(87)
+    x = rng.standard_normal((2, 4, 6, 6)).astype(F32)
+    w = rng.standard_normal((8, 4, 3, 3)).astype(F32)
+    b = rng.standard_normal(8).astype(F32)
+    kw = dict(n=2, c_in=4, c_out=8, in_size=(6, 6), out_size=(8, 7), k=(3, 3), stride=(1, 1), pad=(1, 1),
+              dilation=(1, 1), groups=1)
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        y = conv_ex(bridge, "forward", x, w, b, **kw)
+        names = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    assert _halo_tile(names), names
+    ref = O.conv_forward(x, w, b, (1, 1), (1, 1), (1, 1), 1, (8, 7))
+    assert y.shape == ref.shape == (2, 8, 8, 7)
+    assert O.within(y, ref, TOL).all(), O.report(y, ref, TOL)
+    monkeypatch.setenv("BG_CONV_RING", "0")
+    assert np.array_equal(y, conv_ex(bridge, "forward", x, w, b, **kw))
+
+
 @pytest.mark.parametrize("shape", [(4, 16, 28, 28), (3, 5, 7, 7), (2, 3, 4, 300)])
 def test_bias_gradient_float4_and_scalar_rows(bridge, shape):
     """Spatial sizes that are multiples of 4 (784, 1200) take the float4 row

@@ -991,9 +991,11 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
     const bool b16 = k.b_kmajor && k.Opg % 4 == 0;
     // 3x3, stride 1, dilation 1, 2-D: tiles of whole output rows fed from
     // input patches, 128 x 64 (eight wavefronts) where two channels' patches
-    // fit 512 floats and the grid still has a workgroup per CU, else 64 x 64
-    // (BG_CONV_HALO=0 keeps the ring kernel; =64 or =128 asks for that tile
-    // height where it fits, for comparisons).
+    // fit 512 floats, the grid still has a workgroup per CU and the tiles
+    // use as many of their rows as 64-row ones would, else 64 x 64 (a 7 x 7
+    // image fills 49 of 128 rows but 49 of 64: 211 against 158 us on a
+    // 32 x 512 x 7 x 7 layer).  BG_CONV_HALO=0 keeps the ring kernel; =64 or
+    // =128 asks for that tile height where it fits, for comparisons.
     const char* halo_env = std::getenv("BG_CONV_HALO");
     const int halo_ask = halo_env ? std::atoi(halo_env) : -1;
     auto halo_rows = [&](int bm) {  // output rows per tile, 0 if the patches do not fit
@@ -1007,7 +1009,10 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
       int bm = 0;
       if (halo_ask == 128 || halo_ask == 64) {
         bm = halo_rows(halo_ask) ? halo_ask : 0;
-      } else if (tr128 && p.n * ((k.oH + tr128 - 1) / tr128) * tiles_n64 * G >= 256) {
+      } else if (tr128 && p.n * ((k.oH + tr128 - 1) / tr128) * tiles_n64 * G >= 256 &&
+                 (!tr64 || int64_t((k.oH + tr64 - 1) / tr64) * 64 >= int64_t((k.oH + tr128 - 1) / tr128) * 128)) {
+        // (rows of an image's 64-row tiles >= rows of its 128-row tiles: no
+        // more of the larger tiles is left empty)
         bm = 128;
       } else if (tr64) {
         bm = 64;

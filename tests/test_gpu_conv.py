@@ -482,6 +482,7 @@ HALO = [
     (1, 2, (5, 3), 8, (2, 2), 1),       # padding 2: whole patch rows and columns outside the image
     (1, 9, (1, 1), 4, (1, 1), 1),       # a 1 x 1 image
     (32, 128, (28, 28), 128, (1, 1), 1),  # the benchmark layer (register kernel only, no oracle)
+    (32, 8, (7, 7), 512, (1, 1), 1),    # 7 x 7 images: 64-row tiles (49 of 64 rows) though 128 would fill the CUs
 ]
 
 
@@ -533,10 +534,12 @@ def test_conv3x3_input_patch_kernel(bridge, case, monkeypatch):
             bridge.set_launch_log(False)
         if ask:
             assert _halo_tile(fwd) == int(ask), fwd
-        else:  # 128-row tiles where they fit and still give a workgroup per CU
+        else:  # 128-row tiles where they fit, give a workgroup per CU and leave no more rows empty
             tr = 128 // out[1]
             tiles = n * -(-out[0] // tr) * -(-(co // g) // 64) * g if tr else 0
-            assert _halo_tile(fwd) == (128 if _halo_fits(128, out[1]) and tiles >= 256 else 64), fwd
+            tr64 = 64 // out[1]
+            use = (not _halo_fits(64, out[1])) or -(-out[0] // tr64) * 64 >= -(-out[0] // max(tr, 1)) * 128
+            assert _halo_tile(fwd) == (128 if _halo_fits(128, out[1]) and tiles >= 256 and use else 64), fwd
         if (ci // g) % 4 == 0 and _halo_fits(64, hw[1]):
             assert _halo_tile(bwd), bwd
         runs[ask] = (y, gx)
@@ -548,10 +551,19 @@ def test_conv3x3_input_patch_kernel(bridge, case, monkeypatch):
     for y, gx in runs.values():
         assert np.array_equal(y, y0)
         assert np.array_equal(gx, gx0)
-    if n * ci * hw[0] * hw[1] <= 1 << 16:
+    if n * ci * hw[0] * hw[1] <= 1 << 16 and co * 9 <= 600:
         for got, ref in ((y0, O.conv_forward(x, w, b, s, p, d, g, out)),
                          (gx0, O.conv_backward_input(dy, w, s, p, d, g, hw))):
             assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
+    elif n * ci * hw[0] * hw[1] <= 1 << 16:
+        # Long input-gradient sums (co * 9 terms): float64 with the sqrt(K) bound.
+        xt, wt, dyt = (torch.tensor(t, dtype=torch.float64) for t in (x, w, dy))
+        y64 = F.conv2d(xt, wt, torch.tensor(b, dtype=torch.float64), padding=p, groups=g).numpy()
+        ym = F.conv2d(xt.abs(), wt.abs(), torch.tensor(np.abs(b), dtype=torch.float64), padding=p, groups=g).numpy()
+        gx64 = torch.nn.grad.conv2d_input(xt.shape, wt, dyt, padding=p, groups=g).numpy()
+        gxm = torch.nn.grad.conv2d_input(xt.shape, wt.abs(), dyt.abs(), padding=p, groups=g).numpy()
+        for got, truth, mass, kk in ((y0, y64, ym, (ci // g) * 9), (gx0, gx64, gxm, (co // g) * 9)):
+            assert np.all(np.abs(got - truth) <= _bound(truth, mass, kk))
 
 
 def test_conv3x3_input_patch_output_beyond_formula(bridge, monkeypatch):

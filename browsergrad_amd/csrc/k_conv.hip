@@ -998,9 +998,12 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
     // =128 asks for that tile height where it fits, for comparisons.
     const char* halo_env = std::getenv("BG_CONV_HALO");
     const int halo_ask = halo_env ? std::atoi(halo_env) : -1;
-    auto halo_rows = [&](int bm) {  // output rows per tile, 0 if the patches do not fit
+    // Output rows per tile, 0 if two channels' patches do not fit the tile's
+    // copies: 512 floats, or 1024 for 128-row tiles with two copies per
+    // wavefront (output rows of 84 to 128).
+    auto halo_rows = [&](int bm) {
       const int tr = k.oW > 0 ? bm / k.oW : 0;
-      return tr > 0 && 2 * (tr + 2) * (k.oW + 2) <= 512 ? tr : 0;
+      return tr > 0 && 2 * (tr + 2) * (k.oW + 2) <= (bm == 128 ? 1024 : 512) ? tr : 0;
     };
     if (b16 && k.D == 1 && k.oD == 1 && k.KD == 1 && k.KH == 3 && k.KW == 3 && k.sh == 1 && k.sw == 1 &&
         k.dh == 1 && k.dw == 1 && halo_ask != 0) {
@@ -1009,10 +1012,12 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
       int bm = 0;
       if (halo_ask == 128 || halo_ask == 64) {
         bm = halo_rows(halo_ask) ? halo_ask : 0;
-      } else if (tr128 && p.n * ((k.oH + tr128 - 1) / tr128) * tiles_n64 * G >= 256 &&
-                 (!tr64 || int64_t((k.oH + tr64 - 1) / tr64) * 64 >= int64_t((k.oH + tr128 - 1) / tr128) * 128)) {
+      } else if (tr128 && (!tr64 || (p.n * ((k.oH + tr128 - 1) / tr128) * tiles_n64 * G >= 256 &&
+                                      int64_t((k.oH + tr64 - 1) / tr64) * 64 >=
+                                          int64_t((k.oH + tr128 - 1) / tr128) * 128))) {
         // (rows of an image's 64-row tiles >= rows of its 128-row tiles: no
-        // more of the larger tiles is left empty)
+        // more of the larger tiles is left empty; rows past 64 have only
+        // the larger tiles)
         bm = 128;
       } else if (tr64) {
         bm = 64;
@@ -1021,7 +1026,10 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
         const int tr = bm == 128 ? tr128 : tr64;
         k.tiles_m = int(p.n * ((k.oH + tr - 1) / tr));
         const dim3 hgrid(unsigned(int64_t(k.tiles_m) * tiles_n64), unsigned(G));
-        if (bm == 128)
+        if (bm == 128 && 2 * (tr + 2) * (k.oW + 2) > 512)
+          dispatch(ctx, conv_fwd_halo_kernel<4, 2, 4, 2, 2>, hgrid, dim3(512), 0, k, uint32_t(a_bytes),
+                   uint32_t(b_bytes), tr);
+        else if (bm == 128)
           dispatch(ctx, conv_fwd_halo_kernel<4, 2, 4, 2, 1>, hgrid, dim3(512), 0, k, uint32_t(a_bytes),
                    uint32_t(b_bytes), tr);
         else

@@ -483,19 +483,20 @@ HALO = [
     (1, 9, (1, 1), 4, (1, 1), 1),       # a 1 x 1 image
     (32, 128, (28, 28), 128, (1, 1), 1),  # the benchmark layer (register kernel only, no oracle)
     (32, 8, (7, 7), 512, (1, 1), 1),    # 7 x 7 images: 64-row tiles (49 of 64 rows) though 128 would fill the CUs
+    (1, 3, (100, 112), 8, (1, 1), 1),   # 112-wide rows: 128-row tiles with two patch copies per wavefront
 ]
 
 
 def _halo_fits(bm, ow):
     tr = bm // ow
-    return tr > 0 and 2 * (tr + 2) * (ow + 2) <= 512
+    return tr > 0 and 2 * (tr + 2) * (ow + 2) <= (1024 if bm == 128 else 512)
 
 
 def _halo_tile(names):
     """Tile height of the input-patch kernel in a launch log (0 if absent)."""
     for t in names:
         if "conv_fwd_halo_kernel" in t:
-            return 128 if ("ILi4ELi2ELi4ELi2ELi1E" in t or "<4, 2, 4, 2, 1>" in t) else 64
+            return 128 if any(f"ILi4ELi2ELi4ELi2ELi{pc}E" in t or f"<4, 2, 4, 2, {pc}>" in t for pc in (1, 2)) else 64
     return 0
 
 
@@ -538,8 +539,9 @@ def test_conv3x3_input_patch_kernel(bridge, case, monkeypatch):
             tr = 128 // out[1]
             tiles = n * -(-out[0] // tr) * -(-(co // g) // 64) * g if tr else 0
             tr64 = 64 // out[1]
-            use = (not _halo_fits(64, out[1])) or -(-out[0] // tr64) * 64 >= -(-out[0] // max(tr, 1)) * 128
-            assert _halo_tile(fwd) == (128 if _halo_fits(128, out[1]) and tiles >= 256 and use else 64), fwd
+            big = _halo_fits(128, out[1]) and (not _halo_fits(64, out[1]) or (
+                tiles >= 256 and -(-out[0] // tr64) * 64 >= -(-out[0] // tr) * 128))
+            assert _halo_tile(fwd) == (128 if big else 64), fwd
         if (ci // g) % 4 == 0 and _halo_fits(64, hw[1]):
             assert _halo_tile(bwd), bwd
         runs[ask] = (y, gx)

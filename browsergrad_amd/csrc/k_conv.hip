@@ -949,13 +949,13 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   if (mode == 2) {
     // Split the (n, p) reduction into at most 128 slices, whose partial sums
     // a second kernel adds in order, each over at least 8 k-steps, so that
-    // at most 512 workgroups run: two per CU.  A CU's time is the slices it
-    // holds times the slice length, so the grid stays within a whole number
-    // of workgroups per CU (a 3x3 128 -> 128 layer over 32 x 28 x 28: 567
-    // workgroups of 25 k-steps run in 136 us, 621 of 23 in 128 us, 504 of
-    // 28 in 113 us).
+    // about 768 workgroups run (three per CU).  A CU's time follows the
+    // slices it holds times the slice length: on the ResNet 3x3 layers the
+    // former rule (1024 workgroups, at most 64 slices) and a 512-workgroup
+    // one each lose 5-20% somewhere (e.g. 32 x 128 x 28 x 28: 145 / 124 /
+    // 119 us; 128 x 512 x 7 x 7: 406 / 491 / 400 us).
     const int64_t steps = (int64_t(k.K) + CBK - 1) / CBK;
-    int64_t splits = std::max<int64_t>(1, std::min<int64_t>(512 / std::max<int64_t>(tiles * G, 1), steps / 8));
+    int64_t splits = std::max<int64_t>(1, std::min<int64_t>(768 / std::max<int64_t>(tiles * G, 1), steps / 8));
     splits = std::min<int64_t>(splits, 128);
     splits = std::min<int64_t>(splits, 65535 / G);
     const int64_t chunk_steps = (steps + splits - 1) / std::max<int64_t>(splits, 1);

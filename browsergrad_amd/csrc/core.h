@@ -183,12 +183,18 @@ struct ConvProblem {
   int64_t n, c, o, groups;
   int64_t in[3], out[3], k[3], stride[3], pad[3], dil[3];
 };
+// Where a forward convolution's outputs go when they are one phase of a
+// larger tensor: output (oh, ow) lands at (oh * sh + ph, ow * sw + pw) of an
+// H x W plane (used by the strided input gradient's phase convolutions).
+struct ConvOutMap {
+  int sh, sw, ph, pw, H, W;
+};
 // mode 0: y = conv(a = x, b = w) (+ bias[o]); 1: dx = a = dy against b = w
 // (+ bias[c]); 2: dw from a = dy, b = x.
 // b_kmajor: mode 0 only, b already laid out [G][K][Opg] (the ring kernel's
-// operand order).
+// operand order).  omap: mode 0 only, 2-D, the outputs' phase placement.
 void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, const float* b, const float* bias,
-                 float* out, bool b_kmajor = false);
+                 float* out, bool b_kmajor = false, const ConvOutMap* omap = nullptr);
 void launch_conv_bias_grad(bg_ctx* ctx, const float* dy, float* out, int64_t n, int64_t o, int64_t spatial);
 void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, const float* w, float* dx,
                               int64_t rows, int64_t cols, float eps);

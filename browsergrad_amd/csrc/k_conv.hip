@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
+#include <vector>
 
 #include "common.cuh"
 #include "core.h"
@@ -65,6 +66,7 @@ struct ConvK {
   int M, NC, K;  // per-group GEMM: rows, columns, reduction
   int tiles_m, ksplit, k_chunk;
   int b_kmajor;         // FWD ring kernel: b is w laid out [G][K][Opg]
+  int om, om_sh, om_sw, om_ph, om_pw, om_H, om_W;  // FWD: outputs are one phase of an om_H x om_W plane
   int64_t part_stride;  // WGRAD: floats per split slice (G * Opg * NC)
   FDiv f_oS, f_oHW, f_oW, f_S, f_HW, f_W, f_KV, f_KHW, f_KW, f_sd, f_sh, f_sw;
 };
@@ -107,6 +109,23 @@ __device__ __forceinline__ void conv_epilogue(const ConvK& P, float16v (&acc)[BM
           const int spatial = MODE == MODE_FWD ? P.oS : P.S;
           const int chans = MODE == MODE_FWD ? P.O : P.C;
           const int cpg = MODE == MODE_FWD ? P.Opg : P.Cpg;
+          if constexpr (MODE == MODE_FWD) {
+            if (P.om) {
+              // One phase of a larger 2-D output: output (oh, ow) goes to
+              // (oh * om_sh + om_ph, ow * om_sw + om_pw).
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int re = row + e;
+                if (re >= m_end) break;
+                const uint32_t ne = fdiv(uint32_t(re), P.f_oS);
+                const uint32_t se = uint32_t(re) - ne * uint32_t(P.oS);
+                const uint32_t oh = fdiv(se, P.f_oW), ow = se - oh * uint32_t(P.oW);
+                P.out[(int64_t(ne) * chans + int64_t(g) * cpg + col) * (int64_t(P.om_H) * P.om_W) +
+                      int64_t(oh * P.om_sh + P.om_ph) * P.om_W + ow * P.om_sw + P.om_pw] = acc[i][j][4 * q + e] + bz;
+              }
+              continue;
+            }
+          }
           const uint32_t n = fdiv(uint32_t(row), MODE == MODE_FWD ? P.f_oS : P.f_S);
           const uint32_t sp = uint32_t(row) - n * uint32_t(spatial);
           float* dst = P.out + (int64_t(n) * chans + int64_t(g) * cpg + col) * spatial + sp;
@@ -838,6 +857,44 @@ __global__ void __launch_bounds__(256) conv_flip_kmajor_kernel(const float* __re
   w2t[i] = w[((g * Opg + o) * Cpg + c) * KV + (KV - 1 - kv)];
 }
 
+// Weight of one phase convolution of a strided input gradient, k-major for
+// the ring kernel: wt[(g*K' + o*KVp + th*KWp + tw)*Cpg + c] =
+// w[((g*Opg + o)*Cpg + c)*KH*KW + kh[th]*KW + kw[tw]] (K' = Opg*KVp; the
+// phase's taps in the order the phase convolution reads them).
+struct PhaseTaps {
+  int khp, kwp;
+  int kh[16], kw[16];
+};
+
+__global__ void __launch_bounds__(256) conv_phase_weight_kernel(const float* __restrict__ w, float* __restrict__ wt,
+                                                                int64_t G, int64_t Opg, int64_t Cpg, int KH, int KW,
+                                                                PhaseTaps t) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t kvp = int64_t(t.khp) * t.kwp;
+  const int64_t total = G * Opg * kvp * Cpg;
+  if (i >= total) return;
+  const int64_t c = i % Cpg;
+  const int64_t k = (i / Cpg) % (Opg * kvp);
+  const int64_t g = i / (Cpg * Opg * kvp);
+  const int64_t o = k / kvp, tv = k % kvp;
+  const int th = int(tv / t.kwp), tw = int(tv % t.kwp);
+  wt[i] = w[((g * Opg + o) * Cpg + c) * (int64_t(KH) * KW) + t.kh[th] * KW + t.kw[tw]];
+}
+
+// A phase of dx that no tap reaches: dx[n][c][y*sh + ph][x*sw + pw] =
+// bias[c] (or 0), for y < Hph, x < Wph.
+__global__ void __launch_bounds__(256) conv_phase_fill_kernel(float* __restrict__ dx, const float* __restrict__ bias,
+                                                              int64_t NC, int64_t C, int H, int W, int sh, int sw,
+                                                              int ph, int pw, int Hph, int Wph) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t per = int64_t(Hph) * Wph;
+  if (i >= NC * per) return;
+  const int64_t nc = i / per;
+  const int r = int(i % per);
+  const int y = r / Wph, x = r % Wph;
+  dx[nc * (int64_t(H) * W) + int64_t(y * sh + ph) * W + x * sw + pw] = bias ? bias[nc % C] : 0.f;
+}
+
 // Whether the forward of problem p runs the LDS-ring kernel (x and w within
 // 32-bit byte offsets; BG_CONV_RING=0 selects the register-staged kernel).
 bool conv_fwd_ring(const bg::ConvProblem& p) {
@@ -852,8 +909,96 @@ bool conv_fwd_ring(const bg::ConvProblem& p) {
 
 namespace bg {
 
+// Strided 2-D input gradient as stride_h x stride_w phase convolutions.
+// dx[y][x] with y = sh*i + ry, x = sw*j + rx takes only the taps kh with
+// kh = ry + pad_h (mod sh) (and likewise kw), at dy[i + (ry + pad_h - kh)/sh]
+// [j + (rx + pad_w - kw)/sw]: for each phase (ry, rx) a dense stride-1
+// forward convolution of dy by that phase's taps (channel roles
+// exchanged), written to the phase's positions of dx.  The implicit GEMM of
+// the DGRAD kernel visits every (tap, position) pair and finds a term in
+// only 1 / (sh sw) of them.  False when the problem does not fit this form
+// (3-D, dilation, operands past the ring kernel's 32-bit offsets);
+// BG_CONV_DGRAD_PHASES=0 keeps the DGRAD kernel.
+static bool launch_dgrad_phases(bg_ctx* ctx, const ConvProblem& p, const float* dy, const float* w,
+                                const float* bias, float* dx) {
+  const char* env = std::getenv("BG_CONV_DGRAD_PHASES");
+  if (env && env[0] == '0') return false;
+  if (p.in[0] != 1 || p.out[0] != 1 || p.k[0] != 1 || p.stride[0] != 1 || p.dil[1] != 1 || p.dil[2] != 1) return false;
+  const int64_t G = p.groups, Opg = p.o / G, Cpg = p.c / G;
+  const int sh = int(p.stride[1]), sw = int(p.stride[2]);
+  const int KH = int(p.k[1]), KW = int(p.k[2]);
+  const int H = int(p.in[1]), W = int(p.in[2]);
+  if (KH > 16 || KW > 16 || G > 65535 || p.n <= 0 || H <= 0 || W <= 0) return false;
+  struct Phase {
+    int ry, rx, hph, wph, padh, padw;
+    PhaseTaps t;
+  };
+  std::vector<Phase> phases;
+  int64_t max_w = 0;
+  for (int ry = 0; ry < sh && ry < H; ++ry) {
+    for (int rx = 0; rx < sw && rx < W; ++rx) {
+      Phase f{};
+      f.ry = ry;
+      f.rx = rx;
+      f.hph = (H - ry + sh - 1) / sh;
+      f.wph = (W - rx + sw - 1) / sw;
+      // Taps in descending kh: ascending dy row offset (ry + pad - kh) / sh.
+      for (int kh = KH - 1; kh >= 0; --kh)
+        if (((ry + int(p.pad[1]) - kh) % sh + sh) % sh == 0) f.t.kh[f.t.khp++] = kh;
+      for (int kw = KW - 1; kw >= 0; --kw)
+        if (((rx + int(p.pad[2]) - kw) % sw + sw) % sw == 0) f.t.kw[f.t.kwp++] = kw;
+      if (f.t.khp > 0 && f.t.kwp > 0) {
+        // Leading padding of the phase convolution; negative when the
+        // phase's first tap reads past dy's first row / column (the ring
+        // kernel's index arithmetic is signed, its bounds checks unsigned).
+        f.padh = (f.t.kh[0] - ry - int(p.pad[1])) / sh;
+        f.padw = (f.t.kw[0] - rx - int(p.pad[2])) / sw;
+        max_w = std::max<int64_t>(max_w, G * Opg * f.t.khp * f.t.kwp * Cpg);
+        ConvProblem q{};
+        q.n = p.n;
+        q.c = p.o;
+        q.o = p.c;
+        q.groups = G;
+        q.in[0] = 1; q.in[1] = p.out[1]; q.in[2] = p.out[2];
+        q.k[0] = 1; q.k[1] = f.t.khp; q.k[2] = f.t.kwp;
+        if (!conv_fwd_ring(q)) return false;
+      }
+      phases.push_back(f);
+    }
+  }
+  float* wt = max_w > 0 ? static_cast<float*>(scratch(ctx, size_t(max_w) * 4, 1)) : nullptr;
+  for (const Phase& f : phases) {
+    if (f.t.khp == 0 || f.t.kwp == 0) {
+      const int64_t total = p.n * p.c * int64_t(f.hph) * f.wph;
+      if (total > 0)
+        dispatch(ctx, conv_phase_fill_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, dx, bias,
+                 p.n * p.c, p.c, H, W, sh, sw, f.ry, f.rx, f.hph, f.wph);
+      continue;
+    }
+    const int64_t total = G * Opg * f.t.khp * f.t.kwp * Cpg;
+    dispatch(ctx, conv_phase_weight_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, w, wt, G, Opg, Cpg,
+             KH, KW, f.t);
+    ConvProblem q{};
+    q.n = p.n;
+    q.c = p.o;
+    q.o = p.c;
+    q.groups = G;
+    q.in[0] = 1; q.in[1] = p.out[1]; q.in[2] = p.out[2];
+    q.out[0] = 1; q.out[1] = f.hph; q.out[2] = f.wph;
+    q.k[0] = 1; q.k[1] = f.t.khp; q.k[2] = f.t.kwp;
+    q.stride[0] = q.stride[1] = q.stride[2] = 1;
+    q.pad[0] = 0; q.pad[1] = f.padh; q.pad[2] = f.padw;
+    q.dil[0] = q.dil[1] = q.dil[2] = 1;
+    const ConvOutMap m{sh, sw, f.ry, f.rx, H, W};
+    launch_conv(ctx, q, 0, dy, wt, bias, dx, true, &m);
+  }
+  hip_check(hipGetLastError(), "conv launch");
+  return true;
+}
+
 void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, const float* b, const float* bias,
-                 float* out, bool b_kmajor) {
+                 float* out, bool b_kmajor, const ConvOutMap* omap) {
+  if (mode == 1 && (p.stride[1] > 1 || p.stride[2] > 1) && launch_dgrad_phases(ctx, p, a, b, bias, out)) return;
   if (mode == 1 && p.stride[0] == 1 && p.stride[1] == 1 && p.stride[2] == 1) {
     // dx[q] = sum dy[q + pad - kv*dil] w[kv] is, with kv' = K-1-kv, the
     // forward convolution of dy by the tap-reversed, channel-exchanged
@@ -886,6 +1031,16 @@ void launch_conv(bg_ctx* ctx, const ConvProblem& p, int mode, const float* a, co
   k.a = a;
   k.b = b;
   k.bias = bias;
+  if (omap) {
+    if (mode != 0 || p.in[0] != 1 || p.out[0] != 1) fail(BG_E_UNSUPPORTED, "conv: an output map needs a 2-D forward");
+    k.om = 1;
+    k.om_sh = omap->sh;
+    k.om_sw = omap->sw;
+    k.om_ph = omap->ph;
+    k.om_pw = omap->pw;
+    k.om_H = omap->H;
+    k.om_W = omap->W;
+  }
   k.C = int(p.c);
   k.O = int(p.o);
   k.Cpg = int(p.c / p.groups);

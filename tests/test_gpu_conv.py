@@ -313,7 +313,10 @@ def test_conv_forward_ring_matches_register_kernel(bridge, case, monkeypatch):
     """The forward (and the stride-1 input gradient, which runs as a forward
     convolution) copies its operands into an LDS ring; BG_CONV_RING=0 selects
     the register-staged kernel. Both feed the MFMAs the same k sequence, so
-    the outputs are bit-identical, and both match the oracle."""
+    the outputs are bit-identical, and both match the oracle.  (A strided
+    input gradient runs as phase convolutions on the ring kernel, a
+    different sum order from the DGRAD kernel: switched off here.)"""
+    monkeypatch.setenv("BG_CONV_DGRAD_PHASES", "0")
     r, n, ci, ins, co, k, s, p, d, g = case
     rng = np.random.default_rng(sum(ins) + 29 * co)
     x = rng.standard_normal((n, ci) + ins).astype(F32)
@@ -592,6 +595,60 @@ def test_conv3x3_input_patch_output_beyond_formula(bridge, monkeypatch):
     assert O.within(y, ref, TOL).all(), O.report(y, ref, TOL)
     monkeypatch.setenv("BG_CONV_RING", "0")
     assert np.array_equal(y, conv_ex(bridge, "forward", x, w, b, **kw))
+
+
+STRIDED = [
+    # n, c_in, (H, W), c_out, k, stride, pad, groups, phases used
+    (2, 6, (11, 9), 8, (3, 3), (2, 2), (1, 1), 1, True),
+    (1, 4, (12, 12), 6, (3, 3), (2, 2), (0, 0), 2, True),
+    (2, 4, (9, 10), 4, (1, 1), (2, 2), (0, 0), 1, True),    # 1x1 stride 2: three phases no tap reaches
+    (1, 2, (10, 11), 3, (3, 3), (3, 2), (0, 1), 1, True),   # stride 3 x 2
+    (1, 3, (8, 8), 5, (2, 2), (2, 2), (0, 0), 1, True),     # one tap per phase
+    (2, 3, (9, 13), 4, (5, 3), (2, 2), (2, 1), 1, True),    # a 5-tall kernel: up to 3 taps per phase
+    (2, 3, (7, 13), 4, (5, 3), (2, 3), (2, 1), 1, True),    # a phase whose first tap reads past dy's first column
+    (1, 2, (10, 11), 3, (3, 3), (3, 3), (1, 1), 1, True),   # stride 3, padding 1: negative leading padding
+    (2, 2, (6, 6), 3, (3, 3), (2, 2), (1, 1), 1, True),     # tiny images
+    (32, 64, (56, 56), 128, (3, 3), (2, 2), (1, 1), 1, True),  # ResNet's downsampling layer (float64 bound)
+]
+
+
+@pytest.mark.parametrize("case", STRIDED)
+def test_conv_strided_input_gradient_phases(bridge, case, monkeypatch):
+    """A strided 2-D input gradient runs as stride_h x stride_w phase
+    convolutions (dense stride-1 forward convolutions of dy by each phase's
+    taps, written to that phase's positions of dx; the launch log shows the
+    phase weights), against the oracle (or float64 with the sqrt(K) bound at
+    the large shape) and against the DGRAD kernel (BG_CONV_DGRAD_PHASES=0)."""
+    n, ci, hw, co, k, s, p, g, phases = case
+    d = (1, 1)
+    rng = np.random.default_rng(n * 31 + ci * 7 + co)
+    w = rng.standard_normal((co, ci // g) + k).astype(F32)
+    out = _out_size(hw, k, s, p, d)
+    dy = rng.standard_normal((n, co) + out).astype(F32)
+    kw = dict(n=n, c_in=ci, c_out=co, in_size=hw, out_size=out, k=k, stride=s, pad=p, dilation=d, groups=g)
+    bridge.set_launch_log(True)
+    try:
+        bridge.take_launch_log()
+        gx = conv_ex(bridge, "backward_input", dy, w, **kw)
+        names = [r["kernel"] for r in bridge.take_launch_log()]
+    finally:
+        bridge.set_launch_log(False)
+    assert any("conv_phase_weight_kernel" in t for t in names) == phases, names
+    monkeypatch.setenv("BG_CONV_DGRAD_PHASES", "0")
+    gx0 = conv_ex(bridge, "backward_input", dy, w, **kw)
+    if n * ci * hw[0] * hw[1] <= 1 << 16:
+        ref = O.conv_backward_input(dy, w, s, p, d, g, hw)
+        for got in (gx, gx0):
+            assert got.shape == ref.shape
+            assert O.within(got, ref, TOL).all(), O.report(got, ref, TOL)
+    else:
+        wt, dyt = torch.tensor(w, dtype=torch.float64), torch.tensor(dy, dtype=torch.float64)
+        shape = (n, ci) + hw
+        truth = torch.nn.grad.conv2d_input(shape, wt, dyt, stride=s, padding=p, groups=g).numpy()
+        mass = torch.nn.grad.conv2d_input(shape, wt.abs(), dyt.abs(), stride=s, padding=p, groups=g).numpy()
+        bound = _bound(truth, mass, (co // g) * k[0] * k[1])
+        for got in (gx, gx0):
+            assert np.all(np.abs(got - truth) <= bound), float(np.max(np.abs(got - truth) / bound))
 
 
 @pytest.mark.parametrize("shape", [(4, 16, 28, 28), (3, 5, 7, 7), (2, 3, 4, 300)])

@@ -402,6 +402,60 @@ __global__ void __launch_bounds__(256) layer_norm_vec_kernel(const void* __restr
   }
 }
 
+// Rows of 2048 to 256 * 4 * NV columns (multiples of 4): one 256-thread
+// workgroup per row, thread t holding the float4 groups j * 256 + t
+// (j < NV) in registers; the row's sum and centred sum of squares are taken
+// per wavefront (shuffles) and then over the four wavefronts through LDS in
+// wavefront order.  One read of x and one write of y.
+template <int XD, int YD, int NV>
+__global__ void __launch_bounds__(256) layer_norm_row_kernel(const void* __restrict__ x,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ bias,
+                                                             void* __restrict__ y, int64_t cols, float eps) {
+  __shared__ float red[2][4];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t groups = cols >> 2;
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t g = int64_t(j) * 256 + t;
+    v[j] = g < groups ? ln_load4<XD>(x, row * groups + g) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  s = wave_sum(s);
+  if (lane == 0) red[0][wv] = s;
+  __syncthreads();
+  const float mean = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / float(cols);
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t g = int64_t(j) * 256 + t;
+    v[j] = make_float4(v[j].x - mean, v[j].y - mean, v[j].z - mean, v[j].w - mean);
+    if (g < groups)
+      q += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  }
+  q = wave_sum(q);
+  if (lane == 0) red[1][wv] = q;
+  __syncthreads();
+  const float var = ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / float(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t g = int64_t(j) * 256 + t;
+    if (g < groups) {
+      const float4 a = v[j];
+      const float4 wv4 = reinterpret_cast<const float4*>(w)[g];
+      const float4 bv4 = reinterpret_cast<const float4*>(bias)[g];
+      ln_store4<YD>(y, row * groups + g,
+                    make_float4(a.x * inv * wv4.x + bv4.x, a.y * inv * wv4.y + bv4.y, a.z * inv * wv4.z + bv4.z,
+                                a.w * inv * wv4.w + bv4.w));
+    }
+  }
+}
+
 // Fallback for very wide rows: three passes over global memory.
 __global__ void __launch_bounds__(256) layer_norm_wide_kernel(const void* __restrict__ x, int xd,
                                                               const float* __restrict__ w,
@@ -740,6 +794,30 @@ static bool launch_layer_norm_vec(bg_ctx* ctx, const void* x, int xd, const floa
   return true;
 }
 
+template <int NV>
+static bool launch_layer_norm_row(bg_ctx* ctx, const void* x, int xd, const float* w, const float* b, void* y,
+                                  int yd, int64_t rows, int64_t cols, float eps) {
+  if (rows > 0x7fffffff) return false;
+  const dim3 grid(static_cast<unsigned>(rows));
+#define BG_LNR(XD_, YD_) bg::dispatch(ctx, layer_norm_row_kernel<XD_, YD_, NV>, grid, dim3(256), 0, x, w, b, y, cols, eps)
+#define BG_LNR_Y(XD_)                         \
+  switch (yd) {                               \
+    case BG_F32: BG_LNR(XD_, BG_F32); break;  \
+    case BG_F16: BG_LNR(XD_, BG_F16); break;  \
+    case BG_BF16: BG_LNR(XD_, BG_BF16); break; \
+    default: return false;                    \
+  }
+  switch (xd) {
+    case BG_F32: BG_LNR_Y(BG_F32); break;
+    case BG_F16: BG_LNR_Y(BG_F16); break;
+    case BG_BF16: BG_LNR_Y(BG_BF16); break;
+    default: return false;
+  }
+#undef BG_LNR_Y
+#undef BG_LNR
+  return true;
+}
+
 void launch_layer_norm(bg_ctx* ctx, const void* x, int xd, const float* w, const float* b,
                        void* y, int yd, int64_t rows, int64_t cols, float eps) {
   if (rows == 0) return;
@@ -755,6 +833,21 @@ void launch_layer_norm(bg_ctx* ctx, const void* x, int xd, const float* w, const
     else if (nv <= 3) ok = launch_layer_norm_vec<3>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
     else if (nv <= 4) ok = launch_layer_norm_vec<4>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
     else ok = launch_layer_norm_vec<8>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    if (ok) {
+      hip_check(hipGetLastError(), "layer_norm launch");
+      return;
+    }
+  }
+  // Wider aligned rows: a workgroup per row (the wavefront-per-row kernel
+  // below reads them three times).
+  if (cols % 4 == 0 && cols > 4 * 64 * 8 && cols <= 256 * 4 * 32 && al(x, 4 * xs) && al(y, 4 * ys) &&
+      al(w, 16) && al(b, 16)) {
+    const int64_t nv = (cols / 4 + 255) / 256;
+    bool ok = false;
+    if (nv <= 4) ok = launch_layer_norm_row<4>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    else if (nv <= 8) ok = launch_layer_norm_row<8>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    else if (nv <= 16) ok = launch_layer_norm_row<16>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
+    else ok = launch_layer_norm_row<32>(ctx, x, xd, w, b, y, yd, rows, cols, eps);
     if (ok) {
       hip_check(hipGetLastError(), "layer_norm launch");
       return;

@@ -232,9 +232,11 @@ def _from16(y, dtype):
 
 
 # Widths for every register-group count of the vector path (1, 2, 3, 4, 8
-# groups of 4 columns per lane), its widest row (2048), and widths that take
-# the scalar kernels (not a multiple of 4, wider than 2048).
-@pytest.mark.parametrize("cols", [4, 200, 512, 768, 1024, 1028, 2048, 2052, 766])
+# groups of 4 columns per lane), its widest row (2048), the workgroup-per-row
+# kernel (4, 8, 16, 32 groups per thread, partial last groups), and widths
+# that take the scalar kernels (not a multiple of 4, wider than 32768).
+@pytest.mark.parametrize("cols", [4, 200, 512, 768, 1024, 1028, 2048, 2052, 766, 4096, 5000, 8192, 16380,
+                                  32768, 2050, 32772])
 @pytest.mark.parametrize("in_dtype,out_dtype", [("float32", "float32"), ("float16", "float16"),
                                                 ("bfloat16", "bfloat16"), ("float32", "float16"),
                                                 ("float16", "float32"), ("bfloat16", "float32")])

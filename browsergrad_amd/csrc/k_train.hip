@@ -90,6 +90,88 @@ __global__ void __launch_bounds__(256) ln_bwd_input_kernel(const float* __restri
   }
 }
 
+// dX for aligned rows of 1025 to NT * 4 * NV columns: one NT-thread
+// workgroup per row, thread t holding float4 groups j * NT + t of x and of
+// g = dy * w in registers; each row statistic (sum x, centred sum of squares,
+// sum g, sum g * x_hat) is summed per wavefront (shuffles), then over the
+// wavefronts through LDS in wavefront order.  One read of dy and x, one
+// write of dx (the wavefront-per-row kernel below reads the row three times).
+template <int NT, int NV>
+__global__ void __launch_bounds__(NT) ln_bwd_input_row_kernel(const float4* __restrict__ dy,
+                                                              const float4* __restrict__ x,
+                                                              const float4* __restrict__ w,
+                                                              float4* __restrict__ dx, int64_t cols, float eps) {
+  constexpr int NWV = NT / 64;
+  __shared__ float red[3][NWV];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int64_t groups = cols >> 2;
+  const int64_t base = int64_t(blockIdx.x) * groups;
+  const float n = float(cols);
+  auto block_sum = [&](float v, int slot) {
+    v = wave_sum(v);
+    if (lane == 0) red[slot][wv] = v;
+    __syncthreads();
+    float r = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) r += red[slot][i];
+    return r;
+  };
+  float4 v[NV], g[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = int64_t(j) * NT + t;
+    v[j] = c < groups ? x[base + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  const float mean = block_sum(s, 0) / n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = int64_t(j) * NT + t;
+    v[j] = make_float4(v[j].x - mean, v[j].y - mean, v[j].z - mean, v[j].w - mean);
+    if (c < groups) q += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  }
+  const float inv = 1.0f / sqrtf(block_sum(q, 1) / n + eps);
+  float sg = 0.f, sgx = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = int64_t(j) * NT + t;
+    v[j] = make_float4(v[j].x * inv, v[j].y * inv, v[j].z * inv, v[j].w * inv);  // x_hat
+    if (c < groups) {
+      const float4 d = dy[base + c], ww = w[c];
+      g[j] = make_float4(d.x * ww.x, d.y * ww.y, d.z * ww.z, d.w * ww.w);
+    } else {
+      g[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    sg += (g[j].x + g[j].y) + (g[j].z + g[j].w);
+    sgx += (g[j].x * v[j].x + g[j].y * v[j].y) + (g[j].z * v[j].z + g[j].w * v[j].w);
+  }
+  // Two statistics in one pass through LDS.
+  sg = wave_sum(sg);
+  sgx = wave_sum(sgx);
+  if (lane == 0) {
+    red[2][wv] = sg;
+    red[0][wv] = sgx;  // slot 0's mean was read by every thread before the second barrier
+  }
+  __syncthreads();
+  float tsg = 0.f, tsgx = 0.f;
+#pragma unroll
+  for (int i = 0; i < NWV; ++i) {
+    tsg += red[2][i];
+    tsgx += red[0][i];
+  }
+  const float k = inv / n;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = int64_t(j) * NT + t;
+    if (c < groups)
+      dx[base + c] = make_float4(k * ((n * g[j].x - tsg) - v[j].x * tsgx), k * ((n * g[j].y - tsg) - v[j].y * tsgx),
+                                 k * ((n * g[j].z - tsg) - v[j].z * tsgx), k * ((n * g[j].w - tsg) - v[j].w * tsgx));
+  }
+}
+
 // Same for rows wider than the register-resident variants: three passes over
 // global memory per row.
 __global__ void __launch_bounds__(256) ln_bwd_input_wide_kernel(const float* __restrict__ dy,
@@ -516,6 +598,7 @@ namespace bg {
 void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, const float* w, float* dx,
                               int64_t rows, int64_t cols, float eps) {
   if (rows == 0) return;
+  const auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   const dim3 grid(unsigned((rows + 3) / 4));
   if (cols <= 256)
     bg::dispatch(ctx, ln_bwd_input_kernel<4>, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
@@ -525,8 +608,26 @@ void launch_ln_backward_input(bg_ctx* ctx, const float* dy, const float* x, cons
     bg::dispatch(ctx, ln_bwd_input_kernel<12>, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
   else if (cols <= 1024)
     bg::dispatch(ctx, ln_bwd_input_kernel<16>, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
-  else
+  else if (cols % 4 == 0 && cols <= 1024 * 4 * 8 && rows <= 0x7fffffff && al16(dy) && al16(x) && al16(w) &&
+           al16(dx)) {
+    // A workgroup per row: 256 threads up to 8192 columns, else 1024.
+    const dim3 rgrid(static_cast<unsigned>(rows));
+    const float4 *dy4 = reinterpret_cast<const float4*>(dy), *x4 = reinterpret_cast<const float4*>(x),
+                 *w4 = reinterpret_cast<const float4*>(w);
+    float4* dx4 = reinterpret_cast<float4*>(dx);
+    if (cols <= 256 * 4 * 2)
+      bg::dispatch(ctx, ln_bwd_input_row_kernel<256, 2>, rgrid, dim3(256), 0, dy4, x4, w4, dx4, cols, eps);
+    else if (cols <= 256 * 4 * 4)
+      bg::dispatch(ctx, ln_bwd_input_row_kernel<256, 4>, rgrid, dim3(256), 0, dy4, x4, w4, dx4, cols, eps);
+    else if (cols <= 256 * 4 * 8)
+      bg::dispatch(ctx, ln_bwd_input_row_kernel<256, 8>, rgrid, dim3(256), 0, dy4, x4, w4, dx4, cols, eps);
+    else if (cols <= 1024 * 4 * 4)
+      bg::dispatch(ctx, ln_bwd_input_row_kernel<1024, 4>, rgrid, dim3(1024), 0, dy4, x4, w4, dx4, cols, eps);
+    else
+      bg::dispatch(ctx, ln_bwd_input_row_kernel<1024, 8>, rgrid, dim3(1024), 0, dy4, x4, w4, dx4, cols, eps);
+  } else {
     bg::dispatch(ctx, ln_bwd_input_wide_kernel, grid, dim3(256), 0, dy, x, w, dx, rows, cols, eps);
+  }
   hip_check(hipGetLastError(), "layer_norm_backward_input launch");
 }
 

@@ -136,7 +136,13 @@ def test_adamw_chain_matches_oracle_over_steps(bridge, rng):
 # ---------------------------------------------------------------- LayerNorm backward kernels
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 1), (2, 3), (5, 100), (8, 768), (64, 1024), (3, 3000), (17, 257)])
+# Up to 1024 columns the wavefront-per-row kernels; 4-aligned rows of 1028
+# to 32768 the workgroup-per-row kernel (256 threads with 2, 4, 8 groups per
+# thread, 1024 threads with 4 or 8; partial last groups); the rest the
+# three-pass kernel.
+@pytest.mark.parametrize("rows,cols", [(1, 1), (2, 3), (5, 100), (8, 768), (64, 1024), (3, 3000), (17, 257),
+                                       (9, 1028), (5, 2048), (4, 4100), (3, 8192), (3, 12000), (2, 32768),
+                                       (2, 32772), (3, 2050)])
 def test_layer_norm_backward_input(bridge, rng, rows, cols):
     x = (rng.standard_normal((rows, cols)) * 3 + 1).astype(F32)
     w = rng.standard_normal(cols).astype(F32)

@@ -238,6 +238,53 @@ __global__ void __launch_bounds__(256) ln_row_stats_kernel(const float* __restri
   }
 }
 
+// The same statistics for aligned rows of up to NT * 4 * NV columns: one
+// NT-thread workgroup per row, the row read once into registers, wavefront
+// sums combined through LDS in wavefront order.
+template <int NT, int NV>
+__global__ void __launch_bounds__(NT) ln_row_stats_row_kernel(const float4* __restrict__ x,
+                                                              float* __restrict__ stats, int64_t cols, float eps) {
+  constexpr int NWV = NT / 64;
+  __shared__ float red[2][NWV];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int64_t groups = cols >> 2;
+  const int64_t base = int64_t(blockIdx.x) * groups;
+  const float n = float(cols);
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = int64_t(j) * NT + t;
+    v[j] = c < groups ? x[base + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  s = wave_sum(s);
+  if (lane == 0) red[0][wv] = s;
+  __syncthreads();
+  float ts = 0.f;
+#pragma unroll
+  for (int i = 0; i < NWV; ++i) ts += red[0][i];
+  const float mean = ts / n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = int64_t(j) * NT + t;
+    const float4 a = make_float4(v[j].x - mean, v[j].y - mean, v[j].z - mean, v[j].w - mean);
+    if (c < groups) q += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
+  }
+  q = wave_sum(q);
+  if (lane == 0) red[1][wv] = q;
+  __syncthreads();
+  if (t == 0) {
+    float tq = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) tq += red[1][i];
+    stats[2 * blockIdx.x] = mean;
+    stats[2 * blockIdx.x + 1] = 1.0f / sqrtf(tq / n + eps);
+  }
+}
+
 // Column partial sums over one chunk of rows: part[chunk][c] = sum over the
 // chunk's rows r of dy[r][c] * x_hat[r][c] (WEIGHT) or dy[r][c] (BIAS).  A
 // thread owns one column, so every row's loads are coalesced across lanes.
@@ -700,9 +747,26 @@ void launch_ln_backward_cols(bg_ctx* ctx, const float* dy, const float* x, float
     if (weight) ws += size_t(rows) * 2 * sizeof(float);
     part = static_cast<float*>(bg::scratch(ctx, ws, 0));
     float* stats = weight ? part + chunks * cols : nullptr;
-    if (weight)
+    const bool row_stats = weight && cols % 4 == 0 && cols <= 1024 * 4 * 8 && rows <= 0x7fffffff &&
+                           (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (row_stats) {
+      // A workgroup per row, the row read once.
+      const dim3 rgrid(static_cast<unsigned>(rows));
+      const float4* x4 = reinterpret_cast<const float4*>(x);
+      if (cols <= 256 * 4 * 2)
+        bg::dispatch(ctx, ln_row_stats_row_kernel<256, 2>, rgrid, dim3(256), 0, x4, stats, cols, eps);
+      else if (cols <= 256 * 4 * 4)
+        bg::dispatch(ctx, ln_row_stats_row_kernel<256, 4>, rgrid, dim3(256), 0, x4, stats, cols, eps);
+      else if (cols <= 256 * 4 * 8)
+        bg::dispatch(ctx, ln_row_stats_row_kernel<256, 8>, rgrid, dim3(256), 0, x4, stats, cols, eps);
+      else if (cols <= 1024 * 4 * 4)
+        bg::dispatch(ctx, ln_row_stats_row_kernel<1024, 4>, rgrid, dim3(1024), 0, x4, stats, cols, eps);
+      else
+        bg::dispatch(ctx, ln_row_stats_row_kernel<1024, 8>, rgrid, dim3(1024), 0, x4, stats, cols, eps);
+    } else if (weight) {
       bg::dispatch(ctx, ln_row_stats_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, x, stats, rows, cols,
                    eps);
+    }
     if (weight)
       bg::dispatch(ctx, ln_col_partial_kernel<true>, dim3(unsigned(col_blocks), unsigned(chunks)), dim3(256), 0, dy,
                    x, stats, part, rows, cols, rpc);

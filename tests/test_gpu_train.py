@@ -159,7 +159,8 @@ def test_layer_norm_backward_input(bridge, rng, rows, cols):
 # 4-aligned widths up to 1024 take the 16-byte kernel (every lane width
 # 1..4 groups of 64, ragged rows and groups); the others the scalar ones.
 @pytest.mark.parametrize("rows,cols", [(1, 1), (2, 3), (7, 5), (1, 4), (5, 100), (33, 260), (19, 1024), (100, 768),
-                                       (517, 1030), (33, 4100)])
+                                       (517, 1030), (33, 4100), (9, 2048), (5, 12000), (3, 32768), (4, 32772),
+                                       (6, 2050)])
 def test_layer_norm_backward_weight_bias(bridge, rng, rows, cols):
     x = (rng.standard_normal((rows, cols)) * 2 - 0.5).astype(F32)
     dy = rng.standard_normal((rows, cols)).astype(F32)

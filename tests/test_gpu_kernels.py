@@ -231,6 +231,35 @@ def _from16(y, dtype):
     return y.astype(np.float32) if dtype == "float16" else O.bf16_bits_to_f32(y)
 
 
+# softmax_last: wavefront-per-row kernels below 512 columns (and unaligned
+# up to 2048), the workgroup-per-row kernel for aligned rows of 512-32768
+# (256 threads with 1, 2, 4 or 8 groups each, 1024 threads with 4 or 8), a
+# 1024-thread register kernel for other rows up to 65536 (a GPT-2
+# vocabulary row), the three-pass workgroup-per-row kernel past that.
+@pytest.mark.parametrize("cols", [3, 64, 512, 768, 1000, 2048, 2052, 4096, 5000, 8192, 16384, 32768, 32772,
+                                  50257, 2051, 16385, 65537])
+@pytest.mark.parametrize("in_dtype,out_dtype", [("float32", "float32"), ("float16", "float16"),
+                                                ("bfloat16", "float32"), ("float32", "float16")])
+def test_softmax_last_widths(bridge, rng, cols, in_dtype, out_dtype):
+    rows = 5
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+    x[1] += 30.0  # a row far from zero: the max is subtracted before the exponential
+    if in_dtype == "float32":
+        hx = up(bridge, x)
+    else:
+        x16 = _to16(x, in_dtype)
+        hx = up(bridge, x16, in_dtype)
+        x = _from16(x16, in_dtype)
+    y = bridge.to_numpy(bridge.softmax_last(hx, rows, cols, out_dtype=out_dtype))
+    ref = O.softmax_lastaxis(x)
+    if out_dtype == "float32":
+        assert O.within(y, ref, TOL32).all(), O.report(y, ref, TOL32)
+        assert np.allclose(y.astype(np.float64).sum(axis=1), 1.0, atol=1e-4)
+    else:
+        y32, r32 = _from16(y, out_dtype), _from16(_to16(ref, out_dtype), out_dtype)
+        assert O.within(y32, r32, TOL16).all(), O.report(y32, r32, TOL16)
+
+
 # Widths for every register-group count of the vector path (1, 2, 3, 4, 8
 # groups of 4 columns per lane), its widest row (2048), the workgroup-per-row
 # kernel (4, 8, 16, 32 groups per thread, partial last groups), and widths

@@ -53,6 +53,11 @@ struct FusedArgs {
   int64_t cols;
   float imm[BG_FUSED_MAX_IMMS];
   void* out;
+  // Split reductions: each row is cut into `nch` chunks of `cw` columns whose
+  // partial results go to `part[row * nch + chunk]`.
+  int64_t cw;
+  int64_t nch;
+  float* part;
 };
 
 const char* kPrelude = R"(
@@ -67,6 +72,9 @@ struct Args {
   i64 cols;
   float imm[16];
   void* out;
+  i64 cw;
+  i64 nch;
+  float* part;
 };
 typedef float f4v_ __attribute__((ext_vector_type(4)));
 typedef u32 u2v_ __attribute__((ext_vector_type(2)));
@@ -116,6 +124,8 @@ struct Plan {
   int vec = 1;
   int reduce = BG_RED_NONE;
   int tpr = 64;
+  int split = 0;
+  int one_pass = 0;  // every row fits one vector per lane of its TPR lanes
   int out_dtype = BG_F32;
   std::vector<bg_fused_op> ops;
 };
@@ -319,31 +329,82 @@ std::string generate(const Plan& p) {
   auto combine = [&](const std::string& a, const std::string& b) {
     return comb ? std::string(comb) + "(" + a + ", " + b + ")" : "(" + a + " + " + b + ")";
   };
-  const int TPR = p.tpr;
+  // TPR lanes per row (a power of two dividing 64, or 256 = the whole
+  // workgroup); split plans give each workgroup one chunk of a row and write
+  // the raw partial, which a second kernel combines per row in chunk order.
+  const int TPR = p.split ? 256 : p.tpr;
   const int RPB = 256 / TPR;
   os << "  __shared__ float part[4];\n"
      << "  const int lane = threadIdx.x % " << TPR << ";\n"
-     << "  const int sub = threadIdx.x / " << TPR << ";\n"
-     << "  for (i64 row0 = (i64)blockIdx.x * " << RPB << "; row0 < A.rows; row0 += (i64)gridDim.x * " << RPB
-     << ") {\n"
-     << "    const i64 row = row0 + sub;\n"
-     << "    const bool live = row < A.rows;\n"
-     << "    float acc = " << ident << ";\n"
-     << "    if (live) {\n"
-     << "#pragma unroll 4\n"
-     << "    for (i64 col = (i64)lane * " << V << "; col < A.cols; col += " << TPR * V << ") {\n"
-     << "    const i64 lin = row * A.cols + col;\n";
+     << "  const int sub = threadIdx.x / " << TPR << ";\n";
+  if (p.one_pass && TPR <= 64) {
+    // Narrow rows (one vector per lane covers the row): each workgroup pass
+    // takes NU row blocks, all loads issued before the first butterfly.
+    const int NU = V == 1 ? 8 : 4;
+    os << "  for (i64 row0 = (i64)blockIdx.x * " << RPB * NU << "; row0 < A.rows; row0 += (i64)gridDim.x * "
+       << RPB * NU << ") {\n"
+       << "    float accu[" << NU << "];\n"
+       << "#pragma unroll\n"
+       << "    for (int q = 0; q < " << NU << "; ++q) {\n"
+       << "    const i64 row = row0 + q * " << RPB << " + sub;\n"
+       << "    const i64 col = (i64)lane * " << V << ";\n"
+       << "    float acc = " << ident << ";\n"
+       << "    if (row < A.rows && col < A.cols) {\n"
+       << "    const i64 lin = row * A.cols + col;\n";
+    emit_body(os, p, V);
+    os << "#pragma unroll\n    for (int j = 0; j < " << V << "; ++j) acc = "
+       << combine("acc", "s" + std::to_string(last) + "[j]") << ";\n";
+    os << "    }\n    accu[q] = acc;\n    }\n";
+    os << "#pragma unroll\n    for (int q = 0; q < " << NU << "; ++q) {\n"
+       << "    float acc = accu[q];\n";
+    if (TPR > 1)
+      os << "#pragma unroll\n    for (int s = " << TPR / 2 << "; s >= 1; s >>= 1) acc = "
+         << combine("acc", "__shfl_xor(acc, s, 64)") << ";\n";
+    os << "    const i64 row = row0 + q * " << RPB << " + sub;\n"
+       << "    if (row < A.rows && lane == 0) {\n";
+    if (p.reduce == BG_RED_MEAN) os << "      acc = acc / (float)A.cols;\n";
+    os << "      " << store_expr(p.out_dtype, "row", "acc") << "\n    }\n    }\n  }\n}\n";
+    return os.str();
+  }
+  if (p.split) {
+    os << "  const i64 units = A.rows * A.nch;\n"
+       << "  for (i64 u = blockIdx.x; u < units; u += gridDim.x) {\n"
+       << "    const i64 row = u / A.nch;\n"
+       << "    const i64 c0 = (u - row * A.nch) * A.cw;\n"
+       << "    const i64 c1 = c0 + A.cw < A.cols ? c0 + A.cw : A.cols;\n"
+       << "    const bool live = true;\n"
+       << "    float acc = " << ident << ";\n"
+       << "    {\n"
+       << "#pragma unroll 4\n"
+       << "    for (i64 col = c0 + (i64)lane * " << V << "; col < c1; col += " << TPR * V << ") {\n"
+       << "    const i64 lin = row * A.cols + col;\n";
+  } else {
+    os << "  for (i64 row0 = (i64)blockIdx.x * " << RPB << "; row0 < A.rows; row0 += (i64)gridDim.x * " << RPB
+       << ") {\n"
+       << "    const i64 row = row0 + sub;\n"
+       << "    const bool live = row < A.rows;\n"
+       << "    float acc = " << ident << ";\n"
+       << "    if (live) {\n"
+       << "#pragma unroll 4\n"
+       << "    for (i64 col = (i64)lane * " << V << "; col < A.cols; col += " << TPR * V << ") {\n"
+       << "    const i64 lin = row * A.cols + col;\n";
+  }
   emit_body(os, p, V);
   os << "#pragma unroll\n    for (int j = 0; j < " << V << "; ++j) acc = "
      << combine("acc", "s" + std::to_string(last) + "[j]") << ";\n";
   os << "    }\n    }\n";
-  os << "#pragma unroll\n    for (int s = 32; s >= 1; s >>= 1) acc = "
-     << combine("acc", "__shfl_xor(acc, s, 64)") << ";\n";
+  if (TPR > 1)
+    os << "#pragma unroll\n    for (int s = " << (TPR < 64 ? TPR : 64) / 2 << "; s >= 1; s >>= 1) acc = "
+       << combine("acc", "__shfl_xor(acc, s, 64)") << ";\n";
   if (TPR == 256) {
     os << "    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;\n"
        << "    __syncthreads();\n"
        << "    acc = " << combine(combine("part[0]", "part[1]"), combine("part[2]", "part[3]")) << ";\n"
        << "    __syncthreads();\n";
+  }
+  if (p.split) {
+    os << "    if (threadIdx.x == 0) A.part[u] = acc;\n  }\n}\n";
+    return os.str();
   }
   os << "    if (live && lane == 0) {\n";
   if (p.reduce == BG_RED_MEAN) os << "      acc = acc / (float)A.cols;\n";
@@ -617,7 +678,32 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
       reinterpret_cast<uintptr_t>(A.out) % uintptr_t(4 * dtype_size(d.out_dtype)) != 0)
     v4 = false;
   plan.vec = v4 ? 4 : 1;
-  plan.tpr = cols >= 2048 ? 256 : 64;
+  // Lanes per row for reductions: the whole workgroup for wide rows, else
+  // the fewest power-of-two lanes (at most a wavefront) that cover the row
+  // in one vector each, so narrow rows do not leave most lanes idle.
+  if (cols >= 2048) {
+    plan.tpr = 256;
+  } else {
+    int t = 1;
+    while (t < 64 && int64_t(t) * plan.vec < cols) t *= 2;
+    plan.tpr = t;
+    plan.one_pass = int64_t(t) * plan.vec >= cols;
+  }
+  // Few wide rows: cut each row into chunks of whole 256-lane vector steps
+  // (at least 8 per chunk) until about 1024 workgroups stream the input;
+  // a second kernel combines each row's chunk partials in order.
+  if (d.reduce_op != BG_RED_NONE && plan.tpr == 256 && rows < 512) {
+    const int64_t step = 256 * int64_t(plan.vec);
+    const int64_t min_cw = 8 * step;
+    int64_t nch = std::min<int64_t>((1024 + rows - 1) / rows, (cols + min_cw - 1) / min_cw);
+    if (nch > 1) {
+      int64_t cw = (cols + nch - 1) / nch;
+      cw = (cw + step - 1) / step * step;
+      plan.split = 1;
+      A.cw = cw;
+      A.nch = (cols + cw - 1) / cw;
+    }
+  }
 
   int64_t in_bytes = 0;
   for (int i = 0; i < n_in; ++i)
@@ -626,8 +712,8 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
   // Compact binary signature of everything generate() depends on.
   std::string sig;
   {
-    int32_t head[8] = {ctx->device, plan.n_in, plan.nlead, plan.vec,
-                       plan.reduce, plan.tpr, plan.out_dtype, int32_t(plan.ops.size())};
+    int32_t head[10] = {ctx->device, plan.n_in, plan.nlead, plan.vec, plan.reduce, plan.tpr,
+                        plan.split, plan.one_pass, plan.out_dtype, int32_t(plan.ops.size())};
     sig.append(reinterpret_cast<const char*>(head), sizeof(head));
     for (int i = 0; i < plan.n_in; ++i) {
       int32_t io[2] = {plan.kind[i], plan.dtype[i]};
@@ -657,8 +743,14 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
     const int64_t items = total / plan.vec;
     grid = unsigned(std::max<int64_t>(1, std::min<int64_t>((items + 255) / 256, 256 * 16)));
     obytes = total * dtype_size(d.out_dtype);
+  } else if (plan.split) {
+    A.part = static_cast<float*>(scratch(ctx, size_t(rows * A.nch) * 4, 0));
+    grid = unsigned(rows * A.nch);
+    obytes = rows * dtype_size(d.out_dtype);
   } else {
-    const int64_t rpb = 256 / plan.tpr;
+    // Rows per workgroup pass: 256 / tpr, times the row blocks a narrow-row
+    // kernel takes per pass (8 with scalar loads, 4 with vectors).
+    const int64_t rpb = (256 / plan.tpr) * (plan.one_pass ? (plan.vec == 1 ? 8 : 4) : 1);
     grid = unsigned(std::max<int64_t>(1, std::min<int64_t>((rows + rpb - 1) / rpb, int64_t(1) << 20)));
     obytes = rows * dtype_size(d.out_dtype);
   }
@@ -668,8 +760,12 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
   next_dispatch_events(ctx, &ev_start, &ev_stop);
   // Global size in work-items (grid blocks x 256 lanes).
   hip_check(hipExtModuleLaunchKernel(fn, grid * 256u, 1, 1, 256, 1, 1, 0, ctx->stream, nullptr, cfg,
-                                     ev_start, ev_stop, 0),
+                                     ev_start, plan.split ? nullptr : ev_stop, 0),
             "fused_elementwise launch");
+  if (plan.split) {
+    launch_reduce_partials(ctx, A.part, rows, A.nch, d.reduce_op, cols, A.out, d.out_dtype);
+    if (ev_stop) hip_check(hipEventRecord(ev_stop, ctx->stream), "hipEventRecord");
+  }
 }
 
 }  // namespace bg
@@ -697,7 +793,9 @@ extern "C" int bg_fused_codegen_selftest(char* err, size_t cap) {
         p.n_in = 4;
         p.vec = vec;
         p.reduce = red;
-        p.tpr = red == BG_RED_SUM ? 256 : 64;
+        p.tpr = red == BG_RED_SUM ? 256 : od == BG_F16 ? 1 : od == BG_BF16 ? 8 : 64;
+        p.split = red == BG_RED_MEAN;
+        p.one_pass = red == BG_RED_MAX;
         p.out_dtype = od;
         p.nlead = 2;
         for (int i = 0; i < 4; ++i) {

@@ -781,6 +781,141 @@ __global__ void __launch_bounds__(256) gelu_rows_kernel(const float* __restrict_
   }
 }
 
+// Combines the per-chunk partials of a split row reduction: a workgroup per
+// row, thread t folding chunks t, t + 256, ... in order, then a butterfly
+// per wavefront and the 4 wavefronts in a fixed order; MAX and MIN
+// propagate NaN like the single-pass kernel.
+__device__ __forceinline__ float red_combine(int op, float a, float b) {
+  if (op == BG_RED_MAX) return (a != a || b != b) ? a + b : fmaxf(a, b);
+  if (op == BG_RED_MIN) return (a != a || b != b) ? a + b : fminf(a, b);
+  return a + b;
+}
+
+__global__ void __launch_bounds__(256) reduce_partials_kernel(const float* __restrict__ part, int64_t nch,
+                                                              int op, float cols, void* out, int out_dtype) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* p = part + row * nch;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float acc = op == BG_RED_MAX ? -__builtin_inff() : op == BG_RED_MIN ? __builtin_inff() : 0.f;
+#pragma unroll 4
+  for (int64_t k = threadIdx.x; k < nch; k += 256) acc = red_combine(op, acc, p[k]);
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) acc = red_combine(op, acc, __shfl_xor(acc, s, 64));
+  if (lane == 0) red[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  acc = red_combine(op, red_combine(op, red[0], red[1]), red_combine(op, red[2], red[3]));
+  store_from_f32(out, out_dtype, row, op == BG_RED_MEAN ? acc / cols : acc);
+}
+
+// Reduction of x[R][C] over its leading axis R (the per-column sums of a
+// bias gradient), reading x once in place.  Workgroup = 4 wavefronts; a
+// wavefront's lanes are LC column lanes (V adjacent columns each, so a row
+// segment of LC * V columns is read contiguously) x 64 / LC row lanes.
+// Workgroup u covers column group u % ngroups and rows of chunk u / ngroups;
+// inside it row r goes to row lane (r - r0) % (4 * 64 / LC).  Row lanes
+// combine by a butterfly, wavefronts in order 0..3 through LDS.  With one
+// chunk the result is final, otherwise it is the chunk's partial.
+template <int XD, int V>
+__device__ __forceinline__ void load_v(const void* x, int64_t i, float (&v)[V]) {
+  if constexpr (XD == 0) {
+    if constexpr (V == 4) {
+      const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + i);
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+      v[0] = static_cast<const float*>(x)[i];
+    }
+  } else {
+    const uint16_t* p = static_cast<const uint16_t*>(x) + i;
+    if constexpr (V == 4) {
+      const uint2 t = *reinterpret_cast<const uint2*>(p);
+      const uint16_t h[4] = {uint16_t(t.x), uint16_t(t.x >> 16), uint16_t(t.y), uint16_t(t.y >> 16)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = XD == 1 ? f16_bits_to_f32(h[j]) : bf16_bits_to_f32(h[j]);
+    } else {
+      v[0] = XD == 1 ? f16_bits_to_f32(p[0]) : bf16_bits_to_f32(p[0]);
+    }
+  }
+}
+
+template <int XD, int V, int LC>
+__global__ void __launch_bounds__(256) reduce_lead_kernel(const void* __restrict__ x, int64_t R, int64_t C,
+                                                          int64_t CR, int64_t ngroups, int op, float* part,
+                                                          int final_out, void* out, int od) {
+  constexpr int RL = 64 / LC;
+  __shared__ float red[4][64 * V];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int cl = lane % LC, rl = lane / LC;
+  // Column groups rotate with the chunk, so the workgroups that share an
+  // XCD (every eighth in dispatch order) do not all read the same few
+  // column groups when ngroups divides by 8.
+  const int64_t chunk = blockIdx.x / ngroups;
+  const int64_t group = (blockIdx.x % ngroups + chunk) % ngroups;
+  const int64_t col = (group * LC + cl) * V;
+  const int64_t r0 = chunk * CR;
+  const int64_t r1 = r0 + CR < R ? r0 + CR : R;
+  const float ident = op == BG_RED_MAX ? -__builtin_inff() : op == BG_RED_MIN ? __builtin_inff() : 0.f;
+  float acc[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) acc[j] = ident;
+  if (col < C) {
+#pragma unroll 4
+    for (int64_t r = r0 + wave * RL + rl; r < r1; r += 4 * RL) {
+      float v[V];
+      load_v<XD, V>(x, r * C + col, v);
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = red_combine(op, acc[j], v[j]);
+    }
+  }
+#pragma unroll
+  for (int s = LC; s < 64; s <<= 1)
+#pragma unroll
+    for (int j = 0; j < V; ++j) acc[j] = red_combine(op, acc[j], __shfl_xor(acc[j], s, 64));
+  if (rl == 0)
+#pragma unroll
+    for (int j = 0; j < V; ++j) red[wave][cl * V + j] = acc[j];
+  __syncthreads();
+  if (wave != 0 || rl != 0 || col >= C) return;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    float a = red[0][cl * V + j];
+    a = red_combine(op, a, red[1][cl * V + j]);
+    a = red_combine(op, a, red[2][cl * V + j]);
+    a = red_combine(op, a, red[3][cl * V + j]);
+    if (final_out)
+      store_from_f32(out, od, col + j, op == BG_RED_MEAN ? a / static_cast<float>(R) : a);
+    else
+      part[chunk * C + col + j] = a;
+  }
+}
+
+// Second pass: out[c] = the chunks' partials part[k][c], k = 0..nchunk-1.
+// A workgroup covers 16 columns with 64 chunk lanes each: lane k folds
+// chunks k, k + 64, ... in order; the 4 chunk lanes of a wavefront combine
+// by a butterfly, then the 16 wavefronts in order through LDS.
+__global__ void __launch_bounds__(1024) reduce_lead_final_kernel(const float* __restrict__ part, int64_t nchunk,
+                                                                 int64_t C, int op, float R, void* out, int od) {
+  __shared__ float red[16][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cx = lane & 15, k0 = wave * 4 + (lane >> 4);
+  const int64_t c = int64_t(blockIdx.x) * 16 + cx;
+  float acc = op == BG_RED_MAX ? -__builtin_inff() : op == BG_RED_MIN ? __builtin_inff() : 0.f;
+  if (c < C) {
+#pragma unroll 8
+    for (int64_t k = k0; k < nchunk; k += 64) acc = red_combine(op, acc, part[k * C + c]);
+  }
+  acc = red_combine(op, acc, __shfl_xor(acc, 16, 64));
+  acc = red_combine(op, acc, __shfl_xor(acc, 32, 64));
+  if (lane < 16) red[wave][cx] = acc;
+  __syncthreads();
+  if (wave != 0 || lane >= 16 || c >= C) return;
+  float a = red[0][cx];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) a = red_combine(op, a, red[w][cx]);
+  store_from_f32(out, od, c, op == BG_RED_MEAN ? a / R : a);
+}
+
 }  // namespace
 
 namespace bg {
@@ -901,6 +1036,58 @@ static bool launch_softmax_row(bg_ctx* ctx, const void* x, int xd, void* y, int 
 #undef BG_SMR_Y
 #undef BG_SMR
   return true;
+}
+
+// x[R][C] reduced over R into out[C] (dtype of x); see reduce_lead_kernel.
+void launch_reduce_lead(bg_ctx* ctx, const void* x, int xd, int64_t R, int64_t C, int op, void* out) {
+  if (R <= 0 || C <= 0) fail(BG_E_SHAPE, "reduce: empty reduction");
+  if (xd != BG_F32 && xd != BG_F16 && xd != BG_BF16) fail(BG_E_DTYPE, "reduce: dtype not supported");
+  const int es = xd == BG_F32 ? 4 : 2;
+  const bool v4 = C % 4 == 0 && reinterpret_cast<uintptr_t>(x) % uintptr_t(4 * es) == 0;
+  const int V = v4 ? 4 : 1;
+  const int64_t need = (C + V - 1) / V;  // column lanes the row needs
+  const int LC = need <= 4 ? 4 : need <= 16 ? 16 : 64;
+  const int64_t ngroups = (C + int64_t(LC) * V - 1) / (int64_t(LC) * V);
+  const int64_t rstep = 4 * (64 / LC);  // rows one workgroup pass reads
+  // Chunks of whole workgroup passes (at least 8) until about 1024
+  // workgroups stream x.
+  int64_t nchunk = std::max<int64_t>(1, std::min<int64_t>((1024 + ngroups - 1) / ngroups,
+                                                        (R + 8 * rstep - 1) / (8 * rstep)));
+  int64_t CR = (R + nchunk - 1) / nchunk;
+  CR = (CR + rstep - 1) / rstep * rstep;
+  nchunk = (R + CR - 1) / CR;
+  const int64_t units = ngroups * nchunk;
+  if (units > int64_t(0x7fffffff)) fail(BG_E_UNSUPPORTED, "reduce: too many column groups");
+  float* part = nchunk > 1 ? static_cast<float*>(scratch(ctx, size_t(nchunk * C) * 4, 0)) : nullptr;
+  const int fin = nchunk == 1 ? 1 : 0;
+  auto go = [&](auto xdc, auto vc, auto lcc) {
+    bg::dispatch(ctx, reduce_lead_kernel<decltype(xdc)::value, decltype(vc)::value, decltype(lcc)::value>,
+                 dim3(static_cast<unsigned>(units)), dim3(256), 0, x, R, C, CR, ngroups, op, part, fin, out, xd);
+  };
+  auto by_lc = [&](auto xdc, auto vc) {
+    if (LC == 4) go(xdc, vc, std::integral_constant<int, 4>{});
+    else if (LC == 16) go(xdc, vc, std::integral_constant<int, 16>{});
+    else go(xdc, vc, std::integral_constant<int, 64>{});
+  };
+  auto by_v = [&](auto xdc) {
+    if (V == 4) by_lc(xdc, std::integral_constant<int, 4>{});
+    else by_lc(xdc, std::integral_constant<int, 1>{});
+  };
+  if (xd == BG_F32) by_v(std::integral_constant<int, 0>{});
+  else if (xd == BG_F16) by_v(std::integral_constant<int, 1>{});
+  else by_v(std::integral_constant<int, 2>{});
+  if (nchunk > 1)
+    bg::dispatch(ctx, reduce_lead_final_kernel, dim3(static_cast<unsigned>((C + 15) / 16)), dim3(1024), 0,
+                 static_cast<const float*>(part), nchunk, C, op, static_cast<float>(R), out, xd);
+}
+
+void launch_reduce_partials(bg_ctx* ctx, const float* part, int64_t rows, int64_t nch, int op,
+                            int64_t cols, void* out, int out_dtype) {
+  if (rows <= 0) return;
+  if (out_dtype != BG_F32 && out_dtype != BG_F16 && out_dtype != BG_BF16)
+    fail(BG_E_DTYPE, "reduce: output dtype must be float32, float16 or bfloat16");
+  bg::dispatch(ctx, reduce_partials_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, part, nch, op,
+               static_cast<float>(cols), out, out_dtype);
 }
 
 void launch_softmax_last(bg_ctx* ctx, const void* x, int xd, void* y, int yd, int64_t rows, int64_t cols) {

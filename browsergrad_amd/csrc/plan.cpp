@@ -1294,6 +1294,23 @@ struct Runner {
     bool trailing = true;
     for (int64_t i = 0; i < int64_t(red.size()); ++i)
       if (!red.count(rank - 1 - i)) trailing = false;
+    // Reduced axes that form a leading prefix (a bias gradient's sum over
+    // the batch): one pass over the input in place instead of a transposing
+    // copy followed by a row reduction.
+    bool leading = true;
+    for (int64_t i = 0; i < int64_t(red.size()); ++i)
+      if (!red.count(i)) leading = false;
+    if (!trailing && leading && cols > 0 && rows > 0 &&
+        (r.dtype == BG_F32 || r.dtype == BG_F16 || r.dtype == BG_BF16)) {
+      if (numel(s.shape) != rows) plan_fail("REDUCE output shape differs from the plan");
+      const int dt = r.dtype;
+      if (dt != plan_dtype(s.dtype, "REDUCE dtype")) fail(BG_E_DTYPE, "tensor plan REDUCE dtype differs");
+      const int64_t es = dtype_size(dt);
+      bg_handle out = own(mint(ctx, size_t(rows * es), s.shape, dt));
+      Profile prof(ctx, "reduce_lead", (rows * cols + rows) * es, rows * cols);
+      launch_reduce_lead(ctx, rec(src).ptr(), dt, cols, rows, rop, ctx->handles[out].ptr());
+      return out;
+    }
     bg_handle x = src;
     if (!trailing) {
       std::vector<int64_t> perm;

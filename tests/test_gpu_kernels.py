@@ -171,6 +171,97 @@ def test_fused_c2_rowsum(bridge, rng, shape):
     assert O.within(y2, ref2, TOL32).all(), O.report(y2, ref2, TOL32)
 
 
+# reduce_last across row widths: narrow rows take as few lanes per row as
+# cover the row (1 ... 64), rows of 2048+ columns a whole workgroup, and
+# fewer than 512 such rows are cut into column chunks whose partials a
+# second kernel combines (16384+ columns, both vector widths, ragged last
+# chunks).  The data carry a positive offset, so a dropped or repeated
+# chunk moves a sum far outside the tolerance.
+@pytest.mark.parametrize("rows,cols", [(4099, 1), (5000, 2), (5000, 3), (3001, 5), (4096, 16), (1000, 17),
+                                       (777, 63), (1024, 64), (999, 65), (513, 100), (300, 255), (300, 256),
+                                       (100, 1000), (64, 2047), (1, 2048), (1, 16384), (1, 1 << 20),
+                                       (3, 100003), (7, 65536), (511, 8192), (512, 8192), (2, (1 << 21) + 4)])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_reduce_last_widths(bridge, rng, rows, cols, dtype):
+    if dtype == "float16" and cols > 100003:
+        pytest.skip("row sums beyond float16's range")
+    x = (rng.uniform(-1, 1, (rows, cols)) + 0.25).astype(np.float32)
+    if dtype == "float32":
+        hx = up(bridge, x)
+    else:
+        x16 = _to16(x, dtype)
+        hx = up(bridge, x16, dtype)
+        x = _from16(x16, dtype)
+    x64 = x.astype(np.float64)
+    refs = {1: x64.sum(axis=1), 2: x64.max(axis=1), 3: x64.mean(axis=1), 4: x64.min(axis=1)}
+    bound = 1e-5 * np.abs(x64).sum(axis=1) + 1e-6
+    for op, ref in refs.items():
+        h = bridge.reduce_last(hx, rows, cols, op)
+        y = bridge.to_numpy(h)
+        bridge.release(h)
+        assert y.shape == (rows,)
+        if dtype != "float32":
+            y32, r32 = _from16(y, dtype), _from16(_to16(ref.astype(np.float32), dtype), dtype)
+            assert O.within(y32, r32, TOL16).all(), (op, O.report(y32, r32, TOL16))
+        elif op in (2, 4):
+            assert np.array_equal(y, ref.astype(np.float32)), op
+        else:
+            err = np.abs(y.astype(np.float64) - ref)
+            b = bound / cols if op == 3 else bound
+            assert (err <= b).all(), (op, float(err.max()), float(b.min()))
+    bridge.release(hx)
+
+
+def _reduce_plan(shape, axis, op, dtype):
+    ax = axis if isinstance(axis, list) else [axis]
+    oshape = [d for i, d in enumerate(shape) if i not in ax]
+
+    def st(i, code, ins, shp, arg=None):
+        return {"step": i, "value_id": i, "op": code, "input_ids": ins, "shape": list(shp), "dtype": dtype,
+                "arg": arg}
+    return {"steps": [st(0, "BUFFER", [], shape),
+                      st(1, "REDUCE", [0], oshape, {"op": op, "axis": axis, "keepdims": False})],
+            "buffers": [], "root_id": 1, "materialization_boundary": "root", "peak_live_bytes": 0,
+            "has_custom_ops": False}, tuple(ax)
+
+
+# Plan REDUCE over a leading prefix of the axes (a bias gradient's sum over
+# the batch) reads the input in place: 4, 16 or 64 column lanes per
+# wavefront by width, vector and scalar columns, one row chunk (final
+# result written directly) and many (partials combined by a second kernel).
+@pytest.mark.parametrize("shape,axis", [((4099, 768), 0), ((3, 5, 64), [0, 1]), ((1000, 3), 0), ((16, 17), 0),
+                                        ((100000, 16), 0), ((7, 2050), 0), ((2, 3, 4, 40), [0, 1, 2]),
+                                        ((20000, 64), 0), ((1, 4096), 0), ((300, 50), 0)])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_plan_reduce_leading_axes(bridge, rng, shape, axis, dtype):
+    x = (rng.uniform(-1, 1, shape) + 0.25).astype(np.float32)
+    if dtype == "float32":
+        hx = up(bridge, x)
+    else:
+        x16 = _to16(x, dtype)
+        hx = up(bridge, x16, dtype)
+        x = _from16(x16, dtype)
+    x64 = x.astype(np.float64)
+    for op in ("sum", "mean", "max", "min"):
+        plan, ax = _reduce_plan(shape, axis, op, dtype)
+        h = bridge.run_tensor_plan_resident(plan, [{"value_id": 0, "handle": hx}], dtype)
+        y = bridge.to_numpy(h)
+        bridge.release(h)
+        ref = getattr(x64, op)(axis=ax)
+        n = int(np.prod([shape[a] for a in ax]))
+        if dtype != "float32":
+            y32, r32 = _from16(y, dtype).reshape(ref.shape), _from16(_to16(ref.astype(np.float32), dtype), dtype)
+            assert O.within(y32, r32, TOL16).all(), (op, O.report(y32, r32, TOL16))
+        elif op in ("max", "min"):
+            assert np.array_equal(y.reshape(ref.shape), ref.astype(np.float32)), op
+        else:
+            bound = 1e-5 * np.abs(x64).sum(axis=ax) + 1e-6
+            err = np.abs(y.reshape(ref.shape).astype(np.float64) - ref)
+            b = bound / n if op == "mean" else bound
+            assert (err <= b).all(), (op, float(err.max()), float(b.min()))
+    bridge.release(hx)
+
+
 def test_fused_reference_opcodes_bit_exact(bridge, rng):
     # ADD/MUL/DIV/NEG are IEEE single ops: bit-exact against NumPy.
     a = rng.standard_normal((257, 31)).astype(np.float32)

@@ -218,9 +218,10 @@ void launch_softmax_last(bg_ctx* ctx, const void* x, int x_dtype, void* y, int y
 // part[r * nch + 0 .. nch), combined in a fixed order (MEAN divides by cols).
 void launch_reduce_partials(bg_ctx* ctx, const float* part, int64_t rows, int64_t nch, int op,
                             int64_t cols, void* out, int out_dtype);
-// x[R][C] (f32, f16 or bf16, contiguous) reduced with BG_RED_* `op` over
-// its leading axis into out[C] of x's dtype.
-void launch_reduce_lead(bg_ctx* ctx, const void* x, int xd, int64_t R, int64_t C, int op, void* out);
+// x[B][R][C] (f32, f16 or bf16, contiguous) reduced with BG_RED_* `op` over
+// R into out[B][C] of dtype od (f32, f16 or bf16).
+void launch_reduce_lead(bg_ctx* ctx, const void* x, int xd, int64_t B, int64_t R, int64_t C, int op, void* out,
+                        int od);
 // Extras of bg_matmul_ex2: operand storage dtypes converted in a pre-pass
 // and an f32 residual added after the epilogue.
 struct GemmExtra {

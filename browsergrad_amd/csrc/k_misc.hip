@@ -809,14 +809,15 @@ __global__ void __launch_bounds__(256) reduce_partials_kernel(const float* __res
   store_from_f32(out, out_dtype, row, op == BG_RED_MEAN ? acc / cols : acc);
 }
 
-// Reduction of x[R][C] over its leading axis R (the per-column sums of a
-// bias gradient), reading x once in place.  Workgroup = 4 wavefronts; a
+// Reduction of x[B][R][C] over R (B = 1: the per-column sums of a bias
+// gradient; B > 1: a block of middle axes), reading x once in place.  Workgroup = 4 wavefronts; a
 // wavefront's lanes are LC column lanes (V adjacent columns each, so a row
 // segment of LC * V columns is read contiguously) x 64 / LC row lanes.
-// Workgroup u covers column group u % ngroups and rows of chunk u / ngroups;
-// inside it row r goes to row lane (r - r0) % (4 * 64 / LC).  Row lanes
-// combine by a butterfly, wavefronts in order 0..3 through LDS.  With one
-// chunk the result is final, otherwise it is the chunk's partial.
+// Workgroup u covers batch b = u / (ngroups * nchunk) and, within it, a
+// column group and the rows of one chunk; inside it row r goes to row lane
+// (r - r0) % (4 * 64 / LC).  Row lanes combine by a butterfly, wavefronts
+// in order 0..3 through LDS.  With one chunk the result is final, otherwise
+// it is the chunk's partial, stored at part[(chunk * B + b) * C + col].
 template <int XD, int V>
 __device__ __forceinline__ void load_v(const void* x, int64_t i, float (&v)[V]) {
   if constexpr (XD == 0) {
@@ -841,8 +842,9 @@ __device__ __forceinline__ void load_v(const void* x, int64_t i, float (&v)[V]) 
 
 template <int XD, int V, int LC>
 __global__ void __launch_bounds__(256) reduce_lead_kernel(const void* __restrict__ x, int64_t R, int64_t C,
-                                                          int64_t CR, int64_t ngroups, int op, float* part,
-                                                          int final_out, void* out, int od) {
+                                                          int64_t CR, int64_t ngroups, int64_t nchunk,
+                                                          int64_t B, int op, float* part, int final_out,
+                                                          void* out, int od) {
   constexpr int RL = 64 / LC;
   __shared__ float red[4][64 * V];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -850,8 +852,12 @@ __global__ void __launch_bounds__(256) reduce_lead_kernel(const void* __restrict
   // Column groups rotate with the chunk, so the workgroups that share an
   // XCD (every eighth in dispatch order) do not all read the same few
   // column groups when ngroups divides by 8.
-  const int64_t chunk = blockIdx.x / ngroups;
-  const int64_t group = (blockIdx.x % ngroups + chunk) % ngroups;
+  const int64_t per_b = ngroups * nchunk;
+  const int64_t b = blockIdx.x / per_b;
+  const int64_t u = blockIdx.x - b * per_b;
+  const int64_t chunk = u / ngroups;
+  const int64_t group = (u % ngroups + chunk) % ngroups;
+  x = static_cast<const char*>(x) + b * R * C * (XD == 0 ? 4 : 2);
   const int64_t col = (group * LC + cl) * V;
   const int64_t r0 = chunk * CR;
   const int64_t r1 = r0 + CR < R ? r0 + CR : R;
@@ -884,9 +890,9 @@ __global__ void __launch_bounds__(256) reduce_lead_kernel(const void* __restrict
     a = red_combine(op, a, red[2][cl * V + j]);
     a = red_combine(op, a, red[3][cl * V + j]);
     if (final_out)
-      store_from_f32(out, od, col + j, op == BG_RED_MEAN ? a / static_cast<float>(R) : a);
+      store_from_f32(out, od, b * C + col + j, op == BG_RED_MEAN ? a / static_cast<float>(R) : a);
     else
-      part[chunk * C + col + j] = a;
+      part[(chunk * B + b) * C + col + j] = a;
   }
 }
 
@@ -913,6 +919,18 @@ __global__ void __launch_bounds__(1024) reduce_lead_final_kernel(const float* __
   float a = red[0][cx];
 #pragma unroll
   for (int w = 1; w < 16; ++w) a = red_combine(op, a, red[w][cx]);
+  store_from_f32(out, od, c, op == BG_RED_MEAN ? a / R : a);
+}
+
+// Second pass for few chunks (at most 32): a thread per column folds its
+// chunks in order.
+__global__ void __launch_bounds__(256) reduce_lead_final_few_kernel(const float* __restrict__ part, int64_t nchunk,
+                                                                    int64_t C, int op, float R, void* out, int od) {
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= C) return;
+  float a = part[c];
+#pragma unroll 8
+  for (int64_t k = 1; k < nchunk; ++k) a = red_combine(op, a, part[k * C + c]);
   store_from_f32(out, od, c, op == BG_RED_MEAN ? a / R : a);
 }
 
@@ -1038,10 +1056,13 @@ static bool launch_softmax_row(bg_ctx* ctx, const void* x, int xd, void* y, int 
   return true;
 }
 
-// x[R][C] reduced over R into out[C] (dtype of x); see reduce_lead_kernel.
-void launch_reduce_lead(bg_ctx* ctx, const void* x, int xd, int64_t R, int64_t C, int op, void* out) {
-  if (R <= 0 || C <= 0) fail(BG_E_SHAPE, "reduce: empty reduction");
+// x[B][R][C] reduced over R into out[B][C] of dtype od; see
+// reduce_lead_kernel.
+void launch_reduce_lead(bg_ctx* ctx, const void* x, int xd, int64_t B, int64_t R, int64_t C, int op, void* out,
+                        int od) {
+  if (B <= 0 || R <= 0 || C <= 0) fail(BG_E_SHAPE, "reduce: empty reduction");
   if (xd != BG_F32 && xd != BG_F16 && xd != BG_BF16) fail(BG_E_DTYPE, "reduce: dtype not supported");
+  if (od != BG_F32 && od != BG_F16 && od != BG_BF16) fail(BG_E_DTYPE, "reduce: output dtype not supported");
   const int es = xd == BG_F32 ? 4 : 2;
   const bool v4 = C % 4 == 0 && reinterpret_cast<uintptr_t>(x) % uintptr_t(4 * es) == 0;
   const int V = v4 ? 4 : 1;
@@ -1051,18 +1072,19 @@ void launch_reduce_lead(bg_ctx* ctx, const void* x, int xd, int64_t R, int64_t C
   const int64_t rstep = 4 * (64 / LC);  // rows one workgroup pass reads
   // Chunks of whole workgroup passes (at least 8) until about 1024
   // workgroups stream x.
-  int64_t nchunk = std::max<int64_t>(1, std::min<int64_t>((1024 + ngroups - 1) / ngroups,
+  int64_t nchunk = std::max<int64_t>(1, std::min<int64_t>((1024 + B * ngroups - 1) / (B * ngroups),
                                                         (R + 8 * rstep - 1) / (8 * rstep)));
   int64_t CR = (R + nchunk - 1) / nchunk;
   CR = (CR + rstep - 1) / rstep * rstep;
   nchunk = (R + CR - 1) / CR;
-  const int64_t units = ngroups * nchunk;
+  const int64_t units = B * ngroups * nchunk;
   if (units > int64_t(0x7fffffff)) fail(BG_E_UNSUPPORTED, "reduce: too many column groups");
-  float* part = nchunk > 1 ? static_cast<float*>(scratch(ctx, size_t(nchunk * C) * 4, 0)) : nullptr;
+  float* part = nchunk > 1 ? static_cast<float*>(scratch(ctx, size_t(nchunk * B * C) * 4, 0)) : nullptr;
   const int fin = nchunk == 1 ? 1 : 0;
   auto go = [&](auto xdc, auto vc, auto lcc) {
     bg::dispatch(ctx, reduce_lead_kernel<decltype(xdc)::value, decltype(vc)::value, decltype(lcc)::value>,
-                 dim3(static_cast<unsigned>(units)), dim3(256), 0, x, R, C, CR, ngroups, op, part, fin, out, xd);
+                 dim3(static_cast<unsigned>(units)), dim3(256), 0, x, R, C, CR, ngroups, nchunk, B, op, part, fin,
+                 out, od);
   };
   auto by_lc = [&](auto xdc, auto vc) {
     if (LC == 4) go(xdc, vc, std::integral_constant<int, 4>{});
@@ -1076,9 +1098,12 @@ void launch_reduce_lead(bg_ctx* ctx, const void* x, int xd, int64_t R, int64_t C
   if (xd == BG_F32) by_v(std::integral_constant<int, 0>{});
   else if (xd == BG_F16) by_v(std::integral_constant<int, 1>{});
   else by_v(std::integral_constant<int, 2>{});
-  if (nchunk > 1)
-    bg::dispatch(ctx, reduce_lead_final_kernel, dim3(static_cast<unsigned>((C + 15) / 16)), dim3(1024), 0,
-                 static_cast<const float*>(part), nchunk, C, op, static_cast<float>(R), out, xd);
+  if (nchunk > 32)
+    bg::dispatch(ctx, reduce_lead_final_kernel, dim3(static_cast<unsigned>((B * C + 15) / 16)), dim3(1024), 0,
+                 static_cast<const float*>(part), nchunk, B * C, op, static_cast<float>(R), out, od);
+  else if (nchunk > 1)
+    bg::dispatch(ctx, reduce_lead_final_few_kernel, dim3(static_cast<unsigned>((B * C + 255) / 256)), dim3(256), 0,
+                 static_cast<const float*>(part), nchunk, B * C, op, static_cast<float>(R), out, od);
 }
 
 void launch_reduce_partials(bg_ctx* ctx, const float* part, int64_t rows, int64_t nch, int op,

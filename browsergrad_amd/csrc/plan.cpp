@@ -1294,22 +1294,63 @@ struct Runner {
     bool trailing = true;
     for (int64_t i = 0; i < int64_t(red.size()); ++i)
       if (!red.count(rank - 1 - i)) trailing = false;
-    // Reduced axes that form a leading prefix (a bias gradient's sum over
-    // the batch): one pass over the input in place instead of a transposing
-    // copy followed by a row reduction.
-    bool leading = true;
-    for (int64_t i = 0; i < int64_t(red.size()); ++i)
-      if (!red.count(i)) leading = false;
-    if (!trailing && leading && cols > 0 && rows > 0 &&
-        (r.dtype == BG_F32 || r.dtype == BG_F16 || r.dtype == BG_BF16)) {
+    // Reduced axes that are not all trailing, without a transposing copy:
+    //  - one contiguous block of axes [a0, a1) (a leading prefix is the bias
+    //    gradient's sum over the batch): x read in place as
+    //    [B = dims before a0][R = the block][C = dims from a1];
+    //  - a leading prefix plus a trailing suffix (batch and spatial axes of
+    //    [N, C, L]): the suffix by the fused row reduction into f32, then
+    //    the prefix in place.
+    if (!trailing && cols > 0 && rows > 0 && (r.dtype == BG_F32 || r.dtype == BG_F16 || r.dtype == BG_BF16)) {
       if (numel(s.shape) != rows) plan_fail("REDUCE output shape differs from the plan");
       const int dt = r.dtype;
       if (dt != plan_dtype(s.dtype, "REDUCE dtype")) fail(BG_E_DTYPE, "tensor plan REDUCE dtype differs");
+      const std::vector<int64_t> ax(red.begin(), red.end());  // ascending
+      const std::vector<int64_t> shp = r.shape;
+      auto prod = [&](int64_t lo, int64_t hi) {
+        int64_t v = 1;
+        for (int64_t i = lo; i < hi; ++i) v *= shp[size_t(i)];
+        return v;
+      };
       const int64_t es = dtype_size(dt);
-      bg_handle out = own(mint(ctx, size_t(rows * es), s.shape, dt));
-      Profile prof(ctx, "reduce_lead", (rows * cols + rows) * es, rows * cols);
-      launch_reduce_lead(ctx, rec(src).ptr(), dt, cols, rows, rop, ctx->handles[out].ptr());
-      return out;
+      const int64_t na = int64_t(ax.size());
+      if (ax.back() - ax.front() + 1 == na) {
+        const int64_t a0 = ax.front(), a1 = ax.back() + 1;
+        bg_handle out = own(mint(ctx, size_t(rows * es), s.shape, dt));
+        Profile prof(ctx, "reduce_lead", (rows * cols + rows) * es, rows * cols);
+        launch_reduce_lead(ctx, rec(src).ptr(), dt, prod(0, a0), cols, prod(a1, rank), rop, ctx->handles[out].ptr(),
+                           dt);
+        return out;
+      }
+      int64_t np = 0;
+      while (np < na && ax[size_t(np)] == np) ++np;
+      const int64_t s0 = ax[size_t(np)];
+      const bool suffix = np > 0 && ax.back() == rank - 1 && ax.back() - s0 + 1 == na - np;
+      if (suffix) {
+        const int64_t P = prod(0, np), M = prod(np, s0), L = prod(s0, rank);
+        bg_fused_op cp{BG_OP_COPY, -1, 0, 0};
+        int64_t rs[2] = {P * M, L};
+        bg_fused_desc d{};
+        d.n_inputs = 1;
+        d.inputs = &src;
+        d.n_ops = 1;
+        d.ops = &cp;
+        d.rank = 2;
+        d.shape = rs;
+        d.out_dtype = BG_F32;
+        d.reduce_op = rop;
+        bg_handle y = 0;
+        call(bg_fused_ex(ctx, &d, &y));
+        own(y);
+        bg_handle out = own(mint(ctx, size_t(rows * es), s.shape, dt));
+        {
+          Profile prof(ctx, "reduce_lead", P * M * 4 + rows * es, P * M);
+          launch_reduce_lead(ctx, rec(y).ptr(), BG_F32, 1, P, M, rop, ctx->handles[out].ptr(), dt);
+        }
+        bg_release(ctx, y);
+        owned.erase(y);
+        return out;
+      }
     }
     bg_handle x = src;
     if (!trailing) {

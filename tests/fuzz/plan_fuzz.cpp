@@ -37,7 +37,7 @@ void launch_optimizer_fused(bg_ctx*, int, const bg_optim_args&, double, double, 
                             const float* const (&)[4], float*, int64_t) {
   absent();
 }
-void launch_reduce_lead(bg_ctx*, const void*, int, int64_t, int64_t, int, void*) { absent(); }
+void launch_reduce_lead(bg_ctx*, const void*, int, int64_t, int64_t, int64_t, int, void*, int) { absent(); }
 int64_t dtype_size(int) { absent(); }
 }  // namespace bg
 

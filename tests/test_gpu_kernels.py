@@ -225,13 +225,19 @@ def _reduce_plan(shape, axis, op, dtype):
             "has_custom_ops": False}, tuple(ax)
 
 
-# Plan REDUCE over a leading prefix of the axes (a bias gradient's sum over
-# the batch) reads the input in place: 4, 16 or 64 column lanes per
-# wavefront by width, vector and scalar columns, one row chunk (final
-# result written directly) and many (partials combined by a second kernel).
+# Plan REDUCE over a contiguous block of axes that is not trailing (a
+# leading prefix: a bias gradient's sum over the batch) reads the input in
+# place: 4, 16 or 64 column lanes per wavefront by width, vector and scalar
+# columns, one row chunk (final result written directly) and many (partials
+# combined by a second kernel), batches of such blocks (middle axes).  A
+# leading prefix plus a trailing suffix is a row reduction into f32, then
+# the prefix; other axis sets transpose first.
 @pytest.mark.parametrize("shape,axis", [((4099, 768), 0), ((3, 5, 64), [0, 1]), ((1000, 3), 0), ((16, 17), 0),
                                         ((100000, 16), 0), ((7, 2050), 0), ((2, 3, 4, 40), [0, 1, 2]),
-                                        ((20000, 64), 0), ((1, 4096), 0), ((300, 50), 0)])
+                                        ((20000, 64), 0), ((1, 4096), 0), ((300, 50), 0),
+                                        ((4, 6, 40), 1), ((8, 300, 64), 1), ((5, 2000, 3), 1),
+                                        ((64, 32, 100), [0, 2]), ((2, 3, 4, 40), [0, 3]),
+                                        ((16, 8, 5, 7), [0, 1, 3]), ((6, 5, 4, 3), [0, 2]), ((3, 4, 5), [1, 2])])
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
 def test_plan_reduce_leading_axes(bridge, rng, shape, axis, dtype):
     x = (rng.uniform(-1, 1, shape) + 0.25).astype(np.float32)

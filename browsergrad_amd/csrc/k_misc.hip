@@ -196,6 +196,107 @@ __global__ void __launch_bounds__(256) copy_strided_kernel(const T* __restrict__
   }
 }
 
+// Unsigned 32-bit division by a runtime constant as a multiply-high and a
+// shift (the round-up method of Granlund and Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994): for d >= 1,
+// l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, and
+// n / d = (mulhi(n, m) + ((n - mulhi(n, m)) >> 1)) >> (l - 1) for l >= 1,
+// n itself for d = 1; exact for every 32-bit n.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+static FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0u, 0u};
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+  f.s = l;
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  if (f.d == 1) return n;
+  const uint32_t t = __umulhi(n, f.m);
+  return (t + ((n - t) >> 1)) >> (f.s - 1);
+}
+
+// Row copy: dst[row][v] = src[off(row) + v] in 16-byte pieces, rows of
+// `rv` pieces; off(row) from up to 3 outer dims (byte strides).
+struct RowCopyArgs {
+  FastDiv rv;          // pieces per row
+  FastDiv dim[3];      // outer dims, innermost first
+  int64_t bstride[3];  // their source strides in bytes
+  int nd;
+  uint32_t total;      // pieces in all
+};
+
+__global__ void __launch_bounds__(256) copy_rows16_kernel(const char* __restrict__ src, uint4* __restrict__ dst,
+                                                          RowCopyArgs A) {
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < A.total; i += gridDim.x * 256u) {
+    uint32_t row = fdiv(i, A.rv);
+    const uint32_t v = i - row * A.rv.d;
+    int64_t off = int64_t(v) * 16;
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      if (d < A.nd) {
+        const uint32_t q = fdiv(row, A.dim[d]);
+        off += int64_t(row - q * A.dim[d].d) * A.bstride[d];
+        row = q;
+      }
+    }
+    dst[i] = *reinterpret_cast<const uint4*>(src + off);
+  }
+}
+
+// Batched transpose through LDS: dst is [batch...][K][I] in the collapsed
+// order with I innermost, the source has I at stride si and K at stride 1.
+// A 64 x 64 tile is read along K (coalesced), written along I.
+struct TransposeArgs {
+  int64_t I, K, si, dk;  // dk: destination stride of K (elements)
+  int64_t tiles_i, tiles_k;
+  FastDiv bdim[2];       // batch dims, innermost first
+  int64_t bsrc[2], bdst[2];
+  int nb;
+  int kfast;             // consecutive workgroups step along K (else along I)
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) copy_transpose_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                             TransposeArgs A) {
+  __shared__ T tile[64][65];
+  const int64_t per_b = A.tiles_i * A.tiles_k;
+  uint32_t b = static_cast<uint32_t>(blockIdx.x / per_b);
+  const int64_t t = blockIdx.x - int64_t(b) * per_b;
+  const int64_t i0 = (A.kfast ? t / A.tiles_k : t % A.tiles_i) * 64;
+  const int64_t k0 = (A.kfast ? t % A.tiles_k : t / A.tiles_i) * 64;
+  int64_t so = 0, dof = 0;
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    if (d < A.nb) {
+      const uint32_t q = fdiv(b, A.bdim[d]);
+      const int64_t idx = b - q * A.bdim[d].d;
+      so += idx * A.bsrc[d];
+      dof += idx * A.bdst[d];
+      b = q;
+    }
+  }
+  const int lane = threadIdx.x & 63, row = threadIdx.x >> 6;
+  // Read: lane along K (source stride 1), rows along I.
+#pragma unroll 4
+  for (int r = row; r < 64; r += 4) {
+    const int64_t i = i0 + r, k = k0 + lane;
+    if (i < A.I && k < A.K) tile[r][lane] = src[so + i * A.si + k];
+  }
+  __syncthreads();
+  // Write: lane along I (destination stride 1), rows along K.
+#pragma unroll 4
+  for (int r = row; r < 64; r += 4) {
+    const int64_t i = i0 + lane, k = k0 + r;
+    if (i < A.I && k < A.K) dst[dof + k * A.dk + i] = tile[lane][r];
+  }
+}
+
 // ---- Softmax over the last axis (FUSED_SOFTMAX) -------------------------------
 // The reference kernel's order (kernels/softmax.ts:22-69): m = max(x);
 // e = exp(x - m); y = e * (1 / sum(e)).  One wavefront per row, the row held
@@ -995,19 +1096,106 @@ void launch_cast_transpose(bg_ctx* ctx, const void* src, int sd, void* dst, int 
 
 void launch_copy_strided(bg_ctx* ctx, const void* src, int64_t es, void* dst,
                          const std::vector<int64_t>& shape, const std::vector<int64_t>& strides) {
-  CopyArgs A{};
-  A.rank = int(shape.size());
-  A.n = 1;
-  for (int i = 0; i < A.rank; ++i) {
-    A.shape[i] = shape[i];
-    A.stride[i] = strides[i];
-    A.n *= shape[i];
+  int64_t n = 1;
+  for (int64_t v : shape) n *= v;
+  if (n == 0) return;
+  // Collapse: drop unit dims, merge a dim into the next one when the pair is
+  // contiguous in the source.
+  std::vector<int64_t> sh, st;
+  for (size_t i = 0; i < shape.size(); ++i) {
+    if (shape[i] == 1) continue;
+    if (!sh.empty() && st.back() == strides[i] * shape[i]) {
+      sh.back() *= shape[i];
+      st.back() = strides[i];
+    } else {
+      sh.push_back(shape[i]);
+      st.push_back(strides[i]);
+    }
   }
-  if (A.n == 0) return;
-  if (A.rank == 0) {
-    A.rank = 1;
-    A.shape[0] = 1;
-    A.stride[0] = 0;
+  if (sh.empty()) {
+    sh.push_back(1);
+    st.push_back(1);
+  }
+  const int r = int(sh.size());
+  bool nonneg = true;
+  for (int64_t v : st) nonneg &= v >= 0;
+  const bool fast = std::getenv("BG_COPY_GENERIC") == nullptr && nonneg && n * es < (int64_t(1) << 32);
+  const uintptr_t sa = reinterpret_cast<uintptr_t>(src), da = reinterpret_cast<uintptr_t>(dst);
+  // Rows contiguous in the source, in 16-byte pieces.
+  if (fast && st.back() == 1 && r <= 4 && (sh.back() * es) % 16 == 0 && sa % 16 == 0 && da % 16 == 0) {
+    bool ok = true;
+    for (int d = 0; d < r - 1; ++d) ok &= (st[d] * es) % 16 == 0;
+    if (ok) {
+      RowCopyArgs A{};
+      A.rv = make_fastdiv(uint32_t(sh.back() * es / 16));
+      A.nd = r - 1;
+      for (int d = 0; d < r - 1; ++d) {
+        A.dim[d] = make_fastdiv(uint32_t(sh[r - 2 - d]));
+        A.bstride[d] = st[r - 2 - d] * es;
+      }
+      A.total = uint32_t(n * es / 16);
+      const unsigned g = unsigned(std::min<int64_t>((A.total + 255) / 256, 256 * 32));
+      bg::dispatch(ctx, copy_rows16_kernel, dim3(g), dim3(256), 0, static_cast<const char*>(src),
+                   static_cast<uint4*>(dst), A);
+      return;
+    }
+  }
+  // A transpose: the innermost destination dim is strided in the source and
+  // another dim is the source's contiguous one; at most two more dims.
+  if (fast && st.back() != 1 && r >= 2 && r <= 4) {
+    int k = -1;
+    for (int d = 0; d < r - 1; ++d)
+      if (st[d] == 1) k = d;
+    if (k >= 0) {
+      TransposeArgs A{};
+      A.I = sh[r - 1];
+      A.K = sh[k];
+      A.si = st[r - 1];
+      std::vector<int64_t> dstr(r);
+      int64_t acc = 1;
+      for (int d = r - 1; d >= 0; --d) {
+        dstr[d] = acc;
+        acc *= sh[d];
+      }
+      A.dk = dstr[k];
+      A.tiles_i = (A.I + 63) / 64;
+      A.tiles_k = (A.K + 63) / 64;
+      // Step the longer tile axis fastest (measured: [65536, 768] and
+      // [8192, 4096] transposes 7-15% faster along K, [1000, 3000] 14%
+      // faster along I).
+      A.kfast = A.tiles_i >= A.tiles_k;
+      int64_t batch = 1;
+      for (int d = r - 2; d >= 0; --d) {
+        if (d == k) continue;
+        A.bdim[A.nb] = make_fastdiv(uint32_t(sh[d]));
+        A.bsrc[A.nb] = st[d];
+        A.bdst[A.nb] = dstr[d];
+        ++A.nb;
+        batch *= sh[d];
+      }
+      const int64_t blocks = batch * A.tiles_i * A.tiles_k;
+      if (blocks < (int64_t(1) << 31)) {
+        const dim3 g(static_cast<unsigned>(blocks));
+        switch (es) {
+          case 1: bg::dispatch(ctx, copy_transpose_kernel<uint8_t>, g, dim3(256), 0,
+                               static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), A); return;
+          case 2: bg::dispatch(ctx, copy_transpose_kernel<uint16_t>, g, dim3(256), 0,
+                               static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), A); return;
+          case 4: bg::dispatch(ctx, copy_transpose_kernel<uint32_t>, g, dim3(256), 0,
+                               static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), A); return;
+          case 8: bg::dispatch(ctx, copy_transpose_kernel<uint64_t>, g, dim3(256), 0,
+                               static_cast<const uint64_t*>(src), static_cast<uint64_t*>(dst), A); return;
+          default: break;
+        }
+      }
+    }
+  }
+  CopyArgs A{};
+  A.rank = r;
+  A.n = n;
+  for (int i = 0; i < r; ++i) {
+    A.shape[i] = sh[i];
+    A.stride[i] = st[i];
   }
   const int g = grid1(A.n, 256);
   switch (es) {

@@ -6,7 +6,7 @@ import bench
 
 
 def test_traffic_reported_for_the_measured_generator():
-    assert bench.measured_traffic() == 201509369
+    assert bench.measured_traffic() == 201516282
 
 
 def test_traffic_is_null_once_the_generator_changes(tmp_path, monkeypatch):

@@ -406,6 +406,55 @@ def test_copy_strided_permute(bridge, rng):
     assert np.array_equal(y, np.transpose(x, perm))
 
 
+# Strided copies by path: rows contiguous in the source copied in 16-byte
+# pieces (head split/merge permutes, slices of rows), tiled transposes (the
+# source's contiguous dim moved outward, with 0-2 batch dims, ragged tiles,
+# 1/2/4/8-byte elements, a broadcast innermost dim), and the generic
+# element kernel (negative strides, odd row bytes, 5+ collapsed dims).
+# Each copy is checked bit-exactly against NumPy's view of the same bytes.
+COPY_CASES = [
+    ((2, 128, 12, 64), (0, 2, 1, 3), None),   # [B,S,H,D] -> [B,H,S,D]
+    ((2, 12, 128, 64), (0, 2, 1, 3), None),   # and back
+    ((4096, 768), (1, 0), None),               # 2-D transpose
+    ((3, 100, 70), (0, 2, 1), None),           # batched, ragged tiles
+    ((5, 7, 9, 11), (3, 1, 0, 2), None),       # rank 4, two batch dims
+    ((8, 64, 56, 56), (0, 2, 3, 1), None),     # NCHW -> NHWC
+    ((8, 56, 56, 64), (0, 3, 1, 2), None),     # NHWC -> NCHW
+    ((2, 3, 4, 5, 6, 7), (5, 0, 4, 1, 3, 2), None),  # rank 6: generic kernel
+    ((64, 48), None, "slice_rows"),            # rows of a slice
+    ((33, 47), None, "reverse"),               # negative stride
+    ((40, 30), None, "broadcast_inner"),       # innermost stride 0
+    ((17, 13), None, "every_other"),           # innermost stride 2, no stride-1 dim
+]
+
+
+def _copy_case(x, perm, kind):
+    es = x.itemsize
+    st = [v // es for v in x.strides]
+    if perm is not None:
+        return 0, [x.shape[p] for p in perm], [st[p] for p in perm], np.transpose(x, perm)
+    if kind == "slice_rows":  # rows 5..36 of every 4th column block of 16
+        return 5 * st[0] + 16, [32, 16], [st[0], 1], x[5:37, 16:32]
+    if kind == "reverse":
+        return (x.shape[0] - 1) * st[0], [x.shape[0], x.shape[1]], [-st[0], 1], x[::-1]
+    if kind == "broadcast_inner":
+        return 0, [x.shape[0], x.shape[1], 9], [st[0], 1, 0], np.broadcast_to(x[:, :, None], x.shape + (9,))
+    return 0, [x.shape[0], (x.shape[1] + 1) // 2], [st[0], 2], x[:, ::2]
+
+
+@pytest.mark.parametrize("shape,perm,kind", COPY_CASES)
+@pytest.mark.parametrize("dtype", ["float32", "float16", "uint8", "int64"])
+def test_copy_strided_paths(bridge, rng, shape, perm, kind, dtype):
+    if dtype == "int64":
+        x = rng.integers(-2**62, 2**62, size=shape, dtype=np.int64)
+    else:
+        x = (rng.standard_normal(shape) * 100).astype(dtype)
+    h = up(bridge, x)
+    off, shp, strides, ref = _copy_case(x, perm, kind)
+    y = bridge.to_numpy(bridge.copy_strided(h, off, shp, strides))
+    assert y.shape == ref.shape and np.array_equal(y.view(np.uint8), np.ascontiguousarray(ref).view(np.uint8))
+
+
 @pytest.mark.parametrize("b,h,s,causal", [(1, 2, 4, False), (2, 3, 128, True), (1, 2, 200, True),
                                           (2, 2, 256, False), (1, 1, 1000, True)])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])

@@ -58,6 +58,11 @@ struct FusedArgs {
   int64_t cw;
   int64_t nch;
   float* part;
+  // Division by runtime constants (Granlund-Montgomery round-up method):
+  // divisor, multiplier, shift of the vectors per row (map kernels) and of
+  // each leading dim (strided inputs).
+  uint32_t vc_d, vc_m, vc_s;
+  uint32_t dim_d[kMaxDims], dim_m[kMaxDims], dim_s[kMaxDims];
 };
 
 const char* kPrelude = R"(
@@ -75,6 +80,8 @@ struct Args {
   i64 cw;
   i64 nch;
   float* part;
+  u32 vc_d, vc_m, vc_s;
+  u32 dim_d[4], dim_m[4], dim_s[4];
 };
 typedef float f4v_ __attribute__((ext_vector_type(4)));
 typedef u32 u2v_ __attribute__((ext_vector_type(2)));
@@ -85,6 +92,11 @@ __device__ __forceinline__ u16 bg_f2b(float f) { return __builtin_bit_cast(u16, 
 __device__ __forceinline__ float bg_rh(float x) { return (float)(_Float16)x; }
 __device__ __forceinline__ float bg_rb(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float bg_max(float a, float b) { return (a != a || b != b) ? a + b : fmaxf(a, b); }
+__device__ __forceinline__ u32 bg_fdiv(u32 n, u32 d, u32 m, u32 s) {
+  if (d == 1u) return n;
+  const u32 t = (u32)(((unsigned long long)n * m) >> 32);
+  return (t + ((n - t) >> 1)) >> (s - 1u);
+}
 __device__ __forceinline__ float bg_min(float a, float b) { return (a != a || b != b) ? a + b : fminf(a, b); }
 )";
 
@@ -224,9 +236,13 @@ void emit_body(std::ostringstream& os, const Plan& p, int V) {
   bool any_strided = false;
   for (int i = 0; i < p.n_in; ++i) any_strided |= p.kind[i] == IN_STRIDED;
   if (any_strided) {
+    // The outermost leading index is what remains (row < rows), the others
+    // come from multiply-high divisions.
     os << "    u32 idx[4] = {0u, 0u, 0u, 0u};\n    { u32 rr = (u32)row;\n";
-    for (int d = p.nlead - 1; d >= 0; --d)
-      os << "      idx[" << d << "] = rr % A.dims[" << d << "]; rr /= A.dims[" << d << "];\n";
+    for (int d = p.nlead - 1; d >= 1; --d)
+      os << "      { const u32 q = bg_fdiv(rr, A.dim_d[" << d << "], A.dim_m[" << d << "], A.dim_s[" << d
+         << "]); idx[" << d << "] = rr - q * A.dim_d[" << d << "]; rr = q; }\n";
+    if (p.nlead >= 1) os << "      idx[0] = rr;\n";
     os << "    }\n";
   }
   // Which inputs are used at all.
@@ -304,8 +320,11 @@ std::string generate(const Plan& p) {
        << "  const i64 nvec = A.rows * vcols;\n"
        << "  for (i64 g = (i64)blockIdx.x * 256 + threadIdx.x; g < nvec; g += (i64)gridDim.x * 256) {\n"
        << "    const i64 lin = g * " << V << ";\n"
-       << "    const i64 row = g / vcols;\n"
-       << "    const i64 col = (g - row * vcols) * " << V << ";\n";
+       // Fewer than 2^31 elements (the launcher's limit): 32-bit indices.
+       << "    const u32 g32 = (u32)g;\n"
+       << "    const u32 row32 = bg_fdiv(g32, A.vc_d, A.vc_m, A.vc_s);\n"
+       << "    const i64 row = row32;\n"
+       << "    const i64 col = (i64)(g32 - row32 * A.vc_d) * " << V << ";\n";
     emit_body(os, p, V);
     if (V == 4 && p.out_dtype == BG_F32) {
       os << "    f4v_ r = {s" << last << "[0], s" << last << "[1], s" << last << "[2], s" << last << "[3]};\n"
@@ -678,6 +697,17 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
       reinterpret_cast<uintptr_t>(A.out) % uintptr_t(4 * dtype_size(d.out_dtype)) != 0)
     v4 = false;
   plan.vec = v4 ? 4 : 1;
+  // Multiply-high division constants (Granlund and Montgomery, PLDI 1994,
+  // round-up method): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1.
+  auto magic = [](int64_t dv, uint32_t& d, uint32_t& m, uint32_t& sh) {
+    d = uint32_t(dv);
+    uint32_t l = 0;
+    while ((uint64_t(1) << l) < d) ++l;
+    m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+    sh = l;
+  };
+  magic(cols / plan.vec, A.vc_d, A.vc_m, A.vc_s);
+  for (size_t k = 0; k < lead.size(); ++k) magic(lead[k], A.dim_d[k], A.dim_m[k], A.dim_s[k]);
   // Lanes per row for reductions: the whole workgroup for wide rows, else
   // the fewest power-of-two lanes (at most a wavefront) that cover the row
   // in one vector each, so narrow rows do not leave most lanes idle.

@@ -268,6 +268,25 @@ def test_plan_reduce_leading_axes(bridge, rng, shape, axis, dtype):
     bridge.release(hx)
 
 
+# Broadcast operands index their leading dims by multiply-high division:
+# odd and large leading dims (up to 2^22 rows), 1-3 leading dims, scalar and
+# vector columns, column broadcasts, both with and without a reduction.
+@pytest.mark.parametrize("shape,bshape", [((7, 13, 2999, 5), (7, 1, 2999, 1)), ((5000, 3, 17), (1, 3, 1)),
+                                          ((4194305, 4), (4194305, 1)), ((3, 65537, 8), (3, 1, 8)),
+                                          ((6, 7, 11, 12), (1, 7, 1, 12)), ((1000, 1001), (1, 1001))])
+def test_fused_broadcast_index_math(bridge, rng, shape, bshape):
+    x = rng.standard_normal(shape).astype(np.float32)
+    b = rng.standard_normal(bshape).astype(np.float32)
+    hx, hb = up(bridge, x), up(bridge, b)
+    bst = [0 if d == 1 else int(np.prod(bshape[i + 1:])) for i, d in enumerate(bshape)]
+    xst = [int(np.prod(shape[i + 1:])) for i in range(len(shape))]
+    ops = [("ADD", -1, -2, 0)]
+    y = bridge.to_numpy(bridge.fused_ex([hx, hb], ops, shape, "float32", in_strides=[xst, bst]))
+    assert np.array_equal(y, x + b)
+    r = bridge.to_numpy(bridge.fused_ex([hx, hb], ops, shape, "float32", in_strides=[xst, bst], reduce=2))
+    assert np.array_equal(r, (x + b).max(axis=-1))
+
+
 def test_fused_reference_opcodes_bit_exact(bridge, rng):
     # ADD/MUL/DIV/NEG are IEEE single ops: bit-exact against NumPy.
     a = rng.standard_normal((257, 31)).astype(np.float32)

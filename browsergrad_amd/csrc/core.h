@@ -91,9 +91,9 @@ struct bg_ctx {
   // slot 0 = re-laid-out GEMM operand, slot 1 = f32 GEMM result awaiting an
   // elementwise epilogue pass.
   // GEMM scratch slots: 0 B re-layout / B cast, 1 f32 pre-GELU product,
-  // 2 A cast.
-  void* scratch[3] = {nullptr, nullptr, nullptr};
-  size_t scratch_bytes[3] = {0, 0, 0};
+  // 2 A cast, 3 split-K partials.
+  void* scratch[4] = {nullptr, nullptr, nullptr, nullptr};
+  size_t scratch_bytes[4] = {0, 0, 0, 0};
 
   // Device address of this device's fixed no-allocation scratch (NULL when
   // it could not be resolved; bg_matmul_noalloc then refuses).

@@ -921,6 +921,98 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch, int act) {
   return LdsCfg::T128x128x64s2;
 }
 
+// ---- Skinny 16-bit GEMM (M <= 64): K split over workgroups --------------
+// A 128-row tile would leave most of its rows and most CUs idle when M is
+// small; the problem is a stream over B.  Workgroup u (16 wavefronts) takes
+// 128 columns of C and the K range of split u % nsplit: wavefront w covers
+// columns 32 (w % 4) .. +31 and every fourth 16-deep step of the range,
+// starting at step w / 4, with one v_mfma_f32_32x32x16 per 32 rows of A,
+// operands loaded straight from global memory (lane l: row or column
+// l % 32, k = 8 (l / 32) .. +7 of the step; B stored [N][K]).  The four
+// K-interleaved wavefronts of a column block are summed through LDS in
+// order 0, 1, 2, 3.  With one split the epilogue runs here; otherwise f32
+// partials go to part[split][M][N] and gemm16_skinny_finish_kernel sums
+// them in split order and runs the epilogue.
+template <bool BF16, int MT>
+__global__ void __launch_bounds__(1024) gemm16_skinny_kernel(GemmArgs P, int64_t ks, int nsplit, float* part) {
+  __shared__ float red[3][4][MT][16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nsub = wave & 3, ksub = wave >> 2;
+  const int split = int(blockIdx.x % unsigned(nsplit));
+  const int64_t n0 = int64_t(blockIdx.x / unsigned(nsplit)) * 128 + nsub * 32;
+  const int64_t n = n0 + (lane & 31);
+  const bool n_ok = n < P.N;
+  const int64_t kb0 = int64_t(split) * ks;
+  const int64_t kb1 = kb0 + ks < P.K ? kb0 + ks : P.K;
+  const int kl = 8 * (lane >> 5);
+  const char* A = static_cast<const char*>(P.A);
+  const char* B = static_cast<const char*>(P.B) + (n_ok ? n : 0) * P.ldb * 2;
+  float16v acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll 4
+  for (int64_t kb = kb0 + ksub * 16; kb < kb1; kb += 64) {
+    const int64_t k = kb + kl;
+    const bool k_ok = k < kb1;
+    const u32x4 fb = (n_ok && k_ok) ? *reinterpret_cast<const u32x4*>(B + k * 2) : zero;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int64_t m = i * 32 + (lane & 31);
+      const u32x4 fa = (m < P.M && k_ok) ? *reinterpret_cast<const u32x4*>(A + (m * P.lda + k) * 2) : zero;
+      if constexpr (BF16)
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, fa), __builtin_bit_cast(bf168, fb),
+                                                         acc[i], 0, 0, 0);
+      else
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, fa), __builtin_bit_cast(half8, fb),
+                                                        acc[i], 0, 0, 0);
+    }
+  }
+  if (ksub > 0) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) red[ksub - 1][nsub][i][e][lane] = acc[i][e];
+  }
+  __syncthreads();
+  if (ksub > 0 || !n_ok) return;
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][e] += red[q][nsub][i][e][lane];
+  const float bz = P.bias ? P.bias[n] : 0.f;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int64_t m = i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      if (m >= P.M) continue;
+      if (nsplit > 1) {
+        part[(int64_t(split) * P.M + m) * P.N + n] = acc[i][e];
+      } else {
+        float v = epilogue_value(P, acc[i][e], bz);
+        if (P.R) v += P.R[m * P.ldr + n];
+        store_from_f32(P.C, P.out_dtype, m * P.ldc + n, v);
+      }
+    }
+}
+
+__global__ void __launch_bounds__(256) gemm16_skinny_finish_kernel(GemmArgs P, int nsplit, const float* part) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= P.M * P.N) return;
+  const int64_t m = i / P.N, n = i - m * P.N;
+  float v = part[i];
+#pragma unroll 8
+  for (int s = 1; s < nsplit; ++s) v += part[int64_t(s) * P.M * P.N + i];
+  v = epilogue_value(P, v, P.bias ? P.bias[n] : 0.f);
+  if (P.R) v += P.R[m * P.ldr + n];
+  store_from_f32(P.C, P.out_dtype, m * P.ldc + n, v);
+}
+
 }  // namespace
 
 namespace bg {
@@ -1050,6 +1142,37 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const 
                    P.ldb % 8 == 0 && P.sa % 8 == 0 && P.sb % 8 == 0;
   const bool bf = d.in_dtype == BG_BF16;
   Profile prof(ctx, bf ? "gemm_bf16" : "gemm_f16", bytes, flops);
+  // Skinny problems: at most 64 rows, a K of 512+ and fewer 128-column
+  // tiles than CUs (the tiled kernels would leave most of the chip idle).
+  const int64_t ntiles = (d.n + 127) / 128;
+  if (vec && d.batch == 1 && d.m <= 64 && d.k >= 512 && ntiles < 256 && std::getenv("BG_GEMM_SKINNY") == nullptr) {
+    // K slices of at least 256 (and multiples of 64: four wavefronts
+    // interleave 16-deep steps) until about 256 workgroups stream B.
+    int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(256 / ntiles, d.k / 256));
+    int64_t ks = (d.k + nsplit - 1) / nsplit;
+    ks = (ks + 63) / 64 * 64;
+    nsplit = (d.k + ks - 1) / ks;
+    // A fixed (no-allocation) workspace without room for the partials takes
+    // the whole K in each workgroup instead.
+    if (ws.fixed && size_t(nsplit * d.m * d.n) * 4 + 256 > ws.cap - std::min(ws.cap, ws.used)) {
+      nsplit = 1;
+      ks = (d.k + 63) / 64 * 64;
+    }
+    float* part = nsplit > 1 ? static_cast<float*>(ws.get(size_t(nsplit * d.m * d.n) * 4, 3)) : nullptr;
+    const dim3 grid(static_cast<unsigned>(ntiles * nsplit));
+    const int ns = int(nsplit);
+    if (d.m <= 32) {
+      if (bf) bg::dispatch(ctx, gemm16_skinny_kernel<true, 1>, grid, dim3(1024), 0, P, ks, ns, part);
+      else bg::dispatch(ctx, gemm16_skinny_kernel<false, 1>, grid, dim3(1024), 0, P, ks, ns, part);
+    } else {
+      if (bf) bg::dispatch(ctx, gemm16_skinny_kernel<true, 2>, grid, dim3(1024), 0, P, ks, ns, part);
+      else bg::dispatch(ctx, gemm16_skinny_kernel<false, 2>, grid, dim3(1024), 0, P, ks, ns, part);
+    }
+    if (nsplit > 1)
+      bg::dispatch(ctx, gemm16_skinny_finish_kernel, dim3(static_cast<unsigned>((d.m * d.n + 255) / 256)), dim3(256),
+                   0, P, ns, static_cast<const float*>(part));
+    return;
+  }
   // Direct-to-LDS path: operand byte ranges addressable with 32-bit offsets.
   const int64_t a_span = ((d.m - 1) * P.lda + d.k) * es;
   const int64_t b_span = ((d.n - 1) * P.ldb + d.k) * es;

@@ -894,6 +894,57 @@ def test_gemm_128x192_tiles_ragged(bridge, rng, monkeypatch, m, k, n, act, resid
     assert O.within(y, z, TOL16).all(), O.report(y, z, TOL16)
 
 
+@pytest.mark.parametrize("m,k,n,act,residual,trans_b", [
+    (1, 4096, 4096, 0, False, True), (17, 1024, 300, 1, True, True), (32, 4096, 4096, 0, False, False),
+    (33, 768, 2304, 2, False, True), (64, 3072, 768, 0, True, True), (64, 512, 50, 1, False, True),
+    (5, 4104, 130, 2, True, False), (48, 520, 4000, 0, False, True)])
+@pytest.mark.parametrize("dtype,out_dtype", [("float16", "float32"), ("float16", "float16"),
+                                             ("bfloat16", "bfloat16")])
+def test_gemm_skinny_split_k(bridge, rng, monkeypatch, m, k, n, act, residual, trans_b, dtype, out_dtype):
+    """At most 64 rows with K >= 512 and fewer 128-column tiles than CUs:
+    K split over workgroups (f32 partials summed in split order by a second
+    kernel, or one split), M of one or two 32-row MFMA blocks, ragged N,
+    a K that is a multiple of 8 but not 16, every epilogue stage.  Checked
+    against the oracle's autocast linear and against the tiled kernel."""
+    x = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, (n,)).astype(np.float32)
+    if dtype == "float16":
+        x16, w16 = x.astype(np.float16), w.astype(np.float16)
+        hx = up(bridge, x16)
+        wm = w16 if trans_b else np.ascontiguousarray(w16.T)
+        hw = up(bridge, wm)
+        z = O.matmul(x16, np.ascontiguousarray(w16.T)).astype(np.float32)
+    else:
+        x16, w16 = O.f32_to_bf16_bits(x), O.f32_to_bf16_bits(w)
+        hx = up(bridge, x16, "bfloat16")
+        wm = w16 if trans_b else np.ascontiguousarray(w16.T)
+        hw = up(bridge, wm, "bfloat16")
+        z = O.bf16_bits_to_f32(O.matmul_bf16(x16, np.ascontiguousarray(w16.T)))
+    z = z + b
+    if act == 1:
+        z = np.maximum(z, np.float32(0))
+    elif act == 2:
+        z = O.gelu_tanh_f32(z)
+    r = rng.standard_normal((m, n)).astype(np.float32) if residual else None
+    if residual:
+        z = z + r
+    kw = dict(m=m, n=n, k=k, trans_b=trans_b, in_dtype=dtype, out_dtype=out_dtype, bias=up(bridge, b),
+              round_out=True, act=act, residual=up(bridge, r) if residual else None)
+    y = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw))
+    monkeypatch.setenv("BG_GEMM_SKINNY", "0")
+    y2 = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw))
+    if out_dtype == "float32":
+        y, y2 = y.astype(np.float32), y2.astype(np.float32)
+    elif out_dtype == "float16":
+        y, y2, z = y.astype(np.float32), y2.astype(np.float32), z.astype(np.float16).astype(np.float32)
+    else:
+        y, y2, z = (O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(y2),
+                    O.bf16_bits_to_f32(O.f32_to_bf16_bits(z.astype(np.float32))))
+    assert O.within(y, z, TOL16).all(), O.report(y, z, TOL16)
+    assert O.within(y, y2, TOL16).all(), O.report(y, y2, TOL16)
+
+
 @pytest.mark.parametrize("shared_w", [True, False])
 def test_gemm_128x192_tiles_batched(bridge, rng, monkeypatch, shared_w):
     """Batched 128x192 tiles (batch 8, ragged M = 1100, K tail 200): each

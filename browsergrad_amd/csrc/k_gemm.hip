@@ -34,6 +34,7 @@
 
 #include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "common.cuh"
 #include "core.h"
@@ -921,20 +922,27 @@ LdsCfg choose_lds_cfg(int64_t m, int64_t n, int64_t k, int64_t batch, int act) {
   return LdsCfg::T128x128x64s2;
 }
 
-// ---- Skinny 16-bit GEMM (M <= 64): K split over workgroups --------------
+// ---- Skinny GEMMs (M <= 64): K split over workgroups ----------------------
 // A 128-row tile would leave most of its rows and most CUs idle when M is
 // small; the problem is a stream over B.  Workgroup u (16 wavefronts) takes
 // 128 columns of C and the K range of split u % nsplit: wavefront w covers
-// columns 32 (w % 4) .. +31 and every fourth 16-deep step of the range,
-// starting at step w / 4, with one v_mfma_f32_32x32x16 per 32 rows of A,
-// operands loaded straight from global memory (lane l: row or column
-// l % 32, k = 8 (l / 32) .. +7 of the step; B stored [N][K]).  The four
-// K-interleaved wavefronts of a column block are summed through LDS in
-// order 0, 1, 2, 3.  With one split the epilogue runs here; otherwise f32
-// partials go to part[split][M][N] and gemm16_skinny_finish_kernel sums
-// them in split order and runs the epilogue.
-template <bool BF16, int MT>
-__global__ void __launch_bounds__(1024) gemm16_skinny_kernel(GemmArgs P, int64_t ks, int nsplit, float* part) {
+// columns 32 (w % 4) .. +31 and every fourth step of the range, starting at
+// step w / 4.  A step is 16 bytes of k per lane: lane l holds row (A) or
+// column (B) l % 32 and the k-unit l / 32 of the step, so a 16-bit step is
+// one v_mfma_f32_32x32x16 (k = 8 (l / 32) .. +7) and an f32 step (8 deep)
+// four v_mfma_f32_32x32x2f32, MFMA t taking k = 4 (l / 32) + t on both
+// operands.  Operands come straight from global memory (A is a few KB and
+// stays in cache; B streams once): 16-byte loads, or for f32 B stored
+// [K][N] (TB false) four 4-byte loads that are coalesced along N.  The
+// four K-interleaved wavefronts of a column block are summed through LDS
+// in order 0, 1, 2, 3.  With one split the epilogue runs here; otherwise f32
+// partials go to part[split][M][N] and gemm_skinny_finish_kernel sums them
+// in split order and runs the epilogue.
+template <int DT, int MT, bool TB>
+__global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs P, int64_t ks, int nsplit, float* part) {
+  constexpr int ES = DT == BG_F32 ? 4 : 2;
+  constexpr int KSTEP = 32 / ES;  // k per step
+  constexpr int KU = 16 / ES;     // k per lane per step
   __shared__ float red[3][4][MT][16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nsub = wave & 3, ksub = wave >> 2;
@@ -944,31 +952,74 @@ __global__ void __launch_bounds__(1024) gemm16_skinny_kernel(GemmArgs P, int64_t
   const bool n_ok = n < P.N;
   const int64_t kb0 = int64_t(split) * ks;
   const int64_t kb1 = kb0 + ks < P.K ? kb0 + ks : P.K;
-  const int kl = 8 * (lane >> 5);
+  const int kl = KU * (lane >> 5);
   const char* A = static_cast<const char*>(P.A);
-  const char* B = static_cast<const char*>(P.B) + (n_ok ? n : 0) * P.ldb * 2;
+  const char* B = static_cast<const char*>(P.B);
   float16v acc[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll 4
-  for (int64_t kb = kb0 + ksub * 16; kb < kb1; kb += 64) {
+  // Operand vectors: f32 as float 4-vectors (the wide-K kernel's form),
+  // 16-bit as raw 16-byte words.
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  using V = typename std::conditional<DT == BG_F32, f4, u32x4>::type;
+  struct Frag {
+    V b;
+    V a[MT];
+  };
+  auto load_step = [&](int64_t kb, Frag& f) {
     const int64_t k = kb + kl;
     const bool k_ok = k < kb1;
-    const u32x4 fb = (n_ok && k_ok) ? *reinterpret_cast<const u32x4*>(B + k * 2) : zero;
+    f.b = V{};
+    if (n_ok && k_ok) {
+      if constexpr (DT == BG_F32 && !TB) {
+        const float* bp = reinterpret_cast<const float*>(B) + k * P.ldb + n;
+        f.b = f4{bp[0], bp[P.ldb], bp[2 * P.ldb], bp[3 * P.ldb]};
+      } else {
+        f.b = *reinterpret_cast<const V*>(B + (n * P.ldb + k) * ES);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
       const int64_t m = i * 32 + (lane & 31);
-      const u32x4 fa = (m < P.M && k_ok) ? *reinterpret_cast<const u32x4*>(A + (m * P.lda + k) * 2) : zero;
-      if constexpr (BF16)
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, fa), __builtin_bit_cast(bf168, fb),
-                                                         acc[i], 0, 0, 0);
-      else
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, fa), __builtin_bit_cast(half8, fb),
-                                                        acc[i], 0, 0, 0);
+      f.a[i] = (m < P.M && k_ok) ? *reinterpret_cast<const V*>(A + (m * P.lda + k) * ES) : V{};
     }
+  };
+  auto mma_step = [&](const Frag& f) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      if constexpr (DT == BG_F32) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[i][t], f.b[t], acc[i], 0, 0, 0);
+      } else if constexpr (DT == BG_BF16) {
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, f.a[i]),
+                                                         __builtin_bit_cast(bf168, f.b), acc[i], 0, 0, 0);
+      } else {
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, f.a[i]),
+                                                        __builtin_bit_cast(half8, f.b), acc[i], 0, 0, 0);
+      }
+    }
+  };
+  // This wavefront's steps: kb0 + KSTEP (ksub + 4 j) < kb1.  f32 issues the
+  // loads of D steps before their MFMAs (4 with one row block, 2 with two,
+  // which stays within 128 VGPRs); 16-bit steps go one at a time (batching
+  // them measured slower: 32 x 4096 x 4096 f16 11.4 -> 13.1 us).
+  constexpr int D = DT == BG_F32 ? (MT == 1 ? 4 : 2) : 1;
+  const int64_t first = kb0 + ksub * KSTEP;
+  const int nst = first < kb1 ? int((kb1 - first + 4 * KSTEP - 1) / (4 * KSTEP)) : 0;
+  int st = 0;
+  for (; st + D <= nst; st += D) {
+    Frag f[D];
+#pragma unroll
+    for (int q = 0; q < D; ++q) load_step(first + int64_t(st + q) * 4 * KSTEP, f[q]);
+#pragma unroll
+    for (int q = 0; q < D; ++q) mma_step(f[q]);
+  }
+  for (; st < nst; ++st) {
+    Frag f;
+    load_step(first + int64_t(st) * 4 * KSTEP, f);
+    mma_step(f);
   }
   if (ksub > 0) {
 #pragma unroll
@@ -1001,7 +1052,7 @@ __global__ void __launch_bounds__(1024) gemm16_skinny_kernel(GemmArgs P, int64_t
     }
 }
 
-__global__ void __launch_bounds__(256) gemm16_skinny_finish_kernel(GemmArgs P, int nsplit, const float* part) {
+__global__ void __launch_bounds__(256) gemm_skinny_finish_kernel(GemmArgs P, int nsplit, const float* part) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= P.M * P.N) return;
   const int64_t m = i / P.N, n = i - m * P.N;
@@ -1062,6 +1113,66 @@ static bool gelu_in_epilogue(const bg_matmul_desc& d, const char* a, const char*
 
 // a / b point at the operands' storage (d.offset_a / d.offset_b are applied
 // here); bias is f32 [N] or NULL.
+// Skinny GEMMs: at most 64 rows, a K of 512+, fewer 128-column tiles than
+// CUs and one batch (the tiled kernels would leave most of the chip idle).
+// K slices of at least 256 (and multiples of 64: four wavefronts interleave
+// the steps) until about 256 workgroups stream B; a workspace with less
+// than `room` bytes free for the partials takes one slice.
+struct SkinnyPlan {
+  bool on = false;
+  int64_t ntiles = 0, nsplit = 1, ks = 0;
+};
+
+static SkinnyPlan skinny_plan(const bg_matmul_desc& d, size_t room) {
+  SkinnyPlan sp;
+  sp.ntiles = (d.n + 127) / 128;
+  if (d.batch != 1 || d.m > 64 || d.k < 512 || sp.ntiles >= 256 || std::getenv("BG_GEMM_SKINNY") != nullptr)
+    return sp;
+  sp.on = true;
+  int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(256 / sp.ntiles, d.k / 256));
+  int64_t ks = (d.k + nsplit - 1) / nsplit;
+  ks = (ks + 63) / 64 * 64;
+  nsplit = (d.k + ks - 1) / ks;
+  if (nsplit > 1 && size_t(nsplit * d.m * d.n) * 4 + 256 > room) {
+    nsplit = 1;
+    ks = (d.k + 63) / 64 * 64;
+  }
+  sp.nsplit = nsplit;
+  sp.ks = ks;
+  return sp;
+}
+
+// Operands must allow 16-byte loads along K (the caller checks); tb: B is
+// [N][K].  Returns false when the problem is not skinny.
+static bool launch_skinny(bg_ctx* ctx, const bg_matmul_desc& d, GemmArgs& P, GemmWorkspace& ws, int dt, bool tb) {
+  const SkinnyPlan sp = skinny_plan(d, ws.fixed ? ws.cap - std::min(ws.cap, ws.used) : SIZE_MAX);
+  if (!sp.on) return false;
+  const int64_t ntiles = sp.ntiles, nsplit = sp.nsplit, ks = sp.ks;
+  float* part = nsplit > 1 ? static_cast<float*>(ws.get(size_t(nsplit * d.m * d.n) * 4, 3)) : nullptr;
+  const dim3 grid(static_cast<unsigned>(ntiles * nsplit));
+  const int ns = int(nsplit);
+  auto go = [&](auto dtc, auto mtc, auto tbc) {
+    bg::dispatch(ctx, gemm_skinny_kernel<decltype(dtc)::value, decltype(mtc)::value, decltype(tbc)::value>, grid,
+                 dim3(1024), 0, P, ks, ns, part);
+  };
+  auto by_tb = [&](auto dtc, auto mtc) {
+    if (tb) go(dtc, mtc, std::true_type{});
+    else if constexpr (decltype(dtc)::value == BG_F32) go(dtc, mtc, std::false_type{});
+    else fail(BG_E_UNSUPPORTED, "skinny GEMM: 16-bit B must be [N][K]");
+  };
+  auto by_mt = [&](auto dtc) {
+    if (d.m <= 32) by_tb(dtc, std::integral_constant<int, 1>{});
+    else by_tb(dtc, std::integral_constant<int, 2>{});
+  };
+  if (dt == BG_F32) by_mt(std::integral_constant<int, BG_F32>{});
+  else if (dt == BG_F16) by_mt(std::integral_constant<int, BG_F16>{});
+  else by_mt(std::integral_constant<int, BG_BF16>{});
+  if (nsplit > 1)
+    bg::dispatch(ctx, gemm_skinny_finish_kernel, dim3(static_cast<unsigned>((d.m * d.n + 255) / 256)), dim3(256), 0,
+                 P, ns, static_cast<const float*>(part));
+  return true;
+}
+
 static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const char* b, const float* bias,
                      void* c, int64_t ldc, int64_t stride_c, int out_dtype, int act, GemmWorkspace& ws,
                      const float* residual = nullptr) {
@@ -1114,6 +1225,9 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const 
 #undef BG_WIDE
       return;
     }
+    if (aligned && d.k % 4 == 0 && P.lda % 4 == 0 && P.ldb % 4 == 0) {
+      if (launch_skinny(ctx, d, P, ws, BG_F32, d.trans_b != 0)) return;
+    }
     launch32<128, 128>(ctx, P, d.batch, d.trans_b != 0, aligned);
     return;
   }
@@ -1142,37 +1256,7 @@ static void run_gemm(bg_ctx* ctx, const bg_matmul_desc& d, const char* a, const 
                    P.ldb % 8 == 0 && P.sa % 8 == 0 && P.sb % 8 == 0;
   const bool bf = d.in_dtype == BG_BF16;
   Profile prof(ctx, bf ? "gemm_bf16" : "gemm_f16", bytes, flops);
-  // Skinny problems: at most 64 rows, a K of 512+ and fewer 128-column
-  // tiles than CUs (the tiled kernels would leave most of the chip idle).
-  const int64_t ntiles = (d.n + 127) / 128;
-  if (vec && d.batch == 1 && d.m <= 64 && d.k >= 512 && ntiles < 256 && std::getenv("BG_GEMM_SKINNY") == nullptr) {
-    // K slices of at least 256 (and multiples of 64: four wavefronts
-    // interleave 16-deep steps) until about 256 workgroups stream B.
-    int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(256 / ntiles, d.k / 256));
-    int64_t ks = (d.k + nsplit - 1) / nsplit;
-    ks = (ks + 63) / 64 * 64;
-    nsplit = (d.k + ks - 1) / ks;
-    // A fixed (no-allocation) workspace without room for the partials takes
-    // the whole K in each workgroup instead.
-    if (ws.fixed && size_t(nsplit * d.m * d.n) * 4 + 256 > ws.cap - std::min(ws.cap, ws.used)) {
-      nsplit = 1;
-      ks = (d.k + 63) / 64 * 64;
-    }
-    float* part = nsplit > 1 ? static_cast<float*>(ws.get(size_t(nsplit * d.m * d.n) * 4, 3)) : nullptr;
-    const dim3 grid(static_cast<unsigned>(ntiles * nsplit));
-    const int ns = int(nsplit);
-    if (d.m <= 32) {
-      if (bf) bg::dispatch(ctx, gemm16_skinny_kernel<true, 1>, grid, dim3(1024), 0, P, ks, ns, part);
-      else bg::dispatch(ctx, gemm16_skinny_kernel<false, 1>, grid, dim3(1024), 0, P, ks, ns, part);
-    } else {
-      if (bf) bg::dispatch(ctx, gemm16_skinny_kernel<true, 2>, grid, dim3(1024), 0, P, ks, ns, part);
-      else bg::dispatch(ctx, gemm16_skinny_kernel<false, 2>, grid, dim3(1024), 0, P, ks, ns, part);
-    }
-    if (nsplit > 1)
-      bg::dispatch(ctx, gemm16_skinny_finish_kernel, dim3(static_cast<unsigned>((d.m * d.n + 255) / 256)), dim3(256),
-                   0, P, ns, static_cast<const float*>(part));
-    return;
-  }
+  if (vec && launch_skinny(ctx, d, P, ws, d.in_dtype, true)) return;
   // Direct-to-LDS path: operand byte ranges addressable with 32-bit offsets.
   const int64_t a_span = ((d.m - 1) * P.lda + d.k) * es;
   const int64_t b_span = ((d.n - 1) * P.ldb + d.k) * es;
@@ -1328,6 +1412,32 @@ void plan_matmul(const bg_matmul_desc& d0, bg_launch_plan& out) {
     e.targs[2] = g.aligned ? 1 : 0;
     e.grid[0] = int64_t(g.tiles_m) * g.tiles_n; e.grid[1] = 1; e.grid[2] = 1;
     e.block[0] = kWideWaves * 64; e.block[1] = 1; e.block[2] = 1;
+    return;
+  }
+  const SkinnyPlan sp = g.aligned ? skinny_plan(d, SIZE_MAX) : SkinnyPlan{};
+  if (sp.on) {
+    const int mt = d.m <= 32 ? 1 : 2;
+    out.tile_m = 32 * mt;
+    out.tile_n = 128;
+    out.tile_k = 8;
+    out.k_slices = int32_t(sp.nsplit);
+    out.lds_bytes = int64_t(3) * 4 * mt * 16 * 64 * 4;
+    out.workspace_bytes = sp.nsplit > 1 ? sp.nsplit * d.m * d.n * 4 : 0;
+    std::snprintf(e.family, sizeof e.family, "%s", "gemm_skinny_kernel");
+    e.n_targs = 3;
+    e.targs[0] = BG_F32;
+    e.targs[1] = mt;
+    e.targs[2] = d.trans_b ? 1 : 0;
+    e.grid[0] = sp.ntiles * sp.nsplit; e.grid[1] = 1; e.grid[2] = 1;
+    e.block[0] = 1024; e.block[1] = 1; e.block[2] = 1;
+    if (sp.nsplit > 1) {
+      out.n_launches = 2;
+      bg_launch_plan_entry& f = out.launch[1];
+      std::snprintf(f.family, sizeof f.family, "%s", "gemm_skinny_finish_kernel");
+      f.n_targs = 0;
+      f.grid[0] = (d.m * d.n + 255) / 256; f.grid[1] = 1; f.grid[2] = 1;
+      f.block[0] = 256; f.block[1] = 1; f.block[2] = 1;
+    }
     return;
   }
   out.tile_m = 128;

@@ -244,7 +244,8 @@ _TARG = re.compile(r"L([a-z])(n?)(\d+)E")
 def parse_kernel_symbol(name: str, family: str) -> Optional[List[int]]:
     """Template arguments of `family` in a launch-log kernel name, mangled
     (..15fa32_fwd_kernelILi64ELb1EEEv...) or demangled
-    (fa32_fwd_kernel<64, true>(...)); None when the name is another kernel."""
+    (fa32_fwd_kernel<64, true>(...)); [] for a kernel without template
+    arguments; None when the name is another kernel."""
     m = re.search(re.escape(family) + r"I((?:L[a-z]n?\d+E)+)E", name)
     if m:
         return [(-1 if neg else 1) * int(v) for _, neg, v in _TARG.findall(m.group(1))]
@@ -255,6 +256,11 @@ def parse_kernel_symbol(name: str, family: str) -> Optional[List[int]]:
             tok = tok.strip()
             vals.append(1 if tok == "true" else 0 if tok == "false" else int(tok))
         return vals
+    # A kernel without template arguments: mangled ..25name + E (end of the
+    # nested name), or demangled name(...).
+    if re.search(r"\d" + re.escape(family) + r"E", name) or re.search(
+            r"(?:^|[^A-Za-z0-9_])" + re.escape(family) + r"\(", name):
+        return []
     return None
 
 
@@ -389,19 +395,31 @@ def prepare_semantic_gemm(m: int, n: int, k: int, *, max_transient_working_set_b
     bm, bn, bk = plan["tile"]
     tiles_m, tiles_n = -(-m // bm), -(-n // bn)
     wide = main["family"] == "gemm32_wide_k_kernel"
-    if main["grid"][0] != tiles_m * tiles_n or not (tiles_m * bm >= m > (tiles_m - 1) * bm
-                                                      and tiles_n * bn >= n > (tiles_n - 1) * bn):
+    skinny = main["family"] == "gemm_skinny_kernel"
+    slices = plan["kSlices"]
+    # The skinny kernel runs each column tile once per K slice.
+    per_tile = slices if skinny else 1
+    if main["grid"][0] != tiles_m * tiles_n * per_tile or not (tiles_m * bm >= m > (tiles_m - 1) * bm
+                                                                 and tiles_n * bn >= n > (tiles_n - 1) * bn):
         _fail(code, "$.tile", f"{main['grid'][0]} workgroups do not cover {m} x {n} once with {bm} x {bn} tiles")
-    # Workgroup -> tile: the wide-K kernel walks tiles row-major; the others
-    # use the XCD-aware order restated by gemm_tile_order.
-    order = (lambda p: (p // tiles_n, p % tiles_n)) if wide else (lambda p: gemm_tile_order(p, tiles_m, tiles_n))
+    # Workgroup -> tile: the wide-K kernel walks tiles row-major, the skinny
+    # one (a single tile row) takes tile p // kSlices and K slice p % kSlices;
+    # the others use the XCD-aware order restated by gemm_tile_order.
+    if wide:
+        order = lambda p: (p // tiles_n, p % tiles_n)  # noqa: E731
+    elif skinny:
+        order = lambda p: (0, p)  # noqa: E731
+    else:
+        order = lambda p: gemm_tile_order(p, tiles_m, tiles_n)  # noqa: E731
     seen = {order(p) for p in range(tiles_m * tiles_n)}
     if len(seen) != tiles_m * tiles_n or not all(0 <= a < tiles_m and 0 <= b < tiles_n for a, b in seen):
         _fail(code, "$.schedule.tileOrder", "workgroup -> tile order is not a bijection onto the tile grid")
-    slices = plan["kSlices"]
     if wide and (slices != main["block"][0] // 64 or len(plan["launches"]) != 1 or plan["workspaceBytes"] != 0):
         _fail(code, "$.tile.kSlices", f"{slices} in-workgroup K slices need one wavefront each and one launch")
-    if not wide and (slices != 1 or len(plan["launches"]) != 1):
+    if skinny and (tiles_m != 1 or len(plan["launches"]) != (2 if slices > 1 else 1)
+                   or plan["workspaceBytes"] != (4 * slices * m * n if slices > 1 else 0)):
+        _fail(code, "$.tile.kSlices", f"{slices} K slices need one f32 partial each and a summing launch")
+    if not wide and not skinny and (slices != 1 or len(plan["launches"]) != 1):
         _fail(code, "$.tile.kSlices", "the tiled kernel runs the whole K range in one launch")
     layout = layout_artifact({"lhs": {"shape": [m, k], "dtype": "float32"},
                               "rhs": {"shape": [k, n], "dtype": "float32"},
@@ -411,11 +429,15 @@ def prepare_semantic_gemm(m: int, n: int, k: int, *, max_transient_working_set_b
         "kSlices": slices,
         "accumulation": ("f32; each of the workgroup's wavefronts sums a contiguous run of 8-wide k chunks in "
                          "ascending order; the partials are added in wavefront order through LDS")
-                        if wide else "f32; ascending k",
+                        if wide else
+                        ("f32; per K slice, four wavefronts sum every fourth 8-deep k step in ascending order and "
+                         "are added in wavefront order through LDS; the slices' partials are added in slice order")
+                        if skinny else "f32; ascending k",
     }, ["tiles-cover-output-once", "k-slices-one-per-wavefront"])
     schedule = _artifact("schedule", {
         "launches": plan["launches"], "ldsBytes": plan["ldsBytes"], "workspaceBytes": plan["workspaceBytes"],
-        "tileOrder": "row-major" if wide else "xcd-round-robin-consecutive, groups of 4 tile rows",
+        "tileOrder": "row-major" if wide else "column tile p // kSlices, K slice p % kSlices" if skinny
+                     else "xcd-round-robin-consecutive, groups of 4 tile rows",
     }, ["tile-order-bijection", "within-workgroup-limits"])
     gpu = 4 * (m * k + k * n + m * n) + plan["workspaceBytes"]
     host = 4 * (m * k + k * n) + 2 * 4 * m * n  # certified input copies, readback, returned bytes

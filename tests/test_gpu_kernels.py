@@ -899,17 +899,21 @@ def test_gemm_128x192_tiles_ragged(bridge, rng, monkeypatch, m, k, n, act, resid
     (33, 768, 2304, 2, False, True), (64, 3072, 768, 0, True, True), (64, 512, 50, 1, False, True),
     (5, 4104, 130, 2, True, False), (48, 520, 4000, 0, False, True)])
 @pytest.mark.parametrize("dtype,out_dtype", [("float16", "float32"), ("float16", "float16"),
-                                             ("bfloat16", "bfloat16")])
+                                             ("bfloat16", "bfloat16"), ("float32", "float32")])
 def test_gemm_skinny_split_k(bridge, rng, monkeypatch, m, k, n, act, residual, trans_b, dtype, out_dtype):
-    """At most 64 rows with K >= 512 and fewer 128-column tiles than CUs:
-    K split over workgroups (f32 partials summed in split order by a second
+    """At most 64 rows with K >= 512 and fewer 128-column tiles than CUs
+    (f32 also with B stored [K][N]): K split over workgroups (f32 partials summed in split order by a second
     kernel, or one split), M of one or two 32-row MFMA blocks, ragged N,
     a K that is a multiple of 8 but not 16, every epilogue stage.  Checked
     against the oracle's autocast linear and against the tiled kernel."""
     x = rng.uniform(-1, 1, (m, k)).astype(np.float32)
     w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
     b = rng.uniform(-0.1, 0.1, (n,)).astype(np.float32)
-    if dtype == "float16":
+    if dtype == "float32":
+        hx = up(bridge, x)
+        hw = up(bridge, w if trans_b else np.ascontiguousarray(w.T))
+        z = (x.astype(np.float64) @ w.T.astype(np.float64)).astype(np.float32)
+    elif dtype == "float16":
         x16, w16 = x.astype(np.float16), w.astype(np.float16)
         hx = up(bridge, x16)
         wm = w16 if trans_b else np.ascontiguousarray(w16.T)
@@ -930,7 +934,7 @@ def test_gemm_skinny_split_k(bridge, rng, monkeypatch, m, k, n, act, residual, t
     if residual:
         z = z + r
     kw = dict(m=m, n=n, k=k, trans_b=trans_b, in_dtype=dtype, out_dtype=out_dtype, bias=up(bridge, b),
-              round_out=True, act=act, residual=up(bridge, r) if residual else None)
+              round_out=dtype != "float32", act=act, residual=up(bridge, r) if residual else None)
     y = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw))
     monkeypatch.setenv("BG_GEMM_SKINNY", "0")
     y2 = bridge.to_numpy(bridge.matmul_ex(hx, hw, **kw))
@@ -941,8 +945,9 @@ def test_gemm_skinny_split_k(bridge, rng, monkeypatch, m, k, n, act, residual, t
     else:
         y, y2, z = (O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(y2),
                     O.bf16_bits_to_f32(O.f32_to_bf16_bits(z.astype(np.float32))))
-    assert O.within(y, z, TOL16).all(), O.report(y, z, TOL16)
-    assert O.within(y, y2, TOL16).all(), O.report(y, y2, TOL16)
+    tol = TOL32 if dtype == "float32" else TOL16
+    assert O.within(y, z, tol).all(), O.report(y, z, tol)
+    assert O.within(y, y2, tol).all(), O.report(y, y2, tol)
 
 
 @pytest.mark.parametrize("shared_w", [True, False])

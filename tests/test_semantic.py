@@ -57,7 +57,7 @@ def test_certificate_commits_to_the_bytes():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m,n,k,hi", [(3, 5, 7, 9), (256, 384, 512, 15), (1000, 999, 1024, 3)])
+@pytest.mark.parametrize("m,n,k,hi", [(3, 5, 7, 9), (256, 384, 512, 15), (1000, 999, 1024, 3), (40, 3000, 4096, 2)])
 def test_exact_gemm_is_bit_exact(bridge, m, n, k, hi):
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(0, hi + 1, (m, k)).astype(F32)
@@ -70,7 +70,8 @@ def test_exact_gemm_is_bit_exact(bridge, m, n, k, hi):
     # verified artifacts from the launches that ran, with their hashes
     arts = t["artifacts"]
     assert arts["layout"]["body"]["tensors"]["lhs"]["strides"] == [k, 1]
-    assert arts["schedule"]["body"]["launches"][0]["family"] in ("gemm32_kernel", "gemm32_wide_k_kernel")
+    assert arts["schedule"]["body"]["launches"][0]["family"] in ("gemm32_kernel", "gemm32_wide_k_kernel",
+                                                                  "gemm_skinny_kernel")
     for name, key in (("layout", "layoutSemanticHash"), ("tile", "kernelSemanticHash"),
                       ("schedule", "scheduleSemanticHash")):
         assert t[key] == arts[name]["hash"] == canonical_hash(arts[name]["body"])
@@ -160,6 +161,15 @@ def test_prepare_gemm_fixes_schedule_before_any_launch():
     assert s.tile["body"]["kSlices"] == 16 and "wavefront order" in s.tile["body"]["accumulation"]
     assert s.schedule["body"]["tileOrder"] == "row-major"
     assert s.plannedTransientGpuBytes == 4 * (64 * 784 + 784 * 128 + 64 * 128)
+    # 40 x 3000 x 4096: 24 column tiles of one 64-row block, K in 10 slices
+    # of 448, the slices' partials summed by a second launch.
+    k = prepare_semantic_gemm(40, 3000, 4096)
+    assert k.plan["launches"] == [{"family": "gemm_skinny_kernel", "templateArgs": [0, 2, 0],
+                                   "grid": [240, 1, 1], "block": [1024, 1, 1]},
+                                  {"family": "gemm_skinny_finish_kernel", "templateArgs": [],
+                                   "grid": [469, 1, 1], "block": [256, 1, 1]}]
+    assert k.tile["body"]["kSlices"] == 10 and k.plan["workspaceBytes"] == 4 * 10 * 40 * 3000
+    assert k.schedule["body"]["tileOrder"] == "column tile p // kSlices, K slice p % kSlices"
 
 
 @pytest.mark.parametrize("kw,path", [
@@ -251,6 +261,18 @@ def test_prepare_attention():
 ])
 def test_parse_kernel_symbol(name, args):
     assert parse_kernel_symbol(name, "gemm32_kernel") == args
+
+
+def test_parse_kernel_symbol_without_template_arguments():
+    fin = "_ZN12_GLOBAL__N_125gemm_skinny_finish_kernelENS_8GemmArgsEiPKf"
+    assert parse_kernel_symbol(fin, "gemm_skinny_finish_kernel") == []
+    assert parse_kernel_symbol("(anonymous namespace)::gemm_skinny_finish_kernel((anonymous namespace)::GemmArgs, "
+                               "int, float const*)", "gemm_skinny_finish_kernel") == []
+    # neither the finishing kernel's name nor a longer one matches the main kernel's family
+    assert parse_kernel_symbol(fin, "gemm_skinny_kernel") is None
+    assert parse_kernel_symbol("_ZN12_GLOBAL__N_118gemm_skinny_kernelILi0ELi2ELb0EEEvNS_8GemmArgsEliPf",
+                               "gemm_skinny_kernel") == [0, 2, 0]
+    assert parse_kernel_symbol("_ZN12_GLOBAL__N_121xgemm_skinny_kernelENS_8GemmArgsE", "gemm_skinny_kernel") is None
 
 
 def test_launch_log_must_match_the_prepared_schedule():

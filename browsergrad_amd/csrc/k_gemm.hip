@@ -948,6 +948,7 @@ __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs P, int64_t k
   const int nsub = wave & 3, ksub = wave >> 2;
   const int split = int(blockIdx.x % unsigned(nsplit));
   const int64_t n0 = int64_t(blockIdx.x / unsigned(nsplit)) * 128 + nsub * 32;
+  const int64_t mb = int64_t(blockIdx.y) * 32 * MT;  // first row of this row block
   const int64_t n = n0 + (lane & 31);
   const bool n_ok = n < P.N;
   const int64_t kb0 = int64_t(split) * ks;
@@ -982,7 +983,7 @@ __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs P, int64_t k
     }
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-      const int64_t m = i * 32 + (lane & 31);
+      const int64_t m = mb + i * 32 + (lane & 31);
       f.a[i] = (m < P.M && k_ok) ? *reinterpret_cast<const V*>(A + (m * P.lda + k) * ES) : V{};
     }
   };
@@ -1040,7 +1041,7 @@ __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs P, int64_t k
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int64_t m = i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      const int64_t m = mb + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
       if (m >= P.M) continue;
       if (nsplit > 1) {
         part[(int64_t(split) * P.M + m) * P.N + n] = acc[i][e];
@@ -1113,7 +1114,7 @@ static bool gelu_in_epilogue(const bg_matmul_desc& d, const char* a, const char*
 
 // a / b point at the operands' storage (d.offset_a / d.offset_b are applied
 // here); bias is f32 [N] or NULL.
-// Skinny GEMMs: at most 128 rows for f32 (blocks of 64) or 64 for 16-bit,
+// Skinny GEMMs: at most 256 rows for f32 (blocks of 64) or 64 for 16-bit,
 // a K of 512+, fewer 128-column tiles than CUs and one batch (the tiled
 // kernels would leave most of the chip idle).
 // K slices of at least 256 (and multiples of 64: four wavefronts interleave
@@ -1121,24 +1122,25 @@ static bool gelu_in_epilogue(const bg_matmul_desc& d, const char* a, const char*
 // than `room` bytes free for the partials takes one slice.
 struct SkinnyPlan {
   bool on = false;
-  int64_t ntiles = 0, nsplit = 1, ks = 0;
+  int64_t ntiles = 0, rblocks = 1, nsplit = 1, ks = 0;
 };
 
 static SkinnyPlan skinny_plan(const bg_matmul_desc& d, int dt, size_t room) {
   SkinnyPlan sp;
   sp.ntiles = (d.n + 127) / 128;
-  // Row limit: 128 for f32 (two 64-row blocks beat the tiled f32 kernel
-  // 5x at 128 x 4096 x 4096), 64 for 16-bit (two blocks measured slower
-  // than the tiled kernel: 50 against 40 us).
-  if (d.batch != 1 || d.m > (dt == BG_F32 ? 128 : 64) || d.k < 512 || sp.ntiles >= 256 ||
+  // Row limit: 256 for f32 (64-row blocks; two of them beat the tiled f32
+  // kernel 5x at 128 x 4096 x 4096), 64 for 16-bit (two blocks measured
+  // slower than the tiled kernel: 50 against 40 us).
+  if (d.batch != 1 || d.m > (dt == BG_F32 ? 256 : 64) || d.k < 512 || sp.ntiles >= 256 ||
       std::getenv("BG_GEMM_SKINNY") != nullptr)
     return sp;
   sp.on = true;
-  int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(256 / sp.ntiles, d.k / 256));
+  sp.rblocks = (d.m + 63) / 64;
+  int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(256 / (sp.ntiles * sp.rblocks), d.k / 256));
   int64_t ks = (d.k + nsplit - 1) / nsplit;
   ks = (ks + 63) / 64 * 64;
   nsplit = (d.k + ks - 1) / ks;
-  if (nsplit > 1 && size_t(nsplit * std::min<int64_t>(d.m, 64) * d.n) * 4 + 256 > room) {
+  if (nsplit > 1 && size_t(nsplit * d.m * d.n) * 4 + 256 > room) {
     nsplit = 1;
     ks = (d.k + 63) / 64 * 64;
   }
@@ -1152,42 +1154,30 @@ static SkinnyPlan skinny_plan(const bg_matmul_desc& d, int dt, size_t room) {
 static bool launch_skinny(bg_ctx* ctx, const bg_matmul_desc& d, GemmArgs& P, GemmWorkspace& ws, int dt, bool tb) {
   const SkinnyPlan sp = skinny_plan(d, dt, ws.fixed ? ws.cap - std::min(ws.cap, ws.used) : SIZE_MAX);
   if (!sp.on) return false;
-  const int64_t ntiles = sp.ntiles, nsplit = sp.nsplit, ks = sp.ks;
-  const int64_t rows0 = std::min<int64_t>(d.m, 64);
-  float* part = nsplit > 1 ? static_cast<float*>(ws.get(size_t(nsplit * rows0 * d.n) * 4, 3)) : nullptr;
-  const dim3 grid(static_cast<unsigned>(ntiles * nsplit));
+  const int64_t nsplit = sp.nsplit, ks = sp.ks;
+  float* part = nsplit > 1 ? static_cast<float*>(ws.get(size_t(nsplit * d.m * d.n) * 4, 3)) : nullptr;
+  // Row blocks of 64 (32 when M <= 32) along grid y.
+  const dim3 grid(static_cast<unsigned>(sp.ntiles * nsplit), static_cast<unsigned>(sp.rblocks));
   const int ns = int(nsplit);
-  const int64_t es = dt == BG_F32 ? 4 : 2;
-  const int64_t oes = P.out_dtype == BG_F32 ? 4 : 2;
-  // 65-128 rows: one pair of launches per 64-row block (the second block's
-  // operands and outputs offset by 64 rows; the partials buffer is reused
-  // in stream order).
-  for (int64_t r0 = 0; r0 < d.m; r0 += 64) {
-    GemmArgs Q = P;
-    Q.M = std::min<int64_t>(64, d.m - r0);
-    Q.A = static_cast<const char*>(P.A) + r0 * P.lda * es;
-    Q.C = static_cast<char*>(P.C) + r0 * P.ldc * oes;
-    if (P.R) Q.R = P.R + r0 * P.ldr;
-    auto go = [&](auto dtc, auto mtc, auto tbc) {
-      bg::dispatch(ctx, gemm_skinny_kernel<decltype(dtc)::value, decltype(mtc)::value, decltype(tbc)::value>,
-                   grid, dim3(1024), 0, Q, ks, ns, part);
-    };
-    auto by_tb = [&](auto dtc, auto mtc) {
-      if (tb) go(dtc, mtc, std::true_type{});
-      else if constexpr (decltype(dtc)::value == BG_F32) go(dtc, mtc, std::false_type{});
-      else fail(BG_E_UNSUPPORTED, "skinny GEMM: 16-bit B must be [N][K]");
-    };
-    auto by_mt = [&](auto dtc) {
-      if (Q.M <= 32) by_tb(dtc, std::integral_constant<int, 1>{});
-      else by_tb(dtc, std::integral_constant<int, 2>{});
-    };
-    if (dt == BG_F32) by_mt(std::integral_constant<int, BG_F32>{});
-    else if (dt == BG_F16) by_mt(std::integral_constant<int, BG_F16>{});
-    else by_mt(std::integral_constant<int, BG_BF16>{});
-    if (nsplit > 1)
-      bg::dispatch(ctx, gemm_skinny_finish_kernel, dim3(static_cast<unsigned>((Q.M * d.n + 255) / 256)), dim3(256),
-                   0, Q, ns, static_cast<const float*>(part));
-  }
+  auto go = [&](auto dtc, auto mtc, auto tbc) {
+    bg::dispatch(ctx, gemm_skinny_kernel<decltype(dtc)::value, decltype(mtc)::value, decltype(tbc)::value>, grid,
+                 dim3(1024), 0, P, ks, ns, part);
+  };
+  auto by_tb = [&](auto dtc, auto mtc) {
+    if (tb) go(dtc, mtc, std::true_type{});
+    else if constexpr (decltype(dtc)::value == BG_F32) go(dtc, mtc, std::false_type{});
+    else fail(BG_E_UNSUPPORTED, "skinny GEMM: 16-bit B must be [N][K]");
+  };
+  auto by_mt = [&](auto dtc) {
+    if (d.m <= 32) by_tb(dtc, std::integral_constant<int, 1>{});
+    else by_tb(dtc, std::integral_constant<int, 2>{});
+  };
+  if (dt == BG_F32) by_mt(std::integral_constant<int, BG_F32>{});
+  else if (dt == BG_F16) by_mt(std::integral_constant<int, BG_F16>{});
+  else by_mt(std::integral_constant<int, BG_BF16>{});
+  if (nsplit > 1)
+    bg::dispatch(ctx, gemm_skinny_finish_kernel, dim3(static_cast<unsigned>((d.m * d.n + 255) / 256)), dim3(256), 0,
+                 P, ns, static_cast<const float*>(part));
   return true;
 }
 
@@ -1434,32 +1424,27 @@ void plan_matmul(const bg_matmul_desc& d0, bg_launch_plan& out) {
   }
   const SkinnyPlan sp = g.aligned ? skinny_plan(d, BG_F32, SIZE_MAX) : SkinnyPlan{};
   if (sp.on) {
-    // One kernel (+ the partial sum when K is split) per 64-row block.
-    const int64_t rows0 = std::min<int64_t>(d.m, 64);
-    out.tile_m = d.m > 64 ? 64 : 32 * (d.m <= 32 ? 1 : 2);
+    const int mt = d.m <= 32 ? 1 : 2;
+    out.tile_m = 32 * mt;
     out.tile_n = 128;
     out.tile_k = 8;
     out.k_slices = int32_t(sp.nsplit);
-    out.lds_bytes = int64_t(3) * 4 * (rows0 <= 32 ? 1 : 2) * 16 * 64 * 4;
-    out.workspace_bytes = sp.nsplit > 1 ? sp.nsplit * rows0 * d.n * 4 : 0;
-    out.n_launches = 0;
-    for (int64_t r0 = 0; r0 < d.m; r0 += 64) {
-      const int64_t rows = std::min<int64_t>(64, d.m - r0);
-      bg_launch_plan_entry& k = out.launch[out.n_launches++];
-      std::snprintf(k.family, sizeof k.family, "%s", "gemm_skinny_kernel");
-      k.n_targs = 3;
-      k.targs[0] = BG_F32;
-      k.targs[1] = rows <= 32 ? 1 : 2;
-      k.targs[2] = d.trans_b ? 1 : 0;
-      k.grid[0] = sp.ntiles * sp.nsplit; k.grid[1] = 1; k.grid[2] = 1;
-      k.block[0] = 1024; k.block[1] = 1; k.block[2] = 1;
-      if (sp.nsplit > 1) {
-        bg_launch_plan_entry& f = out.launch[out.n_launches++];
-        std::snprintf(f.family, sizeof f.family, "%s", "gemm_skinny_finish_kernel");
-        f.n_targs = 0;
-        f.grid[0] = (rows * d.n + 255) / 256; f.grid[1] = 1; f.grid[2] = 1;
-        f.block[0] = 256; f.block[1] = 1; f.block[2] = 1;
-      }
+    out.lds_bytes = int64_t(3) * 4 * mt * 16 * 64 * 4;
+    out.workspace_bytes = sp.nsplit > 1 ? sp.nsplit * d.m * d.n * 4 : 0;
+    std::snprintf(e.family, sizeof e.family, "%s", "gemm_skinny_kernel");
+    e.n_targs = 3;
+    e.targs[0] = BG_F32;
+    e.targs[1] = mt;
+    e.targs[2] = d.trans_b ? 1 : 0;
+    e.grid[0] = sp.ntiles * sp.nsplit; e.grid[1] = sp.rblocks; e.grid[2] = 1;
+    e.block[0] = 1024; e.block[1] = 1; e.block[2] = 1;
+    if (sp.nsplit > 1) {
+      out.n_launches = 2;
+      bg_launch_plan_entry& f = out.launch[1];
+      std::snprintf(f.family, sizeof f.family, "%s", "gemm_skinny_finish_kernel");
+      f.n_targs = 0;
+      f.grid[0] = (d.m * d.n + 255) / 256; f.grid[1] = 1; f.grid[2] = 1;
+      f.block[0] = 256; f.block[1] = 1; f.block[2] = 1;
     }
     return;
   }

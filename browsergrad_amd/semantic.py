@@ -397,16 +397,16 @@ def prepare_semantic_gemm(m: int, n: int, k: int, *, max_transient_working_set_b
     wide = main["family"] == "gemm32_wide_k_kernel"
     skinny = main["family"] == "gemm_skinny_kernel"
     slices = plan["kSlices"]
-    # The skinny kernel runs each column tile once per K slice, one launch
-    # per 64-row block.
+    # The skinny kernel runs each column tile once per K slice (grid x) and
+    # row block (grid y).
     per_launch = tiles_n * slices if skinny else tiles_m * tiles_n
-    if main["grid"][0] != per_launch or not (tiles_m * bm >= m > (tiles_m - 1) * bm
-                                             and tiles_n * bn >= n > (tiles_n - 1) * bn):
+    if main["grid"][0] != per_launch or (skinny and main["grid"][1] != tiles_m) or not (
+            tiles_m * bm >= m > (tiles_m - 1) * bm and tiles_n * bn >= n > (tiles_n - 1) * bn):
         _fail(code, "$.tile", f"{main['grid'][0]} workgroups do not cover {m} x {n} once with {bm} x {bn} tiles")
     # Workgroup -> tile: the wide-K kernel walks tiles row-major; the skinny
-    # one covers row block r in launch r, workgroup p taking column tile
-    # p // kSlices and K slice p % kSlices; the others use the XCD-aware
-    # order restated by gemm_tile_order.
+    # one takes row block y and, for workgroup x, column tile x // kSlices
+    # and K slice x % kSlices; the others use the XCD-aware order restated
+    # by gemm_tile_order.
     if wide or skinny:
         order = lambda p: (p // tiles_n, p % tiles_n)  # noqa: E731
     else:
@@ -416,8 +416,8 @@ def prepare_semantic_gemm(m: int, n: int, k: int, *, max_transient_working_set_b
         _fail(code, "$.schedule.tileOrder", "workgroup -> tile order is not a bijection onto the tile grid")
     if wide and (slices != main["block"][0] // 64 or len(plan["launches"]) != 1 or plan["workspaceBytes"] != 0):
         _fail(code, "$.tile.kSlices", f"{slices} in-workgroup K slices need one wavefront each and one launch")
-    if skinny and (bm > 64 or len(plan["launches"]) != tiles_m * (2 if slices > 1 else 1)
-                   or plan["workspaceBytes"] != (4 * slices * min(m, 64) * n if slices > 1 else 0)):
+    if skinny and (bm > 64 or len(plan["launches"]) != (2 if slices > 1 else 1)
+                   or plan["workspaceBytes"] != (4 * slices * m * n if slices > 1 else 0)):
         _fail(code, "$.tile.kSlices", f"{slices} K slices need one f32 partial each and a summing launch")
     if not wide and not skinny and (slices != 1 or len(plan["launches"]) != 1):
         _fail(code, "$.tile.kSlices", "the tiled kernel runs the whole K range in one launch")
@@ -436,7 +436,7 @@ def prepare_semantic_gemm(m: int, n: int, k: int, *, max_transient_working_set_b
     }, ["tiles-cover-output-once", "k-slices-one-per-wavefront"])
     schedule = _artifact("schedule", {
         "launches": plan["launches"], "ldsBytes": plan["ldsBytes"], "workspaceBytes": plan["workspaceBytes"],
-        "tileOrder": "row-major" if wide else "row block per launch; column tile p // kSlices, K slice p % kSlices"
+        "tileOrder": "row-major" if wide else "row block y; column tile x // kSlices, K slice x % kSlices"
                      if skinny
                      else "xcd-round-robin-consecutive, groups of 4 tile rows",
     }, ["tile-order-bijection", "within-workgroup-limits"])

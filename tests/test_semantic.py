@@ -58,7 +58,7 @@ def test_certificate_commits_to_the_bytes():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k,hi", [(3, 5, 7, 9), (256, 384, 512, 15), (1000, 999, 1024, 3), (40, 3000, 4096, 2),
-                                      (100, 3000, 1024, 3)])
+                                      (100, 3000, 1024, 3), (250, 2100, 2048, 2)])
 def test_exact_gemm_is_bit_exact(bridge, m, n, k, hi):
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(0, hi + 1, (m, k)).astype(F32)
@@ -170,13 +170,12 @@ def test_prepare_gemm_fixes_schedule_before_any_launch():
                                   {"family": "gemm_skinny_finish_kernel", "templateArgs": [],
                                    "grid": [469, 1, 1], "block": [256, 1, 1]}]
     assert k.tile["body"]["kSlices"] == 10 and k.plan["workspaceBytes"] == 4 * 10 * 40 * 3000
-    assert k.schedule["body"]["tileOrder"] == "row block per launch; column tile p // kSlices, K slice p % kSlices"
-    # 100 rows: two 64-row blocks, each a kernel and its partial sum.
-    k2 = prepare_semantic_gemm(100, 3000, 4096)
-    assert [(e["family"], e["templateArgs"], e["grid"][0]) for e in k2.plan["launches"]] == [
-        ("gemm_skinny_kernel", [0, 2, 0], 240), ("gemm_skinny_finish_kernel", [], 750),
-        ("gemm_skinny_kernel", [0, 2, 0], 240), ("gemm_skinny_finish_kernel", [], 422)]
-    assert k2.tile["body"]["tilesM"] == 2 and k2.plan["workspaceBytes"] == 4 * 10 * 64 * 3000
+    assert k.schedule["body"]["tileOrder"] == "row block y; column tile x // kSlices, K slice x % kSlices"
+    # 200 rows: four 64-row blocks along grid y, K in 2 slices.
+    k2 = prepare_semantic_gemm(200, 3000, 4096)
+    assert [(e["family"], e["templateArgs"], e["grid"]) for e in k2.plan["launches"]] == [
+        ("gemm_skinny_kernel", [0, 2, 0], [48, 4, 1]), ("gemm_skinny_finish_kernel", [], [2344, 1, 1])]
+    assert k2.tile["body"]["tilesM"] == 4 and k2.plan["workspaceBytes"] == 4 * 2 * 200 * 3000
 
 
 @pytest.mark.parametrize("kw,path", [

@@ -1114,7 +1114,7 @@ static bool gelu_in_epilogue(const bg_matmul_desc& d, const char* a, const char*
 
 // a / b point at the operands' storage (d.offset_a / d.offset_b are applied
 // here); bias is f32 [N] or NULL.
-// Skinny GEMMs: at most 256 rows for f32 (blocks of 64) or 64 for 16-bit,
+// Skinny GEMMs: at most 512 rows for f32 (blocks of 64) or 64 for 16-bit,
 // a K of 512+, fewer 128-column tiles than CUs and one batch (the tiled
 // kernels would leave most of the chip idle).
 // K slices of at least 256 (and multiples of 64: four wavefronts interleave
@@ -1128,10 +1128,11 @@ struct SkinnyPlan {
 static SkinnyPlan skinny_plan(const bg_matmul_desc& d, int dt, size_t room) {
   SkinnyPlan sp;
   sp.ntiles = (d.n + 127) / 128;
-  // Row limit: 256 for f32 (64-row blocks; two of them beat the tiled f32
-  // kernel 5x at 128 x 4096 x 4096), 64 for 16-bit (two blocks measured
-  // slower than the tiled kernel: 50 against 40 us).
-  if (d.batch != 1 || d.m > (dt == BG_F32 ? 256 : 64) || d.k < 512 || sp.ntiles >= 256 ||
+  // Row limit: 512 for f32 (64-row blocks; the tiled f32 kernel has at
+  // most 128 workgroups there: 256 x 4096 x 4096 150 against 479 us), 64
+  // for 16-bit (two blocks measured slower than the tiled kernel: 50
+  // against 40 us at 128 x 4096 x 4096).
+  if (d.batch != 1 || d.m > (dt == BG_F32 ? 512 : 64) || d.k < 512 || sp.ntiles >= 256 ||
       std::getenv("BG_GEMM_SKINNY") != nullptr)
     return sp;
   sp.on = true;

@@ -899,11 +899,11 @@ def test_gemm_128x192_tiles_ragged(bridge, rng, monkeypatch, m, k, n, act, resid
     (33, 768, 2304, 2, False, True), (64, 3072, 768, 0, True, True), (64, 512, 50, 1, False, True),
     (5, 4104, 130, 2, True, False), (48, 520, 4000, 0, False, True), (100, 1024, 2304, 1, True, True),
     (128, 4096, 4096, 0, False, False), (65, 768, 3000, 2, True, True), (256, 1024, 4000, 1, True, True),
-    (200, 2048, 2500, 0, False, False)])
+    (200, 2048, 2500, 0, False, False), (450, 2200, 1024, 2, True, True)])
 @pytest.mark.parametrize("dtype,out_dtype", [("float16", "float32"), ("float16", "float16"),
                                              ("bfloat16", "bfloat16"), ("float32", "float32")])
 def test_gemm_skinny_split_k(bridge, rng, monkeypatch, m, k, n, act, residual, trans_b, dtype, out_dtype):
-    """At most 64 rows (f32: 256, in 64-row blocks) with K >= 512 and fewer
+    """At most 64 rows (f32: 512, in 64-row blocks) with K >= 512 and fewer
     128-column tiles than CUs (f32 also with B stored [K][N]): K split over
     workgroups (f32 partials summed in split order by a second
     kernel, or one split), M of one or two 32-row MFMA blocks, ragged N,

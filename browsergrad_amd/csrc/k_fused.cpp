@@ -650,6 +650,36 @@ void launch_fused(bg_ctx* ctx, const bg_fused_desc& d, Record& out) {
     }
   }
 
+  // A large operand read transposed (innermost stride neither 0 nor 1)
+  // would gather each lane's vector from distant rows; it is first copied
+  // to row-major order (the tiled-transpose copy) and read contiguously.
+  {
+    int64_t need = 0;
+    std::vector<int> tr;
+    for (int i = 0; i < n_in; ++i) {
+      if (plan.kind[i] != IN_STRIDED || cols == 1) continue;
+      const int64_t is = A.stride[i][lead.size()];
+      if (is == 0 || is == 1 || total < (int64_t(1) << 20)) continue;
+      tr.push_back(i);
+      need += (total * dtype_size(plan.dtype[i]) + 255) / 256 * 256;
+    }
+    if (!tr.empty()) {
+      char* buf = static_cast<char*>(scratch(ctx, size_t(need), 2));
+      for (int i : tr) {
+        std::vector<int64_t> shp(lead.begin(), lead.end()), st;
+        shp.push_back(cols);
+        for (size_t k = 0; k < lead.size(); ++k) st.push_back(A.stride[i][k]);
+        st.push_back(A.stride[i][lead.size()]);
+        const int64_t es = dtype_size(plan.dtype[i]);
+        launch_copy_strided(ctx, A.in[i], es, buf, shp, st);
+        A.in[i] = buf;
+        plan.kind[i] = IN_CONTIG;
+        for (size_t k = 0; k <= lead.size(); ++k) A.stride[i][k] = 0;
+        buf += (total * es + 255) / 256 * 256;
+      }
+    }
+  }
+
   // Validate the op list (SSA refs, arities, immediates).
   if (d.n_imms > BG_FUSED_MAX_IMMS) fail(BG_E_INVALID, "fused_elementwise: too many immediates");
   for (int i = 0; i < d.n_imms; ++i) A.imm[i] = float(d.imms[i]);

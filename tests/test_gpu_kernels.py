@@ -287,6 +287,25 @@ def test_fused_broadcast_index_math(bridge, rng, shape, bshape):
     assert np.array_equal(r, (x + b).max(axis=-1))
 
 
+# An operand read transposed (innermost stride neither 0 nor 1) of 2^20+
+# elements is first copied to row-major order; smaller ones are gathered in
+# place.  Both must give NumPy's bits, with and without a row reduction.
+@pytest.mark.parametrize("rows,cols,batch", [(1100, 1000, 0), (3, 7, 0), (700, 600, 3)])
+def test_fused_transposed_operand(bridge, rng, rows, cols, batch):
+    x = rng.standard_normal(((batch,) if batch else ()) + (rows, cols)).astype(np.float32)
+    t = rng.standard_normal((cols, rows)).astype(np.float32)  # read as t.T
+    hx, ht = up(bridge, x), up(bridge, t)
+    shape = x.shape
+    xst = [int(np.prod(shape[i + 1:])) for i in range(len(shape))]
+    tst = ([0] if batch else []) + [1, rows]
+    ops = [("MUL", -1, -2, 0), ("ADD", 0, -1, 0)]
+    ref = x * t.T + x
+    y = bridge.to_numpy(bridge.fused_ex([hx, ht], ops, shape, "float32", in_strides=[xst, tst]))
+    assert np.array_equal(y, ref)
+    r = bridge.to_numpy(bridge.fused_ex([hx, ht], ops, shape, "float32", in_strides=[xst, tst], reduce=2))
+    assert np.array_equal(r, ref.max(axis=-1))
+
+
 def test_fused_reference_opcodes_bit_exact(bridge, rng):
     # ADD/MUL/DIV/NEG are IEEE single ops: bit-exact against NumPy.
     a = rng.standard_normal((257, 31)).astype(np.float32)
